@@ -1,0 +1,182 @@
+/*
+ * lowbit_hip: fused dequantize + GEMM for low-bit weights on AMD Instinct MI355X (gfx950).
+ *
+ * C ABI of liblowbit_hip.so. Every GEMM computes  Y[M,N] = X[M,Kp] . W[N,Kp]^T
+ * (nn.Linear convention). Kp is the padded reduction length: a multiple of 128
+ * for the int4 formats, of 32 for MXFP4; callers pad X with zeros.
+ *
+ * Packed weight layouts (row n of W is Kp/2 contiguous bytes):
+ *   int4, group 128 : group g = bytes [64g, 64g+64); byte j holds element 128g+j
+ *                     (low nibble) and 128g+64+j (high nibble). value = (q - z) * s,
+ *                     q in 0..15, s = scales[n,g] (fp32), z = zeros[n,g] or 8
+ *                     when zeros == NULL.
+ *   MXFP4, block 32 : block b = bytes [16b, 16b+16); byte j holds element 32b+j
+ *                     (low nibble) and 32b+16+j (high nibble); OCP E2M1 codes,
+ *                     value = e2m1(q) * 2^(e8m0[n,b] - 127) (e8m0 0 -> 2^-127,
+ *                     255 -> NaN).
+ *   Same layouts as the reference, src/lowbit/csrc/lowbit.h:9-19.
+ *
+ * Three families of entry points:
+ *   lb_*    host pointers, synchronous: the exact signatures of the reference ABI
+ *           (src/lowbit/csrc/lowbit.h:95-123). Inputs are copied to the device,
+ *           the kernel runs, y is copied back before return.
+ *   lbd_*   device pointers, asynchronous on `stream` (a hipStream_t, NULL = the
+ *           null stream). For callers that keep weights and activations resident
+ *           in HBM. Nothing is copied; the call returns after the launch.
+ *   lb_dev_*, lb_stream_*, lb_event_*: minimal device-memory, stream and event
+ *           plumbing so that a caller without its own HIP runtime bindings (the
+ *           ctypes layer) can use the lbd_* family.
+ *
+ * Return codes: >= 0 success (the id of the path that ran, LB_ISA_*), < 0 error.
+ * These follow the reference (src/lowbit/csrc/dispatch.c:160,205-208,279):
+ *   -1 bad shape (M, N or Kp <= 0, or Kp not a multiple of the block),
+ *   -2 tile parameters that name no compiled micro-tile (lb_params.mr/nr),
+ *   -3 allocation failure, -4 feature unavailable (no device / AMX entry points),
+ *   plus -5 HIP runtime error and -6 bad argument (NULL pointer, bad isa).
+ * lb_last_error() gives a message for the last failure on the calling thread.
+ *
+ * Threading: every host thread gets its own stream and staging buffers, so the
+ * lb_* entry points may be called concurrently from several threads.
+ */
+#ifndef LOWBIT_HIP_H
+#define LOWBIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LB_GROUP 128  /* int4 group size (elements) */
+#define LB_MXBLOCK 32 /* MXFP4 block size (elements) */
+
+/* Path ids, returned by the GEMMs like the reference returns its ISA id
+ * (src/lowbit/csrc/dispatch.c:202). The reference's CPU ids 0..2 (scalar, avx2,
+ * avx512) are accepted as requests and mean "auto": there are no CPU tiers. */
+#define LB_ISA_GFX950 16      /* VALU decode kernels (small M) */
+#define LB_ISA_GFX950_MFMA 17 /* matrix-core kernels (M >= 16 or large M*K) */
+
+#define LB_ERR_SHAPE -1
+#define LB_ERR_TILE -2
+#define LB_ERR_ALLOC -3
+#define LB_ERR_UNAVAILABLE -4
+#define LB_ERR_HIP -5
+#define LB_ERR_ARG -6
+
+/* Dispatch parameters; zero or negative fields mean "default".
+ * Same struct as the reference (src/lowbit/csrc/lowbit.h:37-45). `isa` requests a
+ * path (-1 auto, LB_ISA_GFX950, LB_ISA_GFX950_MFMA; a VALU request that the shape
+ * cannot use is clamped to MFMA, as the reference clamps its ISA). mr/nr must name
+ * one of the reference's micro-tiles (1,2,4,8 x 1,2,4 minus 8x4) or be 0, else -2;
+ * nb/kb/order/nthreads are accepted and have no GPU meaning. */
+typedef struct {
+    int isa;
+    int mr;
+    int nr;
+    int nb;
+    int kb;
+    int order;
+    int nthreads;
+} lb_params;
+
+/* ---- library / device information (src/lowbit/csrc/lowbit.h:95-103) ---- */
+int lb_version(void);
+/* best path the hardware supports: LB_ISA_GFX950_MFMA on a gfx950 device, -4 without one
+ * (replaces lowbit.h:96 lb_cpu_isa) */
+int lb_cpu_isa(void);
+/* same after the LOWBIT_ISA environment cap ("gfx950" limits GEMMs to the VALU
+ * kernels; replaces lowbit.h:97 lb_active_isa) */
+int lb_active_isa(void);
+int lb_has_vnni(void);    /* 0: no CPU VNNI path in this library (lowbit.h:98) */
+int lb_has_openmp(void);  /* 0 (lowbit.h:99) */
+int lb_max_threads(void); /* 1: host threads are not used for compute (lowbit.h:100) */
+/* path a GEMM kind (0 w4a16, 1 mxfp4, 2 w4a8) runs with for a request; mirrors
+ * lowbit.h:102 lb_effective_isa. The shape-dependent regime is reported by the
+ * GEMM's return value. */
+int lb_effective_isa(int kind, int requested);
+/* device name, compute units and LDS bytes per workgroup of the current device */
+int lb_device_info(char *name, int name_len, int *compute_units, int *lds_bytes);
+const char *lb_last_error(void);
+/* return code of the last lb_* / lbd_* call on this thread (lets callers of the
+ * void lb_quant_act_int8 see a failure) */
+int lb_last_status(void);
+
+/* ---- GEMMs, host pointers (src/lowbit/csrc/lowbit.h:105-123) ---- */
+int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw,
+                  const float *scales, const uint8_t *zeros, int N, float *y,
+                  const lb_params *p);
+int lb_gemm_mxfp4(const float *x, int M, int Kp, const uint8_t *qw,
+                  const uint8_t *e8m0, int N, float *y, const lb_params *p);
+/* x is fp32; the per-token int8 quantization runs on the device inside the call */
+int lb_gemm_w4a8(const float *x, int M, int Kp, const uint8_t *qw,
+                 const float *scales, const uint8_t *zeros, int N, float *y,
+                 const lb_params *p);
+/* activations already quantized: xq [M,Kp], xs [M], asum [M,Kp/128] */
+int lb_gemm_w4a8_q(const int8_t *xq, const float *xs, const int32_t *asum,
+                   int M, int Kp, const uint8_t *qw, const float *scales,
+                   const uint8_t *zeros, int N, float *y, const lb_params *p);
+/* per-token symmetric int8 quantization, bit-identical to the reference
+ * (src/lowbit/csrc/dispatch.c:231-257); runs on the device */
+void lb_quant_act_int8(const float *x, int M, int Kp, int8_t *xq, float *xs,
+                       int32_t *asum);
+/* exact int32 group accumulators out[m,n,g] = sum_{k in g} (q - z) * xq (test hook,
+ * src/lowbit/csrc/dispatch.c:288-305). isa selects the integer path that produces
+ * them: -1 or LB_ISA_GFX950 the VALU dot4 path, LB_ISA_GFX950_MFMA the int8 MFMA path. */
+int lb_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp,
+                      const uint8_t *qw, const uint8_t *zeros, int N,
+                      int32_t *out, int isa);
+
+/* ---- GEMMs, device pointers, asynchronous on `stream` (no reference counterpart:
+ *      the reference's buffers are host memory; these are what a device-resident
+ *      caller binds instead of lowbit.h:105-123) ---- */
+int lbd_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw,
+                   const float *scales, const uint8_t *zeros, int N, float *y,
+                   const lb_params *p, void *stream);
+int lbd_gemm_mxfp4(const float *x, int M, int Kp, const uint8_t *qw,
+                   const uint8_t *e8m0, int N, float *y, const lb_params *p,
+                   void *stream);
+/* workspace: device scratch of at least lbd_w4a8_workspace_bytes(M, Kp) bytes for the
+ * quantized activations, or NULL to use a buffer the library keeps per thread
+ * and device (grown on demand; calls on one thread must then not overlap on
+ * different streams). */
+int lbd_gemm_w4a8(const float *x, int M, int Kp, const uint8_t *qw,
+                  const float *scales, const uint8_t *zeros, int N, float *y,
+                  const lb_params *p, void *workspace, size_t workspace_bytes,
+                  void *stream);
+size_t lbd_w4a8_workspace_bytes(int M, int Kp);
+int lbd_gemm_w4a8_q(const int8_t *xq, const float *xs, const int32_t *asum,
+                    int M, int Kp, const uint8_t *qw, const float *scales,
+                    const uint8_t *zeros, int N, float *y, const lb_params *p,
+                    void *stream);
+int lbd_quant_act_int8(const float *x, int M, int Kp, int8_t *xq, float *xs,
+                       int32_t *asum, void *stream);
+int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp,
+                       const uint8_t *qw, const uint8_t *zeros, int N,
+                       int32_t *out, int isa, void *stream);
+
+/* ---- device plumbing for the ctypes layer and benchmarks ---- */
+int lb_dev_malloc(void **ptr, size_t bytes);
+int lb_dev_free(void *ptr);
+int lb_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int lb_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int lb_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int lb_memset_d(void *dst, int value, size_t bytes);
+int lb_dev_synchronize(void);
+int lb_stream_create(void **stream);
+int lb_stream_destroy(void *stream);
+int lb_stream_synchronize(void *stream);
+int lb_event_create(void **event);
+int lb_event_destroy(void *event);
+int lb_event_record(void *event, void *stream);
+int lb_event_synchronize(void *event);
+int lb_event_elapsed_ms(void *start, void *stop, float *ms);
+/* plain streaming copy kernel of `bytes` (multiple of 16) on `stream`: the known-size
+ * reference for scaling HBM traffic counters */
+int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOWBIT_HIP_H */

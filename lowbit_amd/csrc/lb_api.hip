@@ -1,0 +1,683 @@
+// C ABI of liblowbit_hip.so (declared in include/lowbit_hip.h).
+//
+// Replaces the reference's CPU driver (src/lowbit/csrc/dispatch.c): shape checks
+// and return codes follow it (dispatch.c:160,205-208,279); the ISA dispatch and
+// OpenMP tiling become a choice between two gfx950 regimes (VALU decode kernels
+// for small M, matrix-core kernels otherwise), and the host-pointer entry points
+// stage their operands through device memory owned by the calling thread.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/lowbit_hip.h"
+#include "lb_internal.h"
+
+namespace {
+
+thread_local std::string t_error;
+thread_local int t_status = 0;
+
+int fail(int rc, const char *what) {
+  t_error = what;
+  t_status = rc;
+  return rc;
+}
+
+int fail_hip(hipError_t e, const char *what) {
+  t_error = std::string(what) + ": " + hipGetErrorString(e);
+  t_status = LB_ERR_HIP;
+  return LB_ERR_HIP;
+}
+
+int ok(int rc) {
+  t_status = rc;
+  return rc;
+}
+
+#define LB_HIP(call, what)                  \
+  do {                                      \
+    hipError_t e_ = (call);                 \
+    if (e_ != hipSuccess) return fail_hip(e_, what); \
+  } while (0)
+
+inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// ---------------------------------------------------------------- device info
+
+struct DevInfo {
+  int cus = 0;
+  int lds = 0;
+  bool gfx950 = false;
+  char name[64] = {0};
+};
+
+std::mutex g_info_mu;
+std::unordered_map<int, DevInfo> g_info;
+
+int current_device(int *dev) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(LB_ERR_UNAVAILABLE, "no HIP device");
+  LB_HIP(hipGetDevice(dev), "hipGetDevice");
+  return 0;
+}
+
+int device_info(DevInfo *out) {
+  int dev = 0;
+  int rc = current_device(&dev);
+  if (rc < 0) return rc;
+  std::lock_guard<std::mutex> lk(g_info_mu);
+  auto it = g_info.find(dev);
+  if (it == g_info.end()) {
+    hipDeviceProp_t prop;
+    LB_HIP(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    DevInfo d;
+    d.cus = prop.multiProcessorCount;
+    d.lds = (int)prop.sharedMemPerBlock;
+    std::snprintf(d.name, sizeof d.name, "%s", prop.gcnArchName);
+    d.gfx950 = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    it = g_info.emplace(dev, d).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+// ---------------------------------------------------------------- per-thread staging
+
+// Device memory and a stream owned by one host thread on one device. Never freed:
+// releasing HIP objects from thread-exit destructors can run after the runtime is
+// gone, and the buffers are reused by every later call of the thread.
+struct Ctx {
+  hipStream_t stream = nullptr;
+  char *buf = nullptr;
+  size_t cap = 0;
+  char *ws = nullptr;  // lbd_gemm_w4a8 workspace when the caller passes none
+  size_t ws_cap = 0;
+};
+
+thread_local std::unordered_map<int, Ctx *> t_ctx;
+
+int get_ctx(Ctx **out) {
+  int dev = 0;
+  int rc = current_device(&dev);
+  if (rc < 0) return rc;
+  auto it = t_ctx.find(dev);
+  if (it == t_ctx.end()) {
+    Ctx *c = new Ctx();
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete c;
+      return fail_hip(e, "hipStreamCreate");
+    }
+    it = t_ctx.emplace(dev, c).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+int grow(char **buf, size_t *cap, size_t need, hipStream_t s) {
+  if (need <= *cap) return 0;
+  if (*buf) {
+    LB_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+    LB_HIP(hipFree(*buf), "hipFree");
+    *buf = nullptr;
+    *cap = 0;
+  }
+  size_t sz = need < (size_t(1) << 20) ? (size_t(1) << 20) : need + need / 4;
+  if (hipMalloc(reinterpret_cast<void **>(buf), sz) != hipSuccess) {
+    *buf = nullptr;
+    return fail(LB_ERR_ALLOC, "hipMalloc of staging memory failed");
+  }
+  *cap = sz;
+  return 0;
+}
+
+// Carves 256-byte aligned pieces out of the thread's staging buffer.
+struct Arena {
+  size_t off = 0;
+  size_t take(size_t n) {
+    size_t o = off;
+    off += align256(n);
+    return o;
+  }
+};
+
+// ---------------------------------------------------------------- validation
+
+// Reference micro-tiles (src/lowbit/csrc/tiles.inc, kernels.py TILES): a Params that
+// names any other (mr, nr) is rejected with -2, as the reference does.
+bool tile_compiled(int mr, int nr) {
+  static const int tiles[][2] = {{1, 1}, {1, 2}, {1, 4}, {2, 1}, {2, 2}, {2, 4},
+                                 {4, 1}, {4, 2}, {4, 4}, {8, 1}, {8, 2}};
+  for (auto &t : tiles)
+    if (t[0] == mr && t[1] == nr) return true;
+  return false;
+}
+
+int check_params(const lb_params *p, int M) {
+  if (!p) return 0;
+  int mr = p->mr > 0 ? p->mr : (M >= 4 ? 4 : 1);
+  int nr = p->nr > 0 ? p->nr : 2;
+  if (mr > 8) mr = 8;
+  if (nr > 4) nr = 4;
+  if (!tile_compiled(mr, nr)) return fail(LB_ERR_TILE, "lb_params names a micro-tile that does not exist");
+  return 0;
+}
+
+int check_shape(int M, int Kp, int N, int block) {
+  if (M <= 0 || N <= 0 || Kp <= 0 || Kp % block) return fail(LB_ERR_SHAPE, "bad shape (M, N, Kp <= 0 or Kp % block)");
+  return 0;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// LOWBIT_ISA cap (read once): "gfx950" keeps GEMMs on the VALU kernels where the
+// shape allows; anything else (or unset) leaves the choice automatic.
+int env_cap() {
+  static int cap = -2;
+  if (cap == -2) {
+    const char *e = std::getenv("LOWBIT_ISA");
+    cap = (e && std::strcmp(e, "gfx950") == 0) ? LB_ISA_GFX950 : LB_ISA_GFX950_MFMA;
+  }
+  return cap;
+}
+
+// The regime a GEMM runs in. A VALU request the shape cannot use is clamped to
+// the matrix-core kernels, the way the reference clamps an ISA request.
+int choose_path(int fmt, int M, int Kp, const lb_params *p) {
+  const bool valu_ok = lbk::gemv_eligible(fmt, M, Kp);
+  const int req = p ? p->isa : -1;
+  if (req == LB_ISA_GFX950_MFMA) return LB_ISA_GFX950_MFMA;
+  return valu_ok ? LB_ISA_GFX950 : LB_ISA_GFX950_MFMA;
+}
+
+// ---------------------------------------------------------------- device-pointer cores
+
+int run_w4a16(const lbk::GemmArgs &a, const lb_params *p, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  const int path = choose_path(lbk::F_W4A16, a.M, a.Kp, p);
+  hipError_t e = path == LB_ISA_GFX950 ? lbk::launch_gemv(lbk::F_W4A16, a, cus, s)
+                                       : lbk::launch_f32_mfma(lbk::F_W4A16, a, s);
+  if (e != hipSuccess) return fail_hip(e, "W4A16 kernel launch");
+  return ok(path);
+}
+
+int run_mxfp4(const lbk::GemmArgs &a, const lb_params *p, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  const int path = choose_path(lbk::F_MXFP4, a.M, a.Kp, p);
+  hipError_t e = path == LB_ISA_GFX950 ? lbk::launch_gemv(lbk::F_MXFP4, a, cus, s)
+                                       : lbk::launch_f32_mfma(lbk::F_MXFP4, a, s);
+  if (e != hipSuccess) return fail_hip(e, "MXFP4 kernel launch");
+  return ok(path);
+}
+
+size_t w4a8_ws_bytes(int M, int Kp) {
+  return align256((size_t)M * Kp) + align256((size_t)M * 4) + align256((size_t)M * (Kp / LB_GROUP) * 4);
+}
+
+// fp32 activations in; quantized inside (fused into the GEMV, or a quantizer
+// kernel into `ws` before the MFMA kernel).
+int run_w4a8(const lbk::GemmArgs &a, const lb_params *p, char *ws, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  const int path = choose_path(lbk::F_W4A8, a.M, a.Kp, p);
+  if (path == LB_ISA_GFX950) {
+    hipError_t e = lbk::launch_gemv(lbk::F_W4A8, a, cus, s);
+    if (e != hipSuccess) return fail_hip(e, "W4A8 GEMV launch");
+    return ok(path);
+  }
+  lbk::GemmArgs q = a;
+  int8_t *xq = reinterpret_cast<int8_t *>(ws);
+  float *xs = reinterpret_cast<float *>(ws + align256((size_t)a.M * a.Kp));
+  int32_t *asum = reinterpret_cast<int32_t *>(ws + align256((size_t)a.M * a.Kp) + align256((size_t)a.M * 4));
+  hipError_t e = lbk::launch_quant(a.x, a.M, a.Kp, xq, xs, asum, s);
+  if (e != hipSuccess) return fail_hip(e, "quantizer launch");
+  q.xq = xq;
+  q.xs = xs;
+  q.asum = asum;
+  e = lbk::launch_w4a8_mfma(q, nullptr, s);
+  if (e != hipSuccess) return fail_hip(e, "W4A8 MFMA launch");
+  return ok(path);
+}
+
+int run_w4a8_q(const lbk::GemmArgs &a, const lb_params *p, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  const int path = choose_path(lbk::F_W4A8Q, a.M, a.Kp, p);
+  hipError_t e = path == LB_ISA_GFX950 ? lbk::launch_gemv(lbk::F_W4A8Q, a, cus, s)
+                                       : lbk::launch_w4a8_mfma(a, nullptr, s);
+  if (e != hipSuccess) return fail_hip(e, "W4A8 kernel launch");
+  return ok(path);
+}
+
+int run_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, const uint8_t *qw,
+                  const uint8_t *zeros, int N, int32_t *out, int isa, hipStream_t s) {
+  hipError_t e;
+  int path;
+  if (isa == LB_ISA_GFX950_MFMA) {
+    lbk::GemmArgs a;
+    a.xq = xq;
+    a.asum = asum;
+    a.qw = qw;
+    a.zeros = zeros;
+    a.M = M;
+    a.Kp = Kp;
+    a.N = N;
+    e = lbk::launch_w4a8_mfma(a, out, s);
+    path = LB_ISA_GFX950_MFMA;
+  } else {
+    e = lbk::launch_groupacc_dot4(xq, asum, M, Kp, qw, zeros, N, out, s);
+    path = LB_ISA_GFX950;
+  }
+  if (e != hipSuccess) return fail_hip(e, "group accumulator launch");
+  return ok(path);
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+int lb_version(void) { return 1; }
+
+int lb_cpu_isa(void) {
+  DevInfo d;
+  if (device_info(&d) < 0) return LB_ERR_UNAVAILABLE;
+  return d.gfx950 ? LB_ISA_GFX950_MFMA : LB_ERR_UNAVAILABLE;
+}
+
+int lb_active_isa(void) {
+  const int top = lb_cpu_isa();
+  if (top < 0) return top;
+  return env_cap() < top ? env_cap() : top;
+}
+
+int lb_has_vnni(void) { return 0; }
+int lb_has_openmp(void) { return 0; }
+int lb_max_threads(void) { return 1; }
+
+int lb_effective_isa(int kind, int requested) {
+  (void)kind;
+  const int top = lb_active_isa();
+  if (top < 0) return top;
+  if (requested == LB_ISA_GFX950) return LB_ISA_GFX950;
+  return top;
+}
+
+int lb_device_info(char *name, int name_len, int *compute_units, int *lds_bytes) {
+  DevInfo d;
+  int rc = device_info(&d);
+  if (rc < 0) return rc;
+  if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", d.name);
+  if (compute_units) *compute_units = d.cus;
+  if (lds_bytes) *lds_bytes = d.lds;
+  return ok(0);
+}
+
+const char *lb_last_error(void) { return t_error.c_str(); }
+int lb_last_status(void) { return t_status; }
+
+// ---------------------------------------------------------------- device-pointer GEMMs
+
+int lbd_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                   const uint8_t *zeros, int N, float *y, const lb_params *p, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  return run_w4a16(a, p, static_cast<hipStream_t>(stream));
+}
+
+int lbd_gemm_mxfp4(const float *x, int M, int Kp, const uint8_t *qw, const uint8_t *e8m0,
+                   int N, float *y, const lb_params *p, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !e8m0 || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.e8m0 = e8m0; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  return run_mxfp4(a, p, static_cast<hipStream_t>(stream));
+}
+
+size_t lbd_w4a8_workspace_bytes(int M, int Kp) {
+  if (M <= 0 || Kp <= 0) return 0;
+  return w4a8_ws_bytes(M, Kp);
+}
+
+int lbd_gemm_w4a8(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                  const uint8_t *zeros, int N, float *y, const lb_params *p, void *workspace,
+                  size_t workspace_bytes, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  char *ws = static_cast<char *>(workspace);
+  if (choose_path(lbk::F_W4A8, M, Kp, p) == LB_ISA_GFX950_MFMA) {
+    const size_t need = w4a8_ws_bytes(M, Kp);
+    if (ws) {
+      if (workspace_bytes < need) return fail(LB_ERR_ARG, "workspace too small");
+      if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return fail(LB_ERR_ARG, "workspace must be 256-byte aligned");
+    } else {
+      Ctx *c = nullptr;
+      if ((rc = get_ctx(&c)) < 0) return rc;
+      if ((rc = grow(&c->ws, &c->ws_cap, need, s)) < 0) return rc;
+      ws = c->ws;
+    }
+  }
+  return run_w4a8(a, p, ws, s);
+}
+
+int lbd_gemm_w4a8_q(const int8_t *xq, const float *xs, const int32_t *asum, int M, int Kp,
+                    const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, float *y,
+                    const lb_params *p, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!xq || !xs || !asum || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(xq) || !aligned16(qw)) return fail(LB_ERR_ARG, "xq and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.xq = xq; a.xs = xs; a.asum = asum; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  return run_w4a8_q(a, p, static_cast<hipStream_t>(stream));
+}
+
+int lbd_quant_act_int8(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum,
+                       void *stream) {
+  if (M <= 0 || Kp <= 0 || Kp % LB_GROUP) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!x || !xq || !xs || !asum) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(xq)) return fail(LB_ERR_ARG, "x and xq must be 16-byte aligned");
+  hipError_t e = lbk::launch_quant(x, M, Kp, xq, xs, asum, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "quantizer launch");
+  return ok(0);
+}
+
+int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, const uint8_t *qw,
+                       const uint8_t *zeros, int N, int32_t *out, int isa, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!xq || !asum || !qw || !out) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(xq) || !aligned16(qw)) return fail(LB_ERR_ARG, "xq and qw must be 16-byte aligned");
+  return run_group_acc(xq, asum, M, Kp, qw, zeros, N, out, isa, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------- host-pointer GEMMs
+
+int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                  const uint8_t *zeros, int N, float *y, const lb_params *p) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  Ctx *c = nullptr;
+  if ((rc = get_ctx(&c)) < 0) return rc;
+  const int G = Kp / LB_GROUP;
+  const size_t bx = (size_t)M * Kp * 4, bq = (size_t)N * Kp / 2, bs = (size_t)N * G * 4,
+               bz = zeros ? (size_t)N * G : 0, by = (size_t)M * N * 4;
+  Arena ar;
+  const size_t ox = ar.take(bx), oq = ar.take(bq), os = ar.take(bs), oz = ar.take(bz), oy = ar.take(by);
+  if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  LB_HIP(hipMemcpyAsync(b + ox, x, bx, hipMemcpyHostToDevice, s), "copy x");
+  LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
+  LB_HIP(hipMemcpyAsync(b + os, scales, bs, hipMemcpyHostToDevice, s), "copy scales");
+  if (zeros) LB_HIP(hipMemcpyAsync(b + oz, zeros, bz, hipMemcpyHostToDevice, s), "copy zeros");
+  rc = lbd_gemm_w4a16(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
+                      reinterpret_cast<float *>(b + os), zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr, N,
+                      reinterpret_cast<float *>(b + oy), p, s);
+  if (rc < 0) return rc;
+  LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
+  LB_HIP(hipStreamSynchronize(s), "synchronize");
+  return ok(rc);
+}
+
+int lb_gemm_mxfp4(const float *x, int M, int Kp, const uint8_t *qw, const uint8_t *e8m0, int N,
+                  float *y, const lb_params *p) {
+  int rc = check_shape(M, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !e8m0 || !y) return fail(LB_ERR_ARG, "null pointer");
+  Ctx *c = nullptr;
+  if ((rc = get_ctx(&c)) < 0) return rc;
+  const size_t bx = (size_t)M * Kp * 4, bq = (size_t)N * Kp / 2, be = (size_t)N * (Kp / LB_MXBLOCK),
+               by = (size_t)M * N * 4;
+  Arena ar;
+  const size_t ox = ar.take(bx), oq = ar.take(bq), oe = ar.take(be), oy = ar.take(by);
+  if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  LB_HIP(hipMemcpyAsync(b + ox, x, bx, hipMemcpyHostToDevice, s), "copy x");
+  LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
+  LB_HIP(hipMemcpyAsync(b + oe, e8m0, be, hipMemcpyHostToDevice, s), "copy e8m0");
+  rc = lbd_gemm_mxfp4(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
+                      reinterpret_cast<uint8_t *>(b + oe), N, reinterpret_cast<float *>(b + oy), p, s);
+  if (rc < 0) return rc;
+  LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
+  LB_HIP(hipStreamSynchronize(s), "synchronize");
+  return ok(rc);
+}
+
+int lb_gemm_w4a8(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                 const uint8_t *zeros, int N, float *y, const lb_params *p) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  Ctx *c = nullptr;
+  if ((rc = get_ctx(&c)) < 0) return rc;
+  const int G = Kp / LB_GROUP;
+  const size_t bx = (size_t)M * Kp * 4, bq = (size_t)N * Kp / 2, bs = (size_t)N * G * 4,
+               bz = zeros ? (size_t)N * G : 0, by = (size_t)M * N * 4, bw = w4a8_ws_bytes(M, Kp);
+  Arena ar;
+  const size_t ox = ar.take(bx), oq = ar.take(bq), os = ar.take(bs), oz = ar.take(bz), oy = ar.take(by),
+               ow = ar.take(bw);
+  if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  LB_HIP(hipMemcpyAsync(b + ox, x, bx, hipMemcpyHostToDevice, s), "copy x");
+  LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
+  LB_HIP(hipMemcpyAsync(b + os, scales, bs, hipMemcpyHostToDevice, s), "copy scales");
+  if (zeros) LB_HIP(hipMemcpyAsync(b + oz, zeros, bz, hipMemcpyHostToDevice, s), "copy zeros");
+  rc = lbd_gemm_w4a8(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
+                     reinterpret_cast<float *>(b + os), zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr, N,
+                     reinterpret_cast<float *>(b + oy), p, b + ow, bw, s);
+  if (rc < 0) return rc;
+  LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
+  LB_HIP(hipStreamSynchronize(s), "synchronize");
+  return ok(rc);
+}
+
+int lb_gemm_w4a8_q(const int8_t *xq, const float *xs, const int32_t *asum, int M, int Kp,
+                   const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, float *y,
+                   const lb_params *p) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!xq || !xs || !asum || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  Ctx *c = nullptr;
+  if ((rc = get_ctx(&c)) < 0) return rc;
+  const int G = Kp / LB_GROUP;
+  const size_t bxq = (size_t)M * Kp, bxs = (size_t)M * 4, ba = (size_t)M * G * 4, bq = (size_t)N * Kp / 2,
+               bs = (size_t)N * G * 4, bz = zeros ? (size_t)N * G : 0, by = (size_t)M * N * 4;
+  Arena ar;
+  const size_t oxq = ar.take(bxq), oxs = ar.take(bxs), oa = ar.take(ba), oq = ar.take(bq), os = ar.take(bs),
+               oz = ar.take(bz), oy = ar.take(by);
+  if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  LB_HIP(hipMemcpyAsync(b + oxq, xq, bxq, hipMemcpyHostToDevice, s), "copy xq");
+  LB_HIP(hipMemcpyAsync(b + oxs, xs, bxs, hipMemcpyHostToDevice, s), "copy xs");
+  LB_HIP(hipMemcpyAsync(b + oa, asum, ba, hipMemcpyHostToDevice, s), "copy asum");
+  LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
+  LB_HIP(hipMemcpyAsync(b + os, scales, bs, hipMemcpyHostToDevice, s), "copy scales");
+  if (zeros) LB_HIP(hipMemcpyAsync(b + oz, zeros, bz, hipMemcpyHostToDevice, s), "copy zeros");
+  rc = lbd_gemm_w4a8_q(reinterpret_cast<int8_t *>(b + oxq), reinterpret_cast<float *>(b + oxs),
+                       reinterpret_cast<int32_t *>(b + oa), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
+                       reinterpret_cast<float *>(b + os), zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr,
+                       N, reinterpret_cast<float *>(b + oy), p, s);
+  if (rc < 0) return rc;
+  LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
+  LB_HIP(hipStreamSynchronize(s), "synchronize");
+  return ok(rc);
+}
+
+void lb_quant_act_int8(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum) {
+  if (M <= 0 || Kp <= 0 || Kp % LB_GROUP) {
+    fail(LB_ERR_SHAPE, "bad shape");
+    return;
+  }
+  if (!x || !xq || !xs || !asum) {
+    fail(LB_ERR_ARG, "null pointer");
+    return;
+  }
+  Ctx *c = nullptr;
+  if (get_ctx(&c) < 0) return;
+  const int G = Kp / LB_GROUP;
+  const size_t bx = (size_t)M * Kp * 4, bxq = (size_t)M * Kp, bxs = (size_t)M * 4, ba = (size_t)M * G * 4;
+  Arena ar;
+  const size_t ox = ar.take(bx), oxq = ar.take(bxq), oxs = ar.take(bxs), oa = ar.take(ba);
+  if (grow(&c->buf, &c->cap, ar.off, c->stream) < 0) return;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  hipError_t e;
+  if ((e = hipMemcpyAsync(b + ox, x, bx, hipMemcpyHostToDevice, s)) != hipSuccess) { fail_hip(e, "copy x"); return; }
+  if (lbd_quant_act_int8(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<int8_t *>(b + oxq),
+                         reinterpret_cast<float *>(b + oxs), reinterpret_cast<int32_t *>(b + oa), s) < 0)
+    return;
+  if ((e = hipMemcpyAsync(xq, b + oxq, bxq, hipMemcpyDeviceToHost, s)) != hipSuccess) { fail_hip(e, "copy xq"); return; }
+  if ((e = hipMemcpyAsync(xs, b + oxs, bxs, hipMemcpyDeviceToHost, s)) != hipSuccess) { fail_hip(e, "copy xs"); return; }
+  if ((e = hipMemcpyAsync(asum, b + oa, ba, hipMemcpyDeviceToHost, s)) != hipSuccess) { fail_hip(e, "copy asum"); return; }
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) { fail_hip(e, "synchronize"); return; }
+  ok(0);
+}
+
+int lb_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, const uint8_t *qw,
+                      const uint8_t *zeros, int N, int32_t *out, int isa) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!xq || !asum || !qw || !out) return fail(LB_ERR_ARG, "null pointer");
+  Ctx *c = nullptr;
+  if ((rc = get_ctx(&c)) < 0) return rc;
+  const int G = Kp / LB_GROUP;
+  const size_t bxq = (size_t)M * Kp, ba = (size_t)M * G * 4, bq = (size_t)N * Kp / 2, bz = zeros ? (size_t)N * G : 0,
+               bo = (size_t)M * N * G * 4;
+  Arena ar;
+  const size_t oxq = ar.take(bxq), oa = ar.take(ba), oq = ar.take(bq), oz = ar.take(bz), oo = ar.take(bo);
+  if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
+  char *b = c->buf;
+  hipStream_t s = c->stream;
+  LB_HIP(hipMemcpyAsync(b + oxq, xq, bxq, hipMemcpyHostToDevice, s), "copy xq");
+  LB_HIP(hipMemcpyAsync(b + oa, asum, ba, hipMemcpyHostToDevice, s), "copy asum");
+  LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
+  if (zeros) LB_HIP(hipMemcpyAsync(b + oz, zeros, bz, hipMemcpyHostToDevice, s), "copy zeros");
+  rc = lbd_w4a8_group_acc(reinterpret_cast<int8_t *>(b + oxq), reinterpret_cast<int32_t *>(b + oa), M, Kp,
+                          reinterpret_cast<uint8_t *>(b + oq), zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr,
+                          N, reinterpret_cast<int32_t *>(b + oo), isa, s);
+  if (rc < 0) return rc;
+  LB_HIP(hipMemcpyAsync(out, b + oo, bo, hipMemcpyDeviceToHost, s), "copy out");
+  LB_HIP(hipStreamSynchronize(s), "synchronize");
+  return ok(rc);
+}
+
+// ---------------------------------------------------------------- plumbing
+
+int lb_dev_malloc(void **ptr, size_t bytes) {
+  if (!ptr) return fail(LB_ERR_ARG, "null pointer");
+  if (hipMalloc(ptr, bytes ? bytes : 1) != hipSuccess) return fail(LB_ERR_ALLOC, "hipMalloc failed");
+  return ok(0);
+}
+int lb_dev_free(void *ptr) {
+  LB_HIP(hipFree(ptr), "hipFree");
+  return ok(0);
+}
+int lb_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+  LB_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  return ok(0);
+}
+int lb_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+  LB_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+  return ok(0);
+}
+int lb_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+  LB_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice), "hipMemcpy D2D");
+  return ok(0);
+}
+int lb_memset_d(void *dst, int value, size_t bytes) {
+  LB_HIP(hipMemset(dst, value, bytes), "hipMemset");
+  return ok(0);
+}
+int lb_dev_synchronize(void) {
+  LB_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  return ok(0);
+}
+int lb_stream_create(void **stream) {
+  if (!stream) return fail(LB_ERR_ARG, "null pointer");
+  hipStream_t s;
+  LB_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = s;
+  return ok(0);
+}
+int lb_stream_destroy(void *stream) {
+  LB_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+  return ok(0);
+}
+int lb_stream_synchronize(void *stream) {
+  LB_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+  return ok(0);
+}
+int lb_event_create(void **event) {
+  if (!event) return fail(LB_ERR_ARG, "null pointer");
+  hipEvent_t e;
+  LB_HIP(hipEventCreate(&e), "hipEventCreate");
+  *event = e;
+  return ok(0);
+}
+int lb_event_destroy(void *event) {
+  LB_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+  return ok(0);
+}
+int lb_event_record(void *event, void *stream) {
+  LB_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)), "hipEventRecord");
+  return ok(0);
+}
+int lb_event_synchronize(void *event) {
+  LB_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+  return ok(0);
+}
+int lb_event_elapsed_ms(void *start, void *stop, float *ms) {
+  if (!ms) return fail(LB_ERR_ARG, "null pointer");
+  LB_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+         "hipEventElapsedTime");
+  return ok(0);
+}
+int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {
+  if (!dst || !src || bytes % 16 || !aligned16(dst) || !aligned16(src))
+    return fail(LB_ERR_ARG, "copy needs 16-byte aligned pointers and a multiple of 16 bytes");
+  hipError_t e = lbk::launch_copy(dst, src, bytes, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "copy kernel launch");
+  return ok(0);
+}
+
+}  // extern "C"

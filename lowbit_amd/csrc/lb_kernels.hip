@@ -1,0 +1,687 @@
+// gfx950 (MI355X, CDNA4) kernels for the fused dequantize + GEMM
+//     Y[M,N] = X[M,Kp] . W[N,Kp]^T
+// over the packed int4-g128 and MXFP4 layouts (src/lowbit/csrc/lowbit.h:9-19).
+//
+// Regimes
+//   gemv_kernel       M <= 4: HBM-bound. Each lane streams 16 contiguous bytes of
+//                     a weight row (32 codes) per step, decodes them in registers
+//                     and reduces across the wave. No LDS for weights, no MFMA.
+//                     X (or, for W4A8, the int8 codes the fused quantizer
+//                     produces) sits in LDS in "plane" order so that the 32
+//                     activations a lane needs for its 16 bytes are eight (or
+//                     two) conflict-free 16-byte LDS reads.
+//   w4a8_mfma_kernel  W4A8 for larger M: v_mfma_i32_16x16x64_i8 on the int8
+//                     activations and the (q - z) bytes, giving the exact int32
+//                     group accumulator per 16x16 tile, then an fp32 rescale.
+//   f32_mfma_kernel   W4A16 / MXFP4 for larger M: v_mfma_f32_16x16x4_f32 with the
+//                     exactly decoded weights, so products and sums keep fp32
+//                     semantics.
+//   quant_rows_kernel the per-token int8 quantizer (one workgroup per row).
+//
+// MFMA operand mapping. For a 16x16xK MFMA, lane l supplies row (l % 16) of A and
+// column (l % 16) of B for the k-slots owned by lane group q = l / 16; the
+// hardware pairs slot t of A with slot t of B within the same lane group. Which
+// actual k a slot holds is therefore free, as long as A and B agree. Each lane
+// loads 16 contiguous bytes of a weight row (the natural packed order) and puts
+// the matching activations in the same slots, so weights go from HBM to the
+// matrix cores without an LDS transpose.
+#include "lb_device.h"
+#include "lb_internal.h"
+
+namespace lbk {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// ============================================================ per-token quantizer
+
+__global__ __launch_bounds__(kThreads) void quant_rows_kernel(
+    const float *__restrict__ x, int Kp, int8_t *__restrict__ xq,
+    float *__restrict__ xs, int32_t *__restrict__ asum) {
+  __shared__ float red[kWaves];
+  const int m = blockIdx.x;
+  const float *xr = x + (size_t)m * Kp;
+  const float sc = row_scale(block_row_amax<kThreads>(xr, Kp, red));
+  if (threadIdx.x == 0) xs[m] = sc;
+  const int G = Kp / kGroup;
+  uint32_t *qr = reinterpret_cast<uint32_t *>(xq + (size_t)m * Kp);
+  // Thread t handles 4 elements; a group of 128 is one 32-lane half-wave.
+  for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+    int s4;
+    qr[e >> 2] = quant4(*reinterpret_cast<const float4 *>(xr + e), sc, s4);
+    const int gs = half_wave_sum(s4);
+    if ((threadIdx.x & 31) == 0) asum[(size_t)m * G + (e >> 7)] = gs;
+  }
+}
+
+// ============================================================ small-M GEMV (VALU)
+//
+// Work unit: R consecutive weight rows per wave; waves stride over row blocks.
+// Within a row, lane `lane` handles 16-byte chunks ci = lane, lane + 64, ...
+// (chunk ci = bytes [16ci, 16ci+16) of the row = 32 elements):
+//   int4 : group g = ci / 4, bytes b = 16 (ci % 4): low nibbles are elements
+//          128g + b + [0,16), high nibbles 128g + 64 + b + [0,16)
+//   MXFP4: block ci: low nibbles 32ci + [0,16), high nibbles 32ci + 16 + [0,16)
+//
+// LDS plane layout of the activations: for fp32 X, eight planes of float4,
+// plane p = half * 4 + (position within the 16-element half) / 4, entry ci; for
+// int8 codes, two planes of 16 bytes (half 0 / 1). Lane reads of one plane are
+// consecutive 16-byte words: no bank conflicts.
+
+constexpr int kGemvRows = 2;  // weight rows per wave per step
+
+__device__ __forceinline__ void chunk_pos(int fmt, int e, int &ci, int &half, int &within) {
+  if (fmt == F_MXFP4) {
+    const int r = e & 31;
+    ci = e >> 5;
+    half = r >> 4;
+    within = r & 15;
+  } else {
+    const int r = e & 127;
+    ci = ((e >> 7) << 2) + ((r & 63) >> 4);
+    half = r >> 6;
+    within = r & 15;
+  }
+}
+
+size_t gemv_lds_bytes(int fmt, int M, int Kp) {
+  if (fmt == F_W4A16 || fmt == F_MXFP4) return (size_t)M * Kp * sizeof(float);
+  return (size_t)M * Kp + (size_t)M * (Kp / kGroup) * sizeof(int32_t) + 16;
+}
+
+bool gemv_eligible(int fmt, int M, int Kp) {
+  return M >= 1 && M <= kGemvMaxM && gemv_lds_bytes(fmt, M, Kp) <= kGemvLdsLimit;
+}
+
+template <int F, int MB>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemmArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ float red[kWaves];
+  constexpr int R = kGemvRows;
+  constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
+  const int Kp = a.Kp, N = a.N;
+  const int nch = Kp >> 5;            // 16-byte chunks per weight row
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const int G = Kp / kGroup;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+
+  float *xl = reinterpret_cast<float *>(lds);          // fp32 planes [MB][8][nch][4]
+  uint8_t *ql = lds;                                     // int8 planes [MB][2][nch][16]
+  int32_t *asl = reinterpret_cast<int32_t *>(lds + (size_t)MB * Kp);  // [MB][G]
+  float *xsl = reinterpret_cast<float *>(asl + (size_t)MB * G);        // [MB]
+
+  // ---- stage the activations
+  if constexpr (!kInt8) {
+    for (int m = 0; m < MB; m++) {
+      const float *xr = a.x + (size_t)m * Kp;
+      for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+        int ci, half, within;
+        chunk_pos(F, e, ci, half, within);
+        const int plane = half * 4 + (within >> 2);
+        *reinterpret_cast<float4 *>(xl + ((size_t)(m * 8 + plane) * nch + ci) * 4) =
+            *reinterpret_cast<const float4 *>(xr + e);
+      }
+    }
+  } else if constexpr (F == F_W4A8) {
+    // fused per-token quantizer: same arithmetic as quant_rows_kernel
+    for (int m = 0; m < MB; m++) {
+      const float *xr = a.x + (size_t)m * Kp;
+      const float sc = row_scale(block_row_amax<kThreads>(xr, Kp, red));
+      if (threadIdx.x == 0) xsl[m] = sc;
+      for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+        int ci, half, within, s4;
+        chunk_pos(F, e, ci, half, within);
+        const uint32_t q4 = quant4(*reinterpret_cast<const float4 *>(xr + e), sc, s4);
+        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nch + ci) * 16 + within) = q4;
+        const int gs = half_wave_sum(s4);
+        if ((threadIdx.x & 31) == 0) asl[m * G + (e >> 7)] = gs;
+      }
+    }
+  } else {
+    for (int m = 0; m < MB; m++) {
+      const int8_t *qr = a.xq + (size_t)m * Kp;
+      for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+        int ci, half, within;
+        chunk_pos(F, e, ci, half, within);
+        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nch + ci) * 16 + within) =
+            *reinterpret_cast<const uint32_t *>(qr + e);
+      }
+      for (int g = threadIdx.x; g < G; g += kThreads) asl[m * G + g] = a.asum[(size_t)m * G + g];
+      if (threadIdx.x == 0) xsl[m] = a.xs[m];
+    }
+  }
+  __syncthreads();
+
+  const int gw = blockIdx.x * kWaves + wave;
+  const int nw = gridDim.x * kWaves;
+  for (int rb = gw * R; rb < N; rb += nw * R) {
+    float acc[MB][R];
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
+
+    for (int ci = lane; ci < nch; ci += kWave) {
+      // ---- weights of R rows (rows past N re-read row N-1; never stored)
+      uint4 w[R];
+      float sc[R], zf[R];
+      int zi[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int row = min(rb + r, N - 1);
+        w[r] = *reinterpret_cast<const uint4 *>(a.qw + row * rowbytes + (size_t)ci * 16);
+        if constexpr (F == F_MXFP4) {
+          sc[r] = e8m0_to_f32(a.e8m0[(size_t)row * nch + ci]);
+        } else {
+          const int g = ci >> 2;
+          sc[r] = a.scales[(size_t)row * G + g];
+          zi[r] = a.zeros ? (int)a.zeros[(size_t)row * G + g] : 8;
+          zf[r] = (float)zi[r];
+        }
+      }
+      if constexpr (F == F_W4A16) {
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+          float4 xv[8];
+#pragma unroll
+          for (int p = 0; p < 8; p++)
+            xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nch + ci) * 4);
+          // sum of the 32 activations, in the same order as the products below, so
+          // that for a power-of-two zero-point sum(q*x) - z*sum(x) is exactly 0
+          // when every q == z
+          float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+          for (int p = 0; p < 4; p++) {
+            sl += xv[p].x; sl += xv[p].y; sl += xv[p].z; sl += xv[p].w;
+            sh += xv[4 + p].x; sh += xv[4 + p].y; sh += xv[4 + p].z; sh += xv[4 + p].w;
+          }
+          const float xsum = sl + sh;
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+            float pl = 0.0f, ph = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+              const uint32_t lo = lo_nibbles(wd[d]), hi = hi_nibbles(wd[d]);
+              pl = __builtin_fmaf((float)(lo & 0xFF), xv[d].x, pl);
+              pl = __builtin_fmaf((float)((lo >> 8) & 0xFF), xv[d].y, pl);
+              pl = __builtin_fmaf((float)((lo >> 16) & 0xFF), xv[d].z, pl);
+              pl = __builtin_fmaf((float)(lo >> 24), xv[d].w, pl);
+              ph = __builtin_fmaf((float)(hi & 0xFF), xv[4 + d].x, ph);
+              ph = __builtin_fmaf((float)((hi >> 8) & 0xFF), xv[4 + d].y, ph);
+              ph = __builtin_fmaf((float)((hi >> 16) & 0xFF), xv[4 + d].z, ph);
+              ph = __builtin_fmaf((float)(hi >> 24), xv[4 + d].w, ph);
+            }
+            const float part = __builtin_fmaf(-zf[r], xsum, pl + ph);
+            acc[m][r] = __builtin_fmaf(sc[r], part, acc[m][r]);
+          }
+        }
+      } else if constexpr (F == F_MXFP4) {
+        // decode once per row, reuse for every activation row
+        float wl[R][16], wh[R][16];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+#pragma unroll
+          for (int d = 0; d < 4; d++) {
+            const v2f p0 = e2m1_pair<0>(wd[d], 1.0f), p1 = e2m1_pair<1>(wd[d], 1.0f);
+            const v2f p2 = e2m1_pair<2>(wd[d], 1.0f), p3 = e2m1_pair<3>(wd[d], 1.0f);
+            wl[r][4 * d + 0] = p0.x; wh[r][4 * d + 0] = p0.y;
+            wl[r][4 * d + 1] = p1.x; wh[r][4 * d + 1] = p1.y;
+            wl[r][4 * d + 2] = p2.x; wh[r][4 * d + 2] = p2.y;
+            wl[r][4 * d + 3] = p3.x; wh[r][4 * d + 3] = p3.y;
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+          float4 xv[8];
+#pragma unroll
+          for (int p = 0; p < 8; p++)
+            xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nch + ci) * 4);
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            float pl = 0.0f, ph = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+              pl = __builtin_fmaf(wl[r][4 * d + 0], xv[d].x, pl);
+              pl = __builtin_fmaf(wl[r][4 * d + 1], xv[d].y, pl);
+              pl = __builtin_fmaf(wl[r][4 * d + 2], xv[d].z, pl);
+              pl = __builtin_fmaf(wl[r][4 * d + 3], xv[d].w, pl);
+              ph = __builtin_fmaf(wh[r][4 * d + 0], xv[4 + d].x, ph);
+              ph = __builtin_fmaf(wh[r][4 * d + 1], xv[4 + d].y, ph);
+              ph = __builtin_fmaf(wh[r][4 * d + 2], xv[4 + d].z, ph);
+              ph = __builtin_fmaf(wh[r][4 * d + 3], xv[4 + d].w, ph);
+            }
+            acc[m][r] = __builtin_fmaf(sc[r], pl + ph, acc[m][r]);
+          }
+        }
+      } else {
+        // W4A8: int8 dot4 on unsigned codes (0..15 are non-negative int8) and the
+        // int8 activations; the zero-point term z * sum(a) of the group is taken
+        // once, by the lane holding the group's first 16 bytes. Each lane's
+        // integer is exact and below 2^24, so its conversion to fp32 is exact.
+        const int g = ci >> 2;
+        const bool first = (ci & 3) == 0;
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+          const uint4 al = *reinterpret_cast<const uint4 *>(ql + ((size_t)(m * 2 + 0) * nch + ci) * 16);
+          const uint4 ah = *reinterpret_cast<const uint4 *>(ql + ((size_t)(m * 2 + 1) * nch + ci) * 16);
+          const int as = first ? asl[m * G + g] : 0;
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            int d = 0;
+            d = __builtin_amdgcn_sdot4((int)lo_nibbles(w[r].x), (int)al.x, d, false);
+            d = __builtin_amdgcn_sdot4((int)hi_nibbles(w[r].x), (int)ah.x, d, false);
+            d = __builtin_amdgcn_sdot4((int)lo_nibbles(w[r].y), (int)al.y, d, false);
+            d = __builtin_amdgcn_sdot4((int)hi_nibbles(w[r].y), (int)ah.y, d, false);
+            d = __builtin_amdgcn_sdot4((int)lo_nibbles(w[r].z), (int)al.z, d, false);
+            d = __builtin_amdgcn_sdot4((int)hi_nibbles(w[r].z), (int)ah.z, d, false);
+            d = __builtin_amdgcn_sdot4((int)lo_nibbles(w[r].w), (int)al.w, d, false);
+            d = __builtin_amdgcn_sdot4((int)hi_nibbles(w[r].w), (int)ah.w, d, false);
+            d -= zi[r] * as;
+            acc[m][r] = __builtin_fmaf(sc[r], (float)d, acc[m][r]);
+          }
+        }
+      }
+    }
+    // ---- reduce across the wave; lane m*R + r stores (m, r)
+#pragma unroll
+    for (int m = 0; m < MB; m++)
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        float t = wave_sum(acc[m][r]);
+        if constexpr (kInt8) t *= xsl[m];
+        if (lane == m * R + r && rb + r < N) a.y[(size_t)m * N + rb + r] = t;
+      }
+  }
+}
+
+template <int F>
+static hipError_t launch_gemv_mb(const GemmArgs &a, int grid, size_t lds, hipStream_t s) {
+  switch (a.M) {
+    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1>), dim3(grid), dim3(kThreads), lds, s, a); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2>), dim3(grid), dim3(kThreads), lds, s, a); break;
+    case 3: hipLaunchKernelGGL((gemv_kernel<F, 3>), dim3(grid), dim3(kThreads), lds, s, a); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<F, 4>), dim3(grid), dim3(kThreads), lds, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
+  if (!gemv_eligible(fmt, a.M, a.Kp)) return hipErrorInvalidValue;
+  const size_t lds = gemv_lds_bytes(fmt, a.M, a.Kp);
+  const int row_blocks = (a.N + kGemvRows - 1) / kGemvRows;
+  const int want = (row_blocks + kWaves - 1) / kWaves;
+  // Enough workgroups to fill every CU several times over; more would only
+  // repeat the activation staging.
+  const int cap = (num_cus > 0 ? num_cus : 256) * 4;
+  const int grid = want < cap ? want : cap;
+  switch (fmt) {
+    case F_W4A16: return launch_gemv_mb<F_W4A16>(a, grid, lds, s);
+    case F_MXFP4: return launch_gemv_mb<F_MXFP4>(a, grid, lds, s);
+    case F_W4A8: return launch_gemv_mb<F_W4A8>(a, grid, lds, s);
+    case F_W4A8Q: return launch_gemv_mb<F_W4A8Q>(a, grid, lds, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs,
+                        int32_t *asum, hipStream_t s) {
+  hipLaunchKernelGGL(quant_rows_kernel, dim3(M), dim3(kThreads), 0, s, x, Kp, xq, xs, asum);
+  return hipGetLastError();
+}
+
+// ============================================================ W4A8, int8 MFMA
+//
+// Workgroup tile: (16*TM) activation rows x (16*TN) weight rows; the four waves
+// split the groups of K (wave w takes groups w, w+4, ...) and their fp32
+// partial tiles are summed through LDS at the end (a fixed order, so results
+// are deterministic).
+//
+// Per group g, lane (q = l/16, c = l%16):
+//   B (weights, row n0+16j+c): 16 bytes at row offset 64g + 16q -> low nibbles are
+//     elements 128g+16q+[0,16), high nibbles 128g+64+16q+[0,16); each byte becomes
+//     the signed int8 (q - z).
+//   A (activations, row m0+16i+c): the int8 codes of those same elements.
+//   Two MFMAs (low half, high half) give the exact group total per tile element.
+template <int TM, int TN, bool EXPORT>
+__global__ __launch_bounds__(kThreads) void w4a8_mfma_kernel(GemmArgs a, int32_t *__restrict__ out) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int q = lane >> 4, c = lane & 15;
+  const int M = a.M, N = a.N, Kp = a.Kp, G = Kp / kGroup;
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const int n0 = blockIdx.x * 16 * TN, m0 = blockIdx.y * 16 * TM;
+
+  int nrow[TN], mrow[TM];
+  bool nok[TN], mok[TM];
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int n = n0 + 16 * j + c;
+    nok[j] = n < N;
+    nrow[j] = nok[j] ? n : N - 1;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int m = m0 + 16 * i + c;
+    mok[i] = m < M;
+    mrow[i] = mok[i] ? m : M - 1;
+  }
+
+  v4f facc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) facc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const v4i zero4 = {0, 0, 0, 0};
+  for (int g = wave; g < G; g += kWaves) {
+    v4i blo[TN], bhi[TN];
+    float sc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(a.qw + nrow[j] * rowbytes + (size_t)g * 64 + q * 16);
+      const uint32_t z = a.zeros ? a.zeros[(size_t)nrow[j] * G + g] : 8u;
+      const uint32_t zrep = z * 0x01010101u;
+      blo[j] = v4i{(int)sub_zero_bytes(lo_nibbles(w.x), zrep), (int)sub_zero_bytes(lo_nibbles(w.y), zrep),
+                   (int)sub_zero_bytes(lo_nibbles(w.z), zrep), (int)sub_zero_bytes(lo_nibbles(w.w), zrep)};
+      bhi[j] = v4i{(int)sub_zero_bytes(hi_nibbles(w.x), zrep), (int)sub_zero_bytes(hi_nibbles(w.y), zrep),
+                   (int)sub_zero_bytes(hi_nibbles(w.z), zrep), (int)sub_zero_bytes(hi_nibbles(w.w), zrep)};
+      if (!nok[j]) { blo[j] = zero4; bhi[j] = zero4; }
+      if constexpr (!EXPORT) sc[j] = a.scales[(size_t)nrow[j] * G + g];
+    }
+    v4i alo[TM], ahi[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int8_t *p = a.xq + (size_t)mrow[i] * Kp + (size_t)g * kGroup + q * 16;
+      alo[i] = *reinterpret_cast<const v4i *>(p);
+      ahi[i] = *reinterpret_cast<const v4i *>(p + 64);
+      if (!mok[i]) { alo[i] = zero4; ahi[i] = zero4; }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[i], blo[j], zero4, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[i], bhi[j], acc, 0, 0, 0);
+        if constexpr (EXPORT) {
+          const int n = n0 + 16 * j + c;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int m = m0 + 16 * i + 4 * q + r;
+            if (m < M && n < N) out[((size_t)m * N + n) * G + g] = acc[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; r++) facc[i][j][r] = __builtin_fmaf((float)acc[r], sc[j], facc[i][j][r]);
+        }
+      }
+  }
+  if constexpr (!EXPORT) {
+    // cross-wave sum through LDS: red[w][idx][lane], then wave w finalises idx = w, w+4, ...
+    constexpr int NV = TM * TN * 4;
+    __shared__ float red[kWaves][NV][kWave];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[wave][(i * TN + j) * 4 + r][lane] = facc[i][j][r];
+    __syncthreads();
+    for (int idx = wave; idx < NV; idx += kWaves) {
+      const int i = idx / (TN * 4), j = (idx / 4) % TN, r = idx % 4;
+      const float t = (red[0][idx][lane] + red[1][idx][lane]) + (red[2][idx][lane] + red[3][idx][lane]);
+      const int m = m0 + 16 * i + 4 * q + r, n = n0 + 16 * j + c;
+      if (m < M && n < N) a.y[(size_t)m * N + n] = t * a.xs[m];
+    }
+  }
+}
+
+template <int TM>
+static hipError_t launch_w4a8_tm(const GemmArgs &a, int32_t *out, hipStream_t s) {
+  constexpr int TN = 2;
+  dim3 grid((a.N + 16 * TN - 1) / (16 * TN), (a.M + 16 * TM - 1) / (16 * TM));
+  if (out)
+    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, TN, true>), grid, dim3(kThreads), 0, s, a, out);
+  else
+    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, TN, false>), grid, dim3(kThreads), 0, s, a, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, hipStream_t s) {
+  if (a.M <= 16) return launch_w4a8_tm<1>(a, out, s);
+  if (a.M <= 32) return launch_w4a8_tm<2>(a, out, s);
+  return launch_w4a8_tm<4>(a, out, s);
+}
+
+// ============================================================ W4A16 / MXFP4, fp32 MFMA
+//
+// K is walked in chunks of 128 elements (one int4 group, or four MXFP4 blocks);
+// waves split the chunks. Lane (q, c) loads the 16 bytes at row offset
+// 64*chunk + 16q, i.e.
+//   int4 : group `chunk`, low nibbles at k = 128*chunk + 16q + u, high at +64
+//   MXFP4: block 4*chunk + q, low nibbles at k = 128*chunk + 32q + u, high at +16
+// (u = byte 0..15). Byte u feeds two MFMA k-slots: (low, high). The int4 group
+// product is accumulated unscaled ((q - z) is exact in fp32) and rescaled by s
+// once per group; MXFP4 weights carry their power-of-two block scale exactly.
+template <int F, int TM, int TN>
+__global__ __launch_bounds__(kThreads) void f32_mfma_kernel(GemmArgs a) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int q = lane >> 4, c = lane & 15;
+  const int M = a.M, N = a.N, Kp = a.Kp;
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const int nchunk = (Kp + 127) >> 7;
+  const int G = Kp / kGroup, B = Kp / kMxBlock;
+  const int n0 = blockIdx.x * 16 * TN, m0 = blockIdx.y * 16 * TM;
+  constexpr int kHiOff = (F == F_MXFP4) ? 16 : 64;
+
+  int nrow[TN], mrow[TM];
+  bool nok[TN], mok[TM];
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int n = n0 + 16 * j + c;
+    nok[j] = n < N;
+    nrow[j] = nok[j] ? n : N - 1;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int m = m0 + 16 * i + c;
+    mok[i] = m < M;
+    mrow[i] = mok[i] ? m : M - 1;
+  }
+  v4f facc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) facc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int ch = wave; ch < nchunk; ch += kWaves) {
+    const bool kok = (F == F_MXFP4) ? (4 * ch + q < B) : true;
+    const int kbase = (F == F_MXFP4) ? 128 * ch + 32 * q : 128 * ch + 16 * q;
+    uint4 w[TN];
+    float zf[TN], sc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      w[j] = kok ? *reinterpret_cast<const uint4 *>(a.qw + nrow[j] * rowbytes + (size_t)ch * 64 + q * 16)
+                 : make_uint4(0, 0, 0, 0);
+      if constexpr (F == F_MXFP4) {
+        sc[j] = (kok && nok[j]) ? e8m0_to_f32(a.e8m0[(size_t)nrow[j] * B + 4 * ch + q]) : 0.0f;
+      } else {
+        sc[j] = a.scales[(size_t)nrow[j] * G + ch];
+        zf[j] = a.zeros ? (float)a.zeros[(size_t)nrow[j] * G + ch] : 8.0f;
+        if (!nok[j]) zf[j] = 0.0f, w[j] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    v4f dacc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) dacc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      float4 xlo[TM], xhi[TM];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const float *xr = a.x + (size_t)mrow[i] * Kp + kbase + 4 * d;
+        if (mok[i] && kok) {
+          xlo[i] = *reinterpret_cast<const float4 *>(xr);
+          xhi[i] = *reinterpret_cast<const float4 *>(xr + kHiOff);
+        } else {
+          xlo[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+          xhi[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      float wl[TN][4], wh[TN][4];
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint32_t wd = d == 0 ? w[j].x : d == 1 ? w[j].y : d == 2 ? w[j].z : w[j].w;
+        if constexpr (F == F_MXFP4) {
+          const v2f p0 = e2m1_pair<0>(wd, sc[j]), p1 = e2m1_pair<1>(wd, sc[j]);
+          const v2f p2 = e2m1_pair<2>(wd, sc[j]), p3 = e2m1_pair<3>(wd, sc[j]);
+          wl[j][0] = p0.x; wh[j][0] = p0.y; wl[j][1] = p1.x; wh[j][1] = p1.y;
+          wl[j][2] = p2.x; wh[j][2] = p2.y; wl[j][3] = p3.x; wh[j][3] = p3.y;
+        } else {
+          const uint32_t lo = lo_nibbles(wd), hi = hi_nibbles(wd);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            wl[j][u] = (float)((lo >> (8 * u)) & 0xFF) - zf[j];
+            wh[j][u] = (float)((hi >> (8 * u)) & 0xFF) - zf[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const float xa = u == 0 ? xlo[i].x : u == 1 ? xlo[i].y : u == 2 ? xlo[i].z : xlo[i].w;
+          const float xb = u == 0 ? xhi[i].x : u == 1 ? xhi[i].y : u == 2 ? xhi[i].z : xhi[i].w;
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            if constexpr (F == F_MXFP4) {
+              facc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wl[j][u], facc[i][j], 0, 0, 0);
+              facc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, wh[j][u], facc[i][j], 0, 0, 0);
+            } else {
+              dacc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, wl[j][u], dacc[i][j], 0, 0, 0);
+              dacc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, wh[j][u], dacc[i][j], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    if constexpr (F == F_W4A16) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) facc[i][j][r] = __builtin_fmaf(sc[j], dacc[i][j][r], facc[i][j][r]);
+    }
+  }
+  constexpr int NV = TM * TN * 4;
+  __shared__ float red[kWaves][NV][kWave];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) red[wave][(i * TN + j) * 4 + r][lane] = facc[i][j][r];
+  __syncthreads();
+  for (int idx = wave; idx < NV; idx += kWaves) {
+    const int i = idx / (TN * 4), j = (idx / 4) % TN, r = idx % 4;
+    const float t = (red[0][idx][lane] + red[1][idx][lane]) + (red[2][idx][lane] + red[3][idx][lane]);
+    const int m = m0 + 16 * i + 4 * q + r, n = n0 + 16 * j + c;
+    if (m < M && n < N) a.y[(size_t)m * N + n] = t;
+  }
+}
+
+template <int F, int TM>
+static hipError_t launch_f32_tm(const GemmArgs &a, hipStream_t s) {
+  constexpr int TN = 2;
+  dim3 grid((a.N + 16 * TN - 1) / (16 * TN), (a.M + 16 * TM - 1) / (16 * TM));
+  hipLaunchKernelGGL((f32_mfma_kernel<F, TM, TN>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_mfma(int fmt, const GemmArgs &a, hipStream_t s) {
+  if (fmt == F_W4A16) {
+    if (a.M <= 16) return launch_f32_tm<F_W4A16, 1>(a, s);
+    if (a.M <= 32) return launch_f32_tm<F_W4A16, 2>(a, s);
+    return launch_f32_tm<F_W4A16, 4>(a, s);
+  }
+  if (fmt == F_MXFP4) {
+    if (a.M <= 16) return launch_f32_tm<F_MXFP4, 1>(a, s);
+    if (a.M <= 32) return launch_f32_tm<F_MXFP4, 2>(a, s);
+    return launch_f32_tm<F_MXFP4, 4>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ============================================================ group accumulators (dot4 path)
+//
+// out[m, n, g] through exactly the integer arithmetic the W4A8 GEMV uses: for
+// each 16-byte chunk of the group, eight dot4 of unsigned codes and int8
+// activations, then minus z * asum.
+__global__ __launch_bounds__(kThreads) void groupacc_dot4_kernel(
+    const int8_t *__restrict__ xq, const int32_t *__restrict__ asum, int M, int Kp,
+    const uint8_t *__restrict__ qw, const uint8_t *__restrict__ zeros, int N,
+    int32_t *__restrict__ out) {
+  const int G = Kp / kGroup;
+  const size_t total = (size_t)M * N * G;
+  for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+    const int g = (int)(t % G);
+    const int n = (int)((t / G) % N);
+    const int m = (int)(t / ((size_t)G * N));
+    const uint8_t *wrow = qw + (size_t)n * (Kp >> 1) + (size_t)g * 64;
+    const int8_t *arow = xq + (size_t)m * Kp + (size_t)g * kGroup;
+    int d = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(wrow + 16 * b);
+      const uint4 al = *reinterpret_cast<const uint4 *>(arow + 16 * b);
+      const uint4 ah = *reinterpret_cast<const uint4 *>(arow + 64 + 16 * b);
+      d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.x), (int)al.x, d, false);
+      d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.x), (int)ah.x, d, false);
+      d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.y), (int)al.y, d, false);
+      d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.y), (int)ah.y, d, false);
+      d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.z), (int)al.z, d, false);
+      d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.z), (int)ah.z, d, false);
+      d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.w), (int)al.w, d, false);
+      d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.w), (int)ah.w, d, false);
+    }
+    const int z = zeros ? (int)zeros[(size_t)n * G + g] : 8;
+    out[t] = d - z * asum[(size_t)m * G + g];
+  }
+}
+
+hipError_t launch_groupacc_dot4(const int8_t *xq, const int32_t *asum, int M, int Kp,
+                                const uint8_t *qw, const uint8_t *zeros, int N,
+                                int32_t *out, hipStream_t s) {
+  const size_t total = (size_t)M * N * (Kp / kGroup);
+  size_t blocks = (total + kThreads - 1) / kThreads;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(groupacc_dot4_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, xq, asum, M, Kp, qw,
+                     zeros, N, out);
+  return hipGetLastError();
+}
+
+// ============================================================ copy (traffic calibration)
+
+__global__ __launch_bounds__(kThreads) void copy16_kernel(uint4 *__restrict__ dst, const uint4 *__restrict__ src,
+                                                          size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n16; i += (size_t)gridDim.x * kThreads)
+    dst[i] = src[i];
+}
+
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s) {
+  const size_t n16 = bytes / 16;
+  size_t blocks = (n16 + kThreads - 1) / kThreads;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, static_cast<uint4 *>(dst),
+                     static_cast<const uint4 *>(src), n16);
+  return hipGetLastError();
+}
+
+}  // namespace lbk

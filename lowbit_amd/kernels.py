@@ -1,0 +1,399 @@
+"""ctypes binding to liblowbit_hip.so, the gfx950 fused dequantize+GEMM library.
+
+Mirrors the reference binding (src/lowbit/kernels.py): the same public
+functions, arguments and error behaviour (rc < 0 -> ValueError for bad shapes,
+tiles and arguments), so callers switch by changing the import. Differences,
+all forced by the device:
+  * `isa` names a GPU path: "gfx950" (VALU decode kernels, small M) or
+    "gfx950-mfma" (matrix cores). The reference's CPU names ("scalar", "avx2",
+    "avx512") and "auto"/None mean "choose by shape"; there are no CPU tiers.
+  * `threads` is accepted and ignored; `Params` tile fields are validated like
+    the reference (an uncompiled (mr, nr) raises) and otherwise ignored.
+  * Weights passed as Int4Weights / MXFP4Weights are uploaded on every call
+    (the pointer ABI keeps no state). `to_device(w)` uploads once and returns a
+    resident handle that every gemm_* accepts in place of the host container.
+The library is never compiled here; a missing build raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from dataclasses import asdict, dataclass
+from functools import lru_cache
+
+import numpy as np
+
+from ._build import lib_path
+from .formats import GROUP, MXBLOCK, Int4Weights, Int8Acts, MXFP4Weights, pad_acts
+
+ISA_GFX950 = 16
+ISA_GFX950_MFMA = 17
+ISA_NAMES = {ISA_GFX950: "gfx950", ISA_GFX950_MFMA: "gfx950-mfma"}
+ISA_IDS = {v: k for k, v in ISA_NAMES.items()}
+LEGACY_ISAS = ("scalar", "avx2", "avx512")  # reference CPU tiers: accepted, mean "auto"
+KIND_IDS = {"w4a16": 0, "mxfp4": 1, "w4a8": 2}
+
+
+class _Params(C.Structure):
+    _fields_ = [(f, C.c_int) for f in ("isa", "mr", "nr", "nb", "kb", "order", "nthreads")]
+
+
+@dataclass(frozen=True)
+class Params:
+    """Dispatch parameters (include/lowbit_hip.h lb_params). 0 means 'default'.
+
+    Same fields as the reference's Params (src/lowbit/kernels.py:22-33). The GPU
+    kernels choose their tiles from the shape regime; (mr, nr) is still checked
+    against the reference's micro-tile list so an invalid request fails alike.
+    """
+    mr: int = 0
+    nr: int = 0
+    nb: int = 0
+    kb: int = 0
+    order: int = 0
+
+    def as_dict(self) -> dict:
+        return asdict(self)
+
+
+TILES = [(1, 1), (1, 2), (1, 4), (2, 1), (2, 2), (2, 4), (4, 1), (4, 2), (4, 4), (8, 1), (8, 2)]
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_vp = C.c_void_p
+_int = C.c_int
+_sz = C.c_size_t
+_pp = C.POINTER(_Params)
+
+# name -> (argtypes, restype): every symbol the header declares
+SIGNATURES = {
+    "lb_version": ([], _int),
+    "lb_cpu_isa": ([], _int),
+    "lb_active_isa": ([], _int),
+    "lb_has_vnni": ([], _int),
+    "lb_has_openmp": ([], _int),
+    "lb_max_threads": ([], _int),
+    "lb_effective_isa": ([_int, _int], _int),
+    "lb_device_info": ([C.c_char_p, _int, C.POINTER(_int), C.POINTER(_int)], _int),
+    "lb_last_error": ([], C.c_char_p),
+    "lb_last_status": ([], _int),
+    "lb_gemm_w4a16": ([_f32p, _int, _int, _u8p, _f32p, _vp, _int, _f32p, _pp], _int),
+    "lb_gemm_mxfp4": ([_f32p, _int, _int, _u8p, _u8p, _int, _f32p, _pp], _int),
+    "lb_gemm_w4a8": ([_f32p, _int, _int, _u8p, _f32p, _vp, _int, _f32p, _pp], _int),
+    "lb_gemm_w4a8_q": ([_i8p, _f32p, _i32p, _int, _int, _u8p, _f32p, _vp, _int, _f32p, _pp], _int),
+    "lb_quant_act_int8": ([_f32p, _int, _int, _i8p, _f32p, _i32p], None),
+    "lb_w4a8_group_acc": ([_i8p, _i32p, _int, _int, _u8p, _vp, _int, _i32p, _int], _int),
+    "lbd_gemm_w4a16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp], _int),
+    "lbd_gemm_mxfp4": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp], _int),
+    "lbd_gemm_w4a8": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_w4a8_workspace_bytes": ([_int, _int], _sz),
+    "lbd_gemm_w4a8_q": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp], _int),
+    "lbd_quant_act_int8": ([_vp, _int, _int, _vp, _vp, _vp, _vp], _int),
+    "lbd_w4a8_group_acc": ([_vp, _vp, _int, _int, _vp, _vp, _int, _vp, _int, _vp], _int),
+    "lb_dev_malloc": ([C.POINTER(_vp), _sz], _int),
+    "lb_dev_free": ([_vp], _int),
+    "lb_memcpy_h2d": ([_vp, _vp, _sz], _int),
+    "lb_memcpy_d2h": ([_vp, _vp, _sz], _int),
+    "lb_memcpy_d2d": ([_vp, _vp, _sz], _int),
+    "lb_memset_d": ([_vp, _int, _sz], _int),
+    "lb_dev_synchronize": ([], _int),
+    "lb_stream_create": ([C.POINTER(_vp)], _int),
+    "lb_stream_destroy": ([_vp], _int),
+    "lb_stream_synchronize": ([_vp], _int),
+    "lb_event_create": ([C.POINTER(_vp)], _int),
+    "lb_event_destroy": ([_vp], _int),
+    "lb_event_record": ([_vp, _vp], _int),
+    "lb_event_synchronize": ([_vp], _int),
+    "lb_event_elapsed_ms": ([_vp, _vp, C.POINTER(C.c_float)], _int),
+    "lbd_copy_kernel": ([_vp, _vp, _sz, _vp], _int),
+}
+
+
+@lru_cache(maxsize=1)
+def lib() -> C.CDLL:
+    """Load liblowbit_hip.so (raises if it was never built)."""
+    so = C.CDLL(str(lib_path()))
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(so, name)
+        fn.argtypes = args
+        fn.restype = res
+    return so
+
+
+def _err(rc: int, what: str):
+    msg = lib().lb_last_error().decode(errors="replace")
+    if rc in (-1, -2, -6):
+        raise ValueError(f"{what} failed (rc={rc}): {msg}")
+    raise RuntimeError(f"{what} failed (rc={rc}): {msg}")
+
+
+_LAST = threading.local()
+
+
+def _check(rc: int, what: str) -> int:
+    if rc < 0:
+        _err(rc, what)
+    _LAST.rc = rc
+    return rc
+
+
+def last_path() -> str:
+    """Name of the path ("gfx950" or "gfx950-mfma") the calling thread's last GEMM ran on,
+    the way the reference's GEMMs return the ISA they ran with (src/lowbit/csrc/dispatch.c:202)."""
+    return ISA_NAMES.get(getattr(_LAST, "rc", -1), "none")
+
+
+def device_info() -> dict:
+    L = lib()
+    name = C.create_string_buffer(64)
+    cus, lds = _int(0), _int(0)
+    _check(L.lb_device_info(name, 64, C.byref(cus), C.byref(lds)), "lb_device_info")
+    return {"arch": name.value.decode(), "compute_units": cus.value, "lds_per_workgroup": lds.value}
+
+
+def cpu_info() -> dict:
+    """Library capabilities, with the reference's keys (src/lowbit/kernels.py:77-86).
+
+    `cpu_isa` / `active_isa` name the best device path ("gfx950-mfma" on an
+    MI355X); the CPU-only features report False / 1.
+    """
+    L = lib()
+    top, act = L.lb_cpu_isa(), L.lb_active_isa()
+    info = {
+        "cpu_isa": ISA_NAMES.get(top, "none"),
+        "active_isa": ISA_NAMES.get(act, "none"),
+        "vnni": bool(L.lb_has_vnni()),
+        "openmp": bool(L.lb_has_openmp()),
+        "max_threads": L.lb_max_threads(),
+        "amx": amx_available(),
+    }
+    if top >= 0:
+        info.update(device_info())
+    return info
+
+
+def amx_available() -> bool:
+    """The AMX tile path is CPU-only; the GPU library has none (src/lowbit/kernels.py:89-94)."""
+    return False
+
+
+def _isa_id(isa) -> int:
+    if isa is None or isa == "auto" or isa in LEGACY_ISAS:
+        return -1
+    if isinstance(isa, int):
+        return isa
+    if isa not in ISA_IDS:
+        raise ValueError(f"unknown isa {isa!r}; use one of {sorted(ISA_IDS)} or 'auto'")
+    return ISA_IDS[isa]
+
+
+def effective_isa(kind: str, isa=None) -> str:
+    """Path name a GEMM kind runs with for a request (src/lowbit/kernels.py:103-104)."""
+    rc = lib().lb_effective_isa(KIND_IDS[kind], _isa_id(isa))
+    return ISA_NAMES.get(rc, "none")
+
+
+def auto_params(kind: str, m: int, n: int, k: int, isa=None, threads=None) -> Params:
+    """The reference resolves "auto" through its CPU tile cache (src/lowbit/kernels.py:110-116);
+    the GPU kernels pick their tiles from the shape, so "auto" is the default Params."""
+    return Params()
+
+
+def _params(p, isa, threads, kind=None, shape=None) -> _Params:
+    if isinstance(p, str):
+        if p != "auto":
+            raise ValueError(f"params must be a Params, None or 'auto', not {p!r}")
+        p = auto_params(kind, *shape, isa=isa, threads=threads)
+    p = p or Params()
+    return _Params(_isa_id(isa), p.mr, p.nr, p.nb, p.kb, p.order, threads or 0)
+
+
+def _zp(z: np.ndarray | None):
+    return None if z is None else z.ctypes.data_as(C.c_void_p)
+
+
+class _Prepared:
+    """Padded, contiguous X plus an output buffer (src/lowbit/kernels.py:138-146)."""
+
+    def __init__(self, x: np.ndarray, kp: int, n: int):
+        x = np.asarray(x, np.float32)
+        if x.ndim == 1:
+            x = x[None]
+        self.x = pad_acts(x, kp)
+        self.y = np.empty((x.shape[0], n), np.float32)
+
+
+# ------------------------------------------------------------------ device residency
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed when garbage collected)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        _check(lib().lb_dev_malloc(C.byref(p), max(1, self.nbytes)), "lb_dev_malloc")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        if a.nbytes:
+            _check(lib().lb_memcpy_h2d(b.ptr, a.ctypes.data, a.nbytes), "lb_memcpy_h2d")
+        return b
+
+    def to_array(self, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if out.nbytes:
+            _check(lib().lb_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "lb_memcpy_d2h")
+        return out
+
+    def __del__(self):
+        try:
+            if getattr(self, "ptr", None):
+                lib().lb_dev_free(self.ptr)
+                self.ptr = None
+        except Exception:  # interpreter shutdown
+            pass
+
+
+@dataclass
+class DeviceInt4Weights:
+    """int4 g128 weights resident in HBM (same layout as Int4Weights)."""
+    qw: DeviceBuffer
+    scales: DeviceBuffer
+    zeros: DeviceBuffer | None
+    n: int
+    kp: int
+    k: int
+    nbytes: int
+
+
+@dataclass
+class DeviceMXFP4Weights:
+    """MXFP4 weights resident in HBM (same layout as MXFP4Weights)."""
+    qw: DeviceBuffer
+    e8m0: DeviceBuffer
+    n: int
+    kp: int
+    k: int
+    nbytes: int
+
+
+def to_device(w):
+    """Upload packed weights once; the returned handle is accepted by every gemm_*.
+
+    The handle is a snapshot: later edits of the host arrays are not seen.
+    """
+    if isinstance(w, Int4Weights):
+        return DeviceInt4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.scales),
+                                 None if w.zeros is None else DeviceBuffer.from_array(w.zeros),
+                                 w.n, w.kp, w.k, w.nbytes)
+    if isinstance(w, MXFP4Weights):
+        return DeviceMXFP4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.e8m0),
+                                  w.n, w.kp, w.k, w.nbytes)
+    if isinstance(w, (DeviceInt4Weights, DeviceMXFP4Weights)):
+        return w
+    raise TypeError(f"cannot upload {type(w).__name__}")
+
+
+def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
+    L = lib()
+    m = pr.x.shape[0]
+    dx = DeviceBuffer.from_array(pr.x)
+    dy = DeviceBuffer(pr.y.nbytes)
+    zp = None if getattr(w, "zeros", None) is None else w.zeros.ptr
+    if kind == "w4a16":
+        rc = L.lbd_gemm_w4a16(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm), None)
+    elif kind == "mxfp4":
+        rc = L.lbd_gemm_mxfp4(dx.ptr, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, dy.ptr, C.byref(prm), None)
+    else:
+        ws = DeviceBuffer(L.lbd_w4a8_workspace_bytes(m, w.kp))
+        rc = L.lbd_gemm_w4a8(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm),
+                             ws.ptr, ws.nbytes, None)
+    _check(rc, f"lbd_gemm_{kind}")
+    pr.y[...] = dy.to_array(pr.y.shape, np.float32)  # synchronous copy on the null stream
+    return pr.y
+
+
+# ------------------------------------------------------------------ GEMMs
+
+def gemm_w4a16(x, w, params: Params | None = None, isa=None, threads: int | None = None,
+               _prep: _Prepared | None = None) -> np.ndarray:
+    """Y = X @ dequant(W)^T, fp32 activations and accumulation (src/lowbit/kernels.py:149-156)."""
+    pr = _prep or _Prepared(x, w.kp, w.n)
+    prm = _params(params, isa, threads, "w4a16", (pr.x.shape[0], w.n, w.k))
+    if isinstance(w, DeviceInt4Weights):
+        return _dev_gemm("w4a16", pr, w, prm)
+    rc = lib().lb_gemm_w4a16(pr.x, pr.x.shape[0], w.kp, w.qw, w.scales, _zp(w.zeros), w.n, pr.y,
+                             C.byref(prm))
+    _check(rc, "lb_gemm_w4a16")
+    return pr.y
+
+
+def gemm_mxfp4(x, w, params: Params | None = None, isa=None, threads: int | None = None,
+               _prep: _Prepared | None = None) -> np.ndarray:
+    """Y = X @ dequant(W)^T for OCP MXFP4 weights (src/lowbit/kernels.py:159-166)."""
+    pr = _prep or _Prepared(x, w.kp, w.n)
+    prm = _params(params, isa, threads, "mxfp4", (pr.x.shape[0], w.n, w.k))
+    if isinstance(w, DeviceMXFP4Weights):
+        return _dev_gemm("mxfp4", pr, w, prm)
+    rc = lib().lb_gemm_mxfp4(pr.x, pr.x.shape[0], w.kp, w.qw, w.e8m0, w.n, pr.y, C.byref(prm))
+    _check(rc, "lb_gemm_mxfp4")
+    return pr.y
+
+
+def gemm_w4a8(x, w, params: Params | None = None, isa=None, threads: int | None = None,
+              _prep: _Prepared | None = None) -> np.ndarray:
+    """fp32 X in; X is quantized per token to int8 on the device inside the call
+    (src/lowbit/kernels.py:169-177)."""
+    pr = _prep or _Prepared(x, w.kp, w.n)
+    prm = _params(params, isa, threads, "w4a8", (pr.x.shape[0], w.n, w.k))
+    if isinstance(w, DeviceInt4Weights):
+        return _dev_gemm("w4a8", pr, w, prm)
+    rc = lib().lb_gemm_w4a8(pr.x, pr.x.shape[0], w.kp, w.qw, w.scales, _zp(w.zeros), w.n, pr.y,
+                            C.byref(prm))
+    _check(rc, "lb_gemm_w4a8")
+    return pr.y
+
+
+def gemm_w4a8_q(a: Int8Acts, w: Int4Weights, params: Params | None = None, isa=None,
+                threads: int | None = None) -> np.ndarray:
+    """W4A8 on already-quantized activations (src/lowbit/kernels.py:180-187)."""
+    y = np.empty((a.xq.shape[0], w.n), np.float32)
+    prm = _params(params, isa, threads, "w4a8", (a.xq.shape[0], w.n, w.k))
+    rc = lib().lb_gemm_w4a8_q(np.ascontiguousarray(a.xq), np.ascontiguousarray(a.scale, np.float32),
+                              np.ascontiguousarray(a.gsum, np.int32), a.xq.shape[0], w.kp, w.qw,
+                              w.scales, _zp(w.zeros), w.n, y, C.byref(prm))
+    _check(rc, "lb_gemm_w4a8_q")
+    return y
+
+
+def quant_act_int8(x: np.ndarray, kp: int) -> Int8Acts:
+    """The device per-token int8 quantizer (src/lowbit/kernels.py:190-197)."""
+    xp = pad_acts(np.atleast_2d(x), kp)
+    m = xp.shape[0]
+    xq = np.empty((m, kp), np.int8)
+    xs = np.empty(m, np.float32)
+    gs = np.empty((m, kp // GROUP), np.int32)
+    L = lib()
+    L.lb_quant_act_int8(xp, m, kp, xq, xs, gs)
+    _check(L.lb_last_status(), "lb_quant_act_int8")
+    return Int8Acts(xq, xs, gs)
+
+
+def w4a8_group_acc(a: Int8Acts, w: Int4Weights, isa=None) -> np.ndarray:
+    """Exact int32 group accumulators [M, N, G] from the device integer path named by
+    `isa` ("gfx950" dot4 VALU, "gfx950-mfma" int8 MFMA) (src/lowbit/kernels.py:200-205)."""
+    m = a.xq.shape[0]
+    out = np.empty((m, w.n, w.kp // GROUP), np.int32)
+    _check(lib().lb_w4a8_group_acc(np.ascontiguousarray(a.xq), np.ascontiguousarray(a.gsum, np.int32),
+                                   m, w.kp, w.qw, _zp(w.zeros), w.n, out, _isa_id(isa)),
+           "lb_w4a8_group_acc")
+    return out
+
+
+GEMMS = {"w4a16": gemm_w4a16, "mxfp4": gemm_mxfp4, "w4a8": gemm_w4a8}
+BLOCKS = {"w4a16": GROUP, "mxfp4": MXBLOCK, "w4a8": GROUP}

@@ -1,0 +1,117 @@
+"""The C-ABI library and its host logic (CPU; no kernel is launched).
+
+The library must load, export every function include/lowbit_hip.h declares,
+and reject bad shapes and tiles with the reference's return codes before it
+touches a device.
+"""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import lowbit_amd as lb
+from lowbit_amd import _build
+from lowbit_amd import kernels as K
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "lowbit_hip.h"
+
+
+def header_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(lbd?_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_reference_abi():
+    names = header_functions()
+    # the reference's exported API (src/lowbit/csrc/lowbit.h:95-123)
+    ref = {"lb_version", "lb_cpu_isa", "lb_active_isa", "lb_has_vnni", "lb_has_openmp",
+           "lb_max_threads", "lb_effective_isa", "lb_gemm_w4a16", "lb_gemm_mxfp4", "lb_gemm_w4a8",
+           "lb_gemm_w4a8_q", "lb_quant_act_int8", "lb_w4a8_group_acc"}
+    assert ref <= names
+
+
+def test_library_exports_every_declared_symbol():
+    so = _build.lib_path()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(so)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = header_functions() - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+    # and the ctypes layer binds exactly the declared set
+    assert set(K.SIGNATURES) == header_functions()
+
+
+def test_library_loads_and_binds():
+    L = K.lib()
+    for name in K.SIGNATURES:
+        assert hasattr(L, name)
+    assert L.lb_version() == 1
+    assert L.lb_has_vnni() == 0 and L.lb_max_threads() == 1
+
+
+def test_public_surface_matches_reference():
+    # src/lowbit/__init__.py:2-11
+    ref = {"GROUP", "MXBLOCK", "Int4Weights", "Int8Acts", "MXFP4Weights", "Params", "cpu_info",
+           "gemm_mxfp4", "gemm_w4a8", "gemm_w4a16", "quantize_act_int8", "quantize_int4",
+           "quantize_mxfp4"}
+    assert ref <= set(lb.__all__)
+    for name in ref:
+        assert hasattr(lb, name)
+    assert lb.GROUP == 128 and lb.MXBLOCK == 32
+
+
+def test_shape_errors_before_device(rng):
+    # rc -1 on M, N, Kp <= 0 or Kp % block (src/lowbit/csrc/dispatch.c:205-208): checked on the host
+    L = K.lib()
+    x = np.zeros((1, 128), np.float32)
+    qw = np.zeros((1, 64), np.uint8)
+    s = np.ones((1, 1), np.float32)
+    y = np.zeros((1, 1), np.float32)
+    assert L.lb_gemm_w4a16(x, 0, 128, qw, s, None, 1, y, None) == -1
+    assert L.lb_gemm_w4a16(x, 1, 100, qw, s, None, 1, y, None) == -1
+    assert L.lb_gemm_w4a8(x, 1, 128, qw, s, None, 0, y, None) == -1
+    assert L.lb_gemm_mxfp4(x, 1, 48, qw, np.zeros((1, 2), np.uint8), 1, y, None) == -1
+    assert "shape" in L.lb_last_error().decode()
+
+
+def test_bad_tile_rejected_like_reference(rng):
+    # Params(mr=3, nr=3) names no compiled micro-tile: ValueError (tests/test_kernels.py:176-181)
+    W = lb.quantize_int4(rng.standard_normal((8, 128)).astype(np.float32))
+    with pytest.raises(ValueError):
+        K.gemm_w4a16(np.ones((1, 128), np.float32), W, K.Params(mr=3, nr=3))
+    with pytest.raises(ValueError):
+        K.gemm_w4a8(np.ones((1, 128), np.float32), W, K.Params(mr=8, nr=4))
+    with pytest.raises(ValueError):
+        K.gemm_mxfp4(np.ones((1, 128), np.float32), lb.quantize_mxfp4(np.ones((2, 128), np.float32)),
+                     K.Params(mr=5))
+
+
+def test_params_and_isa_host_logic():
+    with pytest.raises(ValueError):
+        K._params("fastest", None, None, "w4a16", (1, 1, 1))
+    p = K._params("auto", "gfx950-mfma", 4, "w4a16", (1, 1, 1))
+    assert p.isa == K.ISA_GFX950_MFMA and p.nthreads == 4
+    assert K._isa_id("avx512") == -1 and K._isa_id(None) == -1 and K._isa_id("gfx950") == 16
+    with pytest.raises(ValueError):
+        K._isa_id("sse2")
+    assert K.Params(mr=4, nr=2).as_dict()["mr"] == 4
+    assert K.amx_available() is False
+
+
+def test_prepared_pads_and_reshapes():
+    pr = K._Prepared(np.arange(5, dtype=np.float64), 128, 3)
+    assert pr.x.shape == (1, 128) and pr.x.dtype == np.float32
+    assert pr.x[0, 4] == 4 and pr.x[0, 5:].sum() == 0
+    assert pr.y.shape == (1, 3)
+
+
+def test_no_device_reports_unavailable():
+    if Path("/dev/kfd").exists():
+        pytest.skip("a GPU is present")
+    L = K.lib()
+    assert L.lb_cpu_isa() == -4
+    assert K.cpu_info()["cpu_isa"] == "none"
