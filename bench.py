@@ -1,0 +1,384 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused dequantize+GEMM hot path on one MI355X.
+
+Metric: weight GB/s (and % of HBM peak) at M=1, N=11008, K=4096,
+and GFLOP/s at M=64, per format. The headline `value` is the W4A8 decode GEMV
+(int4 g128 asymmetric weights, int8 per-token activations quantized inside the
+call) with weights cold: every call reads a different copy from a pool of more
+than 2 x (256 MB Infinity Cache + 8 x 4 MB L2), so each call streams its
+weights from HBM (the cold rule of src/lowbit/bench.py:169-178, sized for the GPU).
+
+One step = one GEMM call on device-resident inputs. The timed launches are
+captured in a HIP graph and replayed, so host launch overhead is not counted;
+HIP events on the launch stream bracket the timed region (after W warm-up
+steps and a device synchronisation on both sides). The metric definitions
+follow src/lowbit/bench.py:213-214: weight GB/s = packed weight bytes / time,
+GFLOP/s = 2*M*N*K / time with the logical K.
+
+The CPU baseline times the reference's own C library (oracle/_ref, built from
+the reference sources) on this host's cores on a bounded sample of the same
+workload; it is a reported baseline only.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, published (POP/s -> TOP/s here)
+FP32_PEAK_TFLOPS = 157.3     # dense fp32 matrix, published
+COLD_POOL_BYTES = 1280 << 20  # > 2 x (256 MB MALL + 32 MB L2)
+DECODE = (1, 11008, 4096)
+BATCH = (64, 11008, 4096)
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_w4a8_gemv_1x11008x4096.txt"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ device helpers
+
+class Dev:
+    """Thin wrapper over the library's device plumbing."""
+
+    def __init__(self):
+        from lowbit_amd import kernels as K
+        self.K = K
+        self.L = K.lib()
+        s = C.c_void_p()
+        self.check(self.L.lb_stream_create(C.byref(s)), "stream")
+        self.stream = s.value
+
+    def check(self, rc, what):
+        if rc < 0:
+            raise RuntimeError(f"{what}: rc={rc} {self.L.lb_last_error().decode()}")
+        return rc
+
+    def upload(self, a: np.ndarray):
+        return self.K.DeviceBuffer.from_array(a)
+
+    def event(self):
+        e = C.c_void_p()
+        self.check(self.L.lb_event_create(C.byref(e)), "event")
+        return e.value
+
+    def elapsed_ms(self, e0, e1) -> float:
+        ms = C.c_float()
+        self.check(self.L.lb_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+        return ms.value
+
+    def time_launches(self, launch, n_launch: int, warmup: int, graph: bool = True) -> float:
+        """ms per launch of `launch(i)` over n_launch launches (HIP events on the stream)."""
+        L = self.L
+        for i in range(warmup):
+            launch(i)
+        self.check(L.lb_stream_synchronize(self.stream), "sync")
+        e0, e1 = self.event(), self.event()
+        if graph:
+            self.check(L.lb_stream_begin_capture(self.stream), "begin capture")
+            for i in range(n_launch):
+                launch(i)
+            ex = C.c_void_p()
+            self.check(L.lb_stream_end_capture(self.stream, C.byref(ex)), "end capture")
+            self.check(L.lb_graph_launch(ex.value, self.stream), "graph warm-up")
+            self.check(L.lb_stream_synchronize(self.stream), "sync")
+            self.check(L.lb_dev_synchronize(), "sync")
+            self.check(L.lb_event_record(e0, self.stream), "record")
+            self.check(L.lb_graph_launch(ex.value, self.stream), "graph launch")
+            self.check(L.lb_event_record(e1, self.stream), "record")
+            self.check(L.lb_event_synchronize(e1), "sync")
+            L.lb_graph_destroy(ex.value)
+        else:
+            self.check(L.lb_dev_synchronize(), "sync")
+            self.check(L.lb_event_record(e0, self.stream), "record")
+            for i in range(n_launch):
+                launch(i)
+            self.check(L.lb_event_record(e1, self.stream), "record")
+            self.check(L.lb_event_synchronize(e1), "sync")
+        self.check(L.lb_dev_synchronize(), "sync")
+        ms = self.elapsed_ms(e0, e1)
+        L.lb_event_destroy(e0)
+        L.lb_event_destroy(e1)
+        return ms / n_launch
+
+
+def weight_pool(dev: Dev, arrays: list[np.ndarray], nbytes: int, cold: bool):
+    """Device copies of the packed weight arrays; > COLD_POOL_BYTES in total when cold."""
+    copies = max(1, math.ceil(COLD_POOL_BYTES / nbytes)) if cold else 1
+    first = [dev.upload(a) for a in arrays]
+    pool = [first]
+    for _ in range(copies - 1):
+        cp = []
+        for a, src in zip(arrays, first):
+            b = dev.K.DeviceBuffer(a.nbytes)
+            dev.check(dev.L.lb_memcpy_d2d(b.ptr, src.ptr, a.nbytes), "d2d")
+            cp.append(b)
+        pool.append(cp)
+    return pool
+
+
+# ------------------------------------------------------------------ one GPU measurement
+
+def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int, warmup: int,
+            graph: bool = True) -> dict:
+    from lowbit_amd import formats as F
+    K = dev.K
+    L = dev.L
+    m, n, k = shape
+    xp = F.pad_acts(x, W.kp)
+    if fmt == "mxfp4":
+        arrays = [W.qw, W.e8m0]
+    else:
+        arrays = [W.qw, W.scales] + ([W.zeros] if W.zeros is not None else [])
+    pool = weight_pool(dev, arrays, W.nbytes, cold)
+    dx = dev.upload(xp)
+    dy = K.DeviceBuffer(m * n * 4)
+    prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
+    ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp)
+    ws = K.DeviceBuffer(ws_bytes)
+    s = dev.stream
+
+    def launch(i):
+        b = pool[i % len(pool)]
+        if fmt == "w4a16":
+            rc = L.lbd_gemm_w4a16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None,
+                                  n, dy.ptr, C.byref(prm), s)
+        elif fmt == "mxfp4":
+            rc = L.lbd_gemm_mxfp4(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, n, dy.ptr, C.byref(prm), s)
+        else:
+            rc = L.lbd_gemm_w4a8(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None,
+                                 n, dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
+        dev.check(rc, f"lbd_gemm_{fmt}")
+        return rc
+
+    path = launch(0)
+    dev.check(L.lb_stream_synchronize(s), "sync")
+    y = dy.to_array((m, n), np.float32)
+    ms = dev.time_launches(launch, steps, warmup, graph=graph)
+    t = ms * 1e-3
+    return {
+        "format": fmt, "M": m, "N": n, "K": k, "cache": "cold" if cold else "hot",
+        "path": K.ISA_NAMES.get(path, "?"), "pool_copies": len(pool),
+        "us_per_call": round(ms * 1e3, 3), "weight_bytes": int(W.nbytes),
+        "weight_gbps": round(W.nbytes / t / 1e9, 1),
+        "gflops": round(2.0 * m * n * k / t / 1e9, 1),
+        "y": y,
+    }
+
+
+def rel_err(fmt: str, W, x, y) -> float:
+    """max|y - ref| / max|ref| against the float64 C oracle (the reference's bench check)."""
+    from lowbit_amd import formats as F
+    from oracle import cref
+    xp = F.pad_acts(x, W.kp)
+    if fmt == "w4a16":
+        ref = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros)
+    elif fmt == "mxfp4":
+        ref = cref.c_gemm_mxfp4(xp, W.qw, W.e8m0)
+    else:
+        a = F.quantize_act_int8(xp)
+        ref, _ = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+    return float(np.max(np.abs(y - ref)) / (np.max(np.abs(ref)) + 1e-30))
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def host_llc_bytes() -> int:
+    best = 0
+    for idx in Path("/sys/devices/system/cpu/cpu0/cache").glob("index*"):
+        try:
+            txt = (idx / "size").read_text().strip()
+        except OSError:
+            continue
+        mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(txt[-1], 1)
+        best = max(best, (int(txt[:-1]) if txt[-1] in "KMG" else int(txt)) * mult)
+    return best or 32 << 20
+
+
+def cpu_model() -> str:
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(W, x: np.ndarray, budget_s: float) -> dict | None:
+    """lb_gemm_w4a8 of the reference's C library at M=1 11008x4096, weights rotated past
+    2x the host LLC, median of >= 3 reps after a warm-up (src/lowbit/bench.py:116-124)."""
+    from dataclasses import replace
+
+    from lowbit_amd import formats as F
+    from oracle import cref
+    L = cref.ref_lib()
+    if L is None:
+        return None
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    llc = host_llc_bytes()
+    copies = min(max(1, math.ceil(max(2 * llc, 512 << 20) / W.nbytes)), max(1, (3 << 30) // W.nbytes))
+    pool = [W] + [replace(W, qw=W.qw.copy(), scales=W.scales.copy(),
+                          zeros=None if W.zeros is None else W.zeros.copy()) for _ in range(copies - 1)]
+    xp = F.pad_acts(x, W.kp)
+    y = np.empty((x.shape[0], W.n), np.float32)
+    res = {}
+    for nt in sorted({1, threads}):
+        p = cref.RefParams(-1, 0, 0, 0, 0, 0, nt)
+        isa = L.lb_effective_isa(2, -1)
+
+        def call(i):
+            w = pool[i % len(pool)]
+            rc = L.lb_gemm_w4a8(xp, xp.shape[0], w.kp, w.qw, w.scales, cref.zp(w.zeros), w.n, y, C.byref(p))
+            assert rc >= 0, rc
+
+        call(0)
+        ts, i, t_end = [], 1, time.perf_counter() + budget_s / 2
+        while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 2000):
+            t0 = time.perf_counter()
+            call(i)
+            ts.append(time.perf_counter() - t0)
+            i += 1
+        med = float(np.median(ts))
+        res[nt] = {"s": med, "reps": len(ts), "isa": {0: "scalar", 1: "avx2", 2: "avx512-vnni"}.get(isa, isa)}
+    nt = threads
+    return {
+        "value": round(W.nbytes / res[nt]["s"] / 1e9, 2),
+        "unit": "weight GB/s",
+        "cores": nt,
+        "kind": "reference",
+        "sample": (f"reference C lb_gemm_w4a8 (oracle/_ref, {res[nt]['isa']} path), M=1 N={W.n} K={W.k} "
+                   f"int4 g128 asym, {copies} rotating weight copies (> 2x {llc >> 20} MiB LLC), "
+                   f"median of {res[nt]['reps']} calls: {res[nt]['s'] * 1e6:.0f} us at {nt} threads, "
+                   f"{res[1]['s'] * 1e6:.0f} us at 1 thread ({W.nbytes / res[1]['s'] / 1e9:.2f} GB/s); "
+                   f"host {cpu_model()}"),
+    }
+
+
+def traffic_bytes() -> int | None:
+    """HBM bytes per launch of the headline kernel, from the committed counter summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for ln in TRAFFIC_FILE.read_text().splitlines():
+        if ln.startswith("traffic_bytes_per_launch:"):
+            return int(float(ln.split(":", 1)[1]))
+    return None
+
+
+# ------------------------------------------------------------------ main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline time budget")
+    ap.add_argument("--no-graph", action="store_true", help="time plain launches instead of a graph replay")
+    ap.add_argument("--only-headline", action="store_true", help="measure only the headline W4A8 decode")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the hot path has no "
+              "multi-GPU part in this build; run with --gpus 1.", file=sys.stderr)
+        return 2
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py is single-process, single-GPU", file=sys.stderr)
+        return 2
+
+    import lowbit_amd as lb
+
+    dev = Dev()
+    info = dev.K.cpu_info()
+    log(f"device {info.get('arch')} with {info.get('compute_units')} CUs")
+    rng = np.random.default_rng(0)
+    results = {}
+    graph = not args.no_graph
+
+    # decode: all three formats at 1 x 11008 x 4096, cold
+    m, n, k = DECODE
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w4 = lb.quantize_int4(w, asym=True)
+    mx = lb.quantize_mxfp4(w)
+    order = ["w4a8"] if args.only_headline else ["w4a8", "w4a16", "mxfp4"]
+    for fmt in order:
+        W = mx if fmt == "mxfp4" else w4
+        r = measure(dev, fmt, DECODE, W, x, cold=True, steps=args.steps, warmup=args.warmup, graph=graph)
+        r["max_rel_err"] = float(f"{rel_err(fmt, W, x, r.pop('y')):.3g}")
+        r["hbm_frac"] = round(r["weight_gbps"] / HBM_PEAK_GBS, 4)
+        results[f"{fmt}_decode"] = r
+        log(f"{fmt:6s} M=1 cold: {r['us_per_call']:8.2f} us  {r['weight_gbps']:7.1f} GB/s "
+            f"({100 * r['hbm_frac']:.1f}% HBM)  path {r['path']}  rel err {r['max_rel_err']}")
+
+    # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167)
+    if not args.only_headline:
+        mb, nb, kb = BATCH
+        xb = rng.standard_normal((mb, kb)).astype(np.float32)
+        for fmt in ["w4a8", "w4a16", "mxfp4"]:
+            W = mx if fmt == "mxfp4" else w4
+            r = measure(dev, fmt, BATCH, W, xb, cold=False, steps=max(20, args.steps // 4),
+                        warmup=max(2, args.warmup // 4), graph=graph)
+            r["max_rel_err"] = float(f"{rel_err(fmt, W, xb, r.pop('y')):.3g}")
+            peak = INT8_PEAK_TOPS if fmt == "w4a8" else FP32_PEAK_TFLOPS
+            r["mfma_frac"] = round(r["gflops"] / 1e3 / peak, 4)
+            results[f"{fmt}_m64"] = r
+            log(f"{fmt:6s} M=64 hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
+                f"({100 * r['mfma_frac']:.1f}% of {'int8' if fmt == 'w4a8' else 'fp32'} peak)  path {r['path']}")
+
+    head = results["w4a8_decode"]
+    t_launch_s = head["us_per_call"] * 1e-6
+    # algorithmic bytes of one launch: packed weights + fp32 X + fp32 Y
+    algo_bytes = head["weight_bytes"] + 4 * k * m + 4 * n * m
+    achieved = algo_bytes / t_launch_s / 1e9
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(w4, x, args.cpu_seconds)
+        except Exception as e:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {e}")
+    line = {
+        "metric": "weight GB/s (%HBM peak) at 1x11008x4096; GFLOP/s at M=64, per format",
+        "value": head["weight_gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] * 1e-3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "W4A8 decode GEMV, M=1 N=11008 K=4096, int4 g128 asym weights, int8 "
+                               "per-token activations quantized in-call, cold (weights rotated over "
+                               f"{head['pool_copies']} HBM copies), HIP-graph replay",
+                   "M": m, "N": n, "K": k, "format": "w4a8", "cache": "cold", "parallelism": "single GPU",
+                   "timing": "graph" if graph else "launch"},
+        "hbm_frac": head["hbm_frac"],
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
+                     "algorithmic_bytes": int(algo_bytes)},
+        "cpu_baseline": cpu,
+        "per_format": {kk: {f: v for f, v in vv.items() if f not in ("N", "K")} for kk, vv in results.items()},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

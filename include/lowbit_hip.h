@@ -171,6 +171,14 @@ int lb_event_destroy(void *event);
 int lb_event_record(void *event, void *stream);
 int lb_event_synchronize(void *event);
 int lb_event_elapsed_ms(void *start, void *stop, float *ms);
+/* HIP graph capture of launch-bound loops: everything enqueued on `stream` between
+ * begin and end becomes one graph, replayed by lb_graph_launch without per-kernel
+ * host overhead. Entry points that allocate (lbd_gemm_w4a8 without a workspace
+ * on first use) must not be captured. */
+int lb_stream_begin_capture(void *stream);
+int lb_stream_end_capture(void *stream, void **graph_exec);
+int lb_graph_launch(void *graph_exec, void *stream);
+int lb_graph_destroy(void *graph_exec);
 /* plain streaming copy kernel of `bytes` (multiple of 16) on `stream`: the known-size
  * reference for scaling HBM traffic counters */
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);

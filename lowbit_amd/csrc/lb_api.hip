@@ -672,6 +672,31 @@ int lb_event_elapsed_ms(void *start, void *stop, float *ms) {
          "hipEventElapsedTime");
   return ok(0);
 }
+int lb_stream_begin_capture(void *stream) {
+  LB_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
+         "hipStreamBeginCapture");
+  return ok(0);
+}
+int lb_stream_end_capture(void *stream, void **graph_exec) {
+  if (!graph_exec) return fail(LB_ERR_ARG, "null pointer");
+  hipGraph_t g = nullptr;
+  LB_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g), "hipStreamEndCapture");
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+  *graph_exec = ex;
+  return ok(0);
+}
+int lb_graph_launch(void *graph_exec, void *stream) {
+  LB_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), static_cast<hipStream_t>(stream)),
+         "hipGraphLaunch");
+  return ok(0);
+}
+int lb_graph_destroy(void *graph_exec) {
+  LB_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+  return ok(0);
+}
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {
   if (!dst || !src || bytes % 16 || !aligned16(dst) || !aligned16(src))
     return fail(LB_ERR_ARG, "copy needs 16-byte aligned pointers and a multiple of 16 bytes");

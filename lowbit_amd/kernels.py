@@ -107,6 +107,10 @@ SIGNATURES = {
     "lb_event_record": ([_vp, _vp], _int),
     "lb_event_synchronize": ([_vp], _int),
     "lb_event_elapsed_ms": ([_vp, _vp, C.POINTER(C.c_float)], _int),
+    "lb_stream_begin_capture": ([_vp], _int),
+    "lb_stream_end_capture": ([_vp, C.POINTER(_vp)], _int),
+    "lb_graph_launch": ([_vp, _vp], _int),
+    "lb_graph_destroy": ([_vp], _int),
     "lbd_copy_kernel": ([_vp, _vp, _sz, _vp], _int),
 }
 
