@@ -683,7 +683,7 @@ int lb_stream_end_capture(void *stream, void **graph_exec) {
   LB_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g), "hipStreamEndCapture");
   hipGraphExec_t ex = nullptr;
   hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  (void)hipGraphDestroy(g);
   if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
   *graph_exec = ex;
   return ok(0);

@@ -12,25 +12,99 @@ constexpr int kGroup = 128;    // int4 group (elements)
 constexpr int kMxBlock = 32;   // MXFP4 block (elements)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
+// ---------------------------------------------------------------- reductions
+//
+// Cross-lane steps use DPP (data-parallel primitives: a VALU operand read from
+// another lane) instead of LDS permutes, so each step costs one VALU op:
+//   quad_perm [1,0,3,2], [2,3,0,1]  -> every lane holds its quad's total
+//   row_half_mirror, row_mirror     -> every lane holds its 16-lane row's total
+//   row_bcast:15 (rows 1, 3)        -> rows 1 / 3 hold rows 0+1 / 2+3
+//   row_bcast:31 (rows 2, 3)        -> row 3 holds the wave total
+// Rows excluded by the row mask add the identity (`old` operand).
+constexpr int kDppQuad1032 = 0xB1, kDppQuad2301 = 0x4E, kDppRowHalfMirror = 0x141,
+              kDppRowMirror = 0x140, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float v, float identity) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_i(int v, int identity) {
+  return __builtin_amdgcn_update_dpp(identity, v, CTRL, ROWS, 0xF, false);
+}
+
+// Sum over the wave; every lane gets the total (read back from lane 63).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v += dpp_f<kDppQuad1032>(v, 0.0f);
+  v += dpp_f<kDppQuad2301>(v, 0.0f);
+  v += dpp_f<kDppRowHalfMirror>(v, 0.0f);
+  v += dpp_f<kDppRowMirror>(v, 0.0f);
+  v += dpp_f<kDppRowBcast15, 0xA>(v, 0.0f);
+  v += dpp_f<kDppRowBcast31, 0xC>(v, 0.0f);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Max over the wave (NaN never wins, as with fmaxf); every lane gets it.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  v = fmaxf(v, dpp_f<kDppQuad1032>(v, v));
+  v = fmaxf(v, dpp_f<kDppQuad2301>(v, v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v, v));
+  v = fmaxf(v, dpp_f<kDppRowMirror>(v, v));
+  v = fmaxf(v, dpp_f<kDppRowBcast15, 0xA>(v, v));
+  v = fmaxf(v, dpp_f<kDppRowBcast31, 0xC>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over each 32-lane half of the wave; the totals land in lanes 31 and 63
+// (other lanes hold partial sums).
+__device__ __forceinline__ int half_wave_sum(int v) {
+  v += dpp_i<kDppQuad1032>(v, 0);
+  v += dpp_i<kDppQuad2301>(v, 0);
+  v += dpp_i<kDppRowHalfMirror>(v, 0);
+  v += dpp_i<kDppRowMirror>(v, 0);
+  v += dpp_i<kDppRowBcast15, 0xA>(v, 0);
   return v;
 }
 
-// Sum over each 32-lane half of the wave (the xor offsets never cross lane 32).
-__device__ __forceinline__ int half_wave_sum(int v) {
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off);
+// ---------------------------------------------------------------- buffer loads
+//
+// Raw buffer loads through a resource descriptor (base, byte count): offsets at
+// or past the byte count read 0 in hardware, so a descriptor per weight row
+// makes row and chunk tails free of clamps and selects. Offsets are 32-bit
+// (rows and activation vectors are far below 4 GiB). The third descriptor word
+// 0x00020000 is the raw-buffer format word of the gfx9 family.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld_b128(Rsrc r, uint32_t off) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ld_f4(Rsrc r, uint32_t off) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ float ld_f32(Rsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld_u32(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t ld_u8(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+
+// Hides a value from the optimizer (no instruction is emitted), so that a mask
+// is not folded into later byte extractions: (m >> 8k) & 0xFF of an opaque m
+// becomes one v_cvt_f32_ubyte<k> instead of a bitfield extract plus a convert.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
   return v;
 }
 
@@ -71,10 +145,34 @@ __device__ __forceinline__ int8_t quant_one(float v, float sc) {
   return (int8_t)(int)q;
 }
 
+// rint(fl(v / sc)) without a division on the common path. inv = fl(1 / sc) and
+// t = fl(v * inv) differ from v / sc by at most |v/sc| * (2^-24 + 2^-24 + 2^-48)
+// < 2^-16 (|v/sc| <= 127 * (1 + 2^-23) because |v| <= amax and sc = fl(amax/127)),
+// and fl(v / sc) differs from v / sc by at most 2^-17, so |t - fl(v/sc)| < 2^-15.
+// Unless t lies within 2^-15 of a half-integer, t and fl(v / sc) therefore round
+// to the same integer (and fl(v / sc) cannot itself be a tie). |t - rint(t)| and
+// its distance to 0.5 are exact in float32 (|t| < 256). Near-ties, NaN and an
+// overflowed inv (sc < 2^-126) take the IEEE division.
+__device__ __forceinline__ int8_t quant_one_fast(float v, float sc, float inv) {
+  const float t = v * inv;
+  float q = rintf(t);
+  if (!(fabsf(fabsf(t - q) - 0.5f) > 0x1p-15f)) q = rintf(v / sc);
+  q = q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q);
+  return (int8_t)(int)q;
+}
+
 // Four consecutive elements -> packed int8x4 and their integer sum.
 __device__ __forceinline__ uint32_t quant4(float4 v, float sc, int &sum) {
   const int8_t a = quant_one(v.x, sc), b = quant_one(v.y, sc);
   const int8_t c = quant_one(v.z, sc), d = quant_one(v.w, sc);
+  sum = (int)a + (int)b + (int)c + (int)d;
+  return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
+         ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
+}
+
+__device__ __forceinline__ uint32_t quant4_fast(float4 v, float sc, float inv, int &sum) {
+  const int8_t a = quant_one_fast(v.x, sc, inv), b = quant_one_fast(v.y, sc, inv);
+  const int8_t c = quant_one_fast(v.z, sc, inv), d = quant_one_fast(v.w, sc, inv);
   sum = (int)a + (int)b + (int)c + (int)d;
   return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
          ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
