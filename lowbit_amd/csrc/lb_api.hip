@@ -220,7 +220,7 @@ int run_mxfp4(const lbk::GemmArgs &a, const lb_params *p, hipStream_t s) {
 }
 
 size_t w4a8_ws_bytes(int M, int Kp) {
-  return align256((size_t)M * Kp) + align256((size_t)M * 4) + align256((size_t)M * (Kp / LB_GROUP) * 4);
+  return align256(lbk::tiled_xq_bytes(M, Kp)) + align256((size_t)M * 4) + align256(lbk::tiled_asum_bytes(M, Kp));
 }
 
 // fp32 activations in; quantized inside (fused into the GEMV, or a quantizer
@@ -236,15 +236,18 @@ int run_w4a8(const lbk::GemmArgs &a, const lb_params *p, char *ws, hipStream_t s
     return ok(path);
   }
   lbk::GemmArgs q = a;
+  // quantized activations in the tiled layout the MFMA kernel reads
+  const size_t xq_bytes = align256(lbk::tiled_xq_bytes(a.M, a.Kp));
   int8_t *xq = reinterpret_cast<int8_t *>(ws);
-  float *xs = reinterpret_cast<float *>(ws + align256((size_t)a.M * a.Kp));
-  int32_t *asum = reinterpret_cast<int32_t *>(ws + align256((size_t)a.M * a.Kp) + align256((size_t)a.M * 4));
-  hipError_t e = lbk::launch_quant(a.x, a.M, a.Kp, xq, xs, asum, s);
+  float *xs = reinterpret_cast<float *>(ws + xq_bytes);
+  int32_t *asum = reinterpret_cast<int32_t *>(ws + xq_bytes + align256((size_t)a.M * 4));
+  hipError_t e = lbk::launch_quant(a.x, a.M, a.Kp, xq, xs, asum, true, s);
   if (e != hipSuccess) return fail_hip(e, "quantizer launch");
   q.xq = xq;
   q.xs = xs;
   q.asum = asum;
-  e = lbk::launch_w4a8_mfma(q, nullptr, s);
+  q.tiled = true;
+  e = lbk::launch_w4a8_mfma(q, nullptr, cus, s);
   if (e != hipSuccess) return fail_hip(e, "W4A8 MFMA launch");
   return ok(path);
 }
@@ -255,7 +258,7 @@ int run_w4a8_q(const lbk::GemmArgs &a, const lb_params *p, hipStream_t s) {
   if (device_info(&di) == 0) cus = di.cus;
   const int path = choose_path(lbk::F_W4A8Q, a.M, a.Kp, p);
   hipError_t e = path == LB_ISA_GFX950 ? lbk::launch_gemv(lbk::F_W4A8Q, a, cus, s)
-                                       : lbk::launch_w4a8_mfma(a, nullptr, s);
+                                       : lbk::launch_w4a8_mfma(a, nullptr, cus, s);
   if (e != hipSuccess) return fail_hip(e, "W4A8 kernel launch");
   return ok(path);
 }
@@ -273,7 +276,10 @@ int run_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, const ui
     a.M = M;
     a.Kp = Kp;
     a.N = N;
-    e = lbk::launch_w4a8_mfma(a, out, s);
+    int cus = 0;
+    DevInfo di;
+    if (device_info(&di) == 0) cus = di.cus;
+    e = lbk::launch_w4a8_mfma(a, out, cus, s);
     path = LB_ISA_GFX950_MFMA;
   } else {
     e = lbk::launch_groupacc_dot4(xq, asum, M, Kp, qw, zeros, N, out, s);
@@ -408,7 +414,7 @@ int lbd_quant_act_int8(const float *x, int M, int Kp, int8_t *xq, float *xs, int
   if (M <= 0 || Kp <= 0 || Kp % LB_GROUP) return fail(LB_ERR_SHAPE, "bad shape");
   if (!x || !xq || !xs || !asum) return fail(LB_ERR_ARG, "null pointer");
   if (!aligned16(x) || !aligned16(xq)) return fail(LB_ERR_ARG, "x and xq must be 16-byte aligned");
-  hipError_t e = lbk::launch_quant(x, M, Kp, xq, xs, asum, static_cast<hipStream_t>(stream));
+  hipError_t e = lbk::launch_quant(x, M, Kp, xq, xs, asum, false, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail_hip(e, "quantizer launch");
   return ok(0);
 }

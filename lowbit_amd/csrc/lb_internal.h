@@ -22,6 +22,7 @@ struct GemmArgs {
   const uint8_t *e8m0 = nullptr;  // [N, Kp/32]
   float *y = nullptr;             // [M, N]
   int M = 0, Kp = 0, N = 0;
+  bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
 };
 
 // Small-M VALU kernels: largest M they take and the LDS they need.
@@ -31,11 +32,16 @@ size_t gemv_lds_bytes(int fmt, int M, int Kp);
 bool gemv_eligible(int fmt, int M, int Kp);
 
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
-hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs,
-                        int32_t *asum, hipStream_t s);
-// int8 MFMA W4A8 on quantized activations; with `out` non-null it writes the exact
-// int32 group accumulators [M, N, G] instead of Y.
-hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, hipStream_t s);
+// Per-token int8 quantizer: xq, xs, asum as lb_quant_act_int8, or (tiled) xq and asum
+// in the MFMA path's tiled layout over ceil(M/16)*16 rows, padding rows zero.
+hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum, bool tiled,
+                        hipStream_t s);
+// Bytes of the tiled xq / asum for M rows.
+inline size_t tiled_xq_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * 16 * Kp; }
+inline size_t tiled_asum_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * 16 * (Kp / 128) * 4; }
+// int8 MFMA W4A8 on quantized activations; with `out` non-null it writes the
+// exact int32 group accumulators [M, N, G] instead of Y.
+hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, int num_cus, hipStream_t s);
 // fp32 MFMA W4A16 / MXFP4.
 hipError_t launch_f32_mfma(int fmt, const GemmArgs &a, hipStream_t s);
 // exact int32 group accumulators through the VALU dot4 arithmetic of the GEMV.

@@ -34,23 +34,89 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
 // ============================================================ per-token quantizer
-
+//
+// Tiled int8 activation layout (internal to the W4A8 MFMA path): rows in blocks of
+// 16, each (row block, group, half) a 1 KiB tile holding the 16-byte MFMA operand
+// of every lane in lane order, so that the GEMM reads each operand with one fully
+// contiguous 1 KiB wave load. Element e of row m (group g = e / 128, r = e % 128,
+// half h = r / 64, lane group q = (r % 64) / 16) sits at byte
+//   (((m / 16 * G + g) * 2 + h) * 64 + 16 q + m % 16) * 16 + r % 16.
+// The group sums of the tiled path are stored [m / 16][g][m % 16].
+__device__ __forceinline__ uint32_t w4a8_tiled_offset(int m, int e, int G) {
+  const int g = e >> 7, r = e & 127;
+  return (uint32_t)((((((m >> 4) * G + g) * 2 + (r >> 6)) * 64 + ((r >> 4) & 3) * 16 + (m & 15)) * 16) + (r & 15));
+}
+//
+// One workgroup per activation row. With NR > 0 the row (at most NR * 1024
+// elements) is loaded into registers by NR unconditional 16-byte loads per thread
+// (offsets past the row read 0), so all loads are in flight together; NR == 0
+// streams longer rows twice. The absmax is reduced across the workgroup and each
+// thread quantizes its 4-element slots with the exact fast path; group sums land
+// in asum.
+template <int NR, bool TILED>
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(
-    const float *__restrict__ x, int Kp, int8_t *__restrict__ xq,
-    float *__restrict__ xs, int32_t *__restrict__ asum) {
+    const float *__restrict__ x, int M, int Kp, int8_t *__restrict__ xq, float *__restrict__ xs,
+    int32_t *__restrict__ asum) {
   __shared__ float red[kWaves];
   const int m = blockIdx.x;
-  const float *xr = x + (size_t)m * Kp;
-  const float sc = row_scale(block_row_amax<kThreads>(xr, Kp, red));
-  if (threadIdx.x == 0) xs[m] = sc;
   const int G = Kp / kGroup;
-  uint32_t *qr = reinterpret_cast<uint32_t *>(xq + (size_t)m * Kp);
-  // Thread t handles 4 elements; a group of 128 is one 32-lane half-wave.
-  for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+  if (TILED && m >= M) {
+    // padding rows of the last 16-row block: zero codes and sums
+    for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4)
+      *reinterpret_cast<uint32_t *>(xq + w4a8_tiled_offset(m, e, G)) = 0u;
+    for (int g = threadIdx.x; g < G; g += kThreads) asum[((m >> 4) * G + g) * 16 + (m & 15)] = 0;
+    return;
+  }
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const Rsrc rx = make_rsrc(x + (size_t)m * Kp, (uint32_t)Kp * 4);
+  float4 v[NR > 0 ? NR : 1];
+  float amax = 0.0f;
+  if constexpr (NR > 0) {
+#pragma unroll
+    for (int i = 0; i < NR; i++) v[i] = ld_f4(rx, (threadIdx.x + i * kThreads) * 16);
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      amax = fmaxf(fmaxf(amax, fabsf(v[i].x)), fabsf(v[i].y));
+      amax = fmaxf(fmaxf(amax, fabsf(v[i].z)), fabsf(v[i].w));
+    }
+  } else {
+    for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) {
+      const float4 t = ld_f4(rx, e * 4);
+      amax = fmaxf(fmaxf(amax, fabsf(t.x)), fabsf(t.y));
+      amax = fmaxf(fmaxf(amax, fabsf(t.z)), fabsf(t.w));
+    }
+  }
+  amax = wave_max(amax);
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  float rmax = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) rmax = fmaxf(rmax, red[w]);
+  const float sc = row_scale(rmax);
+  const float inv = 1.0f / sc;
+  if (threadIdx.x == 0) xs[m] = sc;
+  // thread t handles 4 elements per slot; a group of 128 is one 32-lane half-wave
+  // (Kp % 128 == 0, so half-waves enter and leave a slot together)
+  auto emit = [&](float4 t, int e) {
     int s4;
-    qr[e >> 2] = quant4(*reinterpret_cast<const float4 *>(xr + e), sc, s4);
+    const uint32_t qv = quant4_fast(t, sc, inv, s4);
     const int gs = half_wave_sum(s4);
-    if ((threadIdx.x & 31) == 31) asum[(size_t)m * G + (e >> 7)] = gs;
+    if constexpr (TILED) {
+      *reinterpret_cast<uint32_t *>(xq + w4a8_tiled_offset(m, e, G)) = qv;
+      if ((threadIdx.x & 31) == 31) asum[((m >> 4) * G + (e >> 7)) * 16 + (m & 15)] = gs;
+    } else {
+      reinterpret_cast<uint32_t *>(xq + (size_t)m * Kp)[e >> 2] = qv;
+      if ((threadIdx.x & 31) == 31) asum[(size_t)m * G + (e >> 7)] = gs;
+    }
+  };
+  if constexpr (NR > 0) {
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const int e = threadIdx.x * 4 + i * kThreads * 4;
+      if (e < Kp) emit(v[i], e);
+    }
+  } else {
+    for (int e = threadIdx.x * 4; e < Kp; e += kThreads * 4) emit(ld_f4(rx, e * 4), e);
   }
 }
 
@@ -497,132 +563,313 @@ hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs,
-                        int32_t *asum, hipStream_t s) {
-  hipLaunchKernelGGL(quant_rows_kernel, dim3(M), dim3(kThreads), 0, s, x, Kp, xq, xs, asum);
+template <bool TILED>
+static void launch_quant_t(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum, hipStream_t s) {
+  const int n4 = (Kp + kThreads * 4 - 1) / (kThreads * 4);  // 16-byte slots per thread
+  const dim3 grid(TILED ? (M + 15) / 16 * 16 : M), block(kThreads);
+  if (n4 <= 1)
+    hipLaunchKernelGGL((quant_rows_kernel<1, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+  else if (n4 <= 2)
+    hipLaunchKernelGGL((quant_rows_kernel<2, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+  else if (n4 <= 4)
+    hipLaunchKernelGGL((quant_rows_kernel<4, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+  else if (n4 <= 8)
+    hipLaunchKernelGGL((quant_rows_kernel<8, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+  else if (n4 <= 16)
+    hipLaunchKernelGGL((quant_rows_kernel<16, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+  else
+    hipLaunchKernelGGL((quant_rows_kernel<0, TILED>), grid, block, 0, s, x, M, Kp, xq, xs, asum);
+}
+
+hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum, bool tiled,
+                        hipStream_t s) {
+  if (tiled)
+    launch_quant_t<true>(x, M, Kp, xq, xs, asum, s);
+  else
+    launch_quant_t<false>(x, M, Kp, xq, xs, asum, s);
   return hipGetLastError();
 }
 
 // ============================================================ W4A8, int8 MFMA
 //
-// Workgroup tile: (16*TM) activation rows x (16*TN) weight rows; the four waves
-// split the groups of K (wave w takes groups w, w+4, ...) and their fp32
-// partial tiles are summed through LDS at the end (a fixed order, so results
-// are deterministic).
+// Persistent workgroups of kW8Waves waves. A workgroup owns a contiguous range of
+// 16-row weight subtiles and a block of 16*TM activation rows; its waves split
+// the K groups (wave w: kW8GW consecutive groups of each phase of
+// kW8Waves * kW8GW groups). Per phase each wave holds its activation slice in
+// registers (2 * TM * kW8GW 16-byte operands), so the activations are read
+// once per workgroup while the weights stream past:
+//   for each subtile (weights prefetched one subtile ahead):
+//     two v_mfma_i32_16x16x64_i8 per (row block, group) on the raw codes,
+//     acc - z * asum  = the exact int32 group accumulator,
+//     fp32 rescale by the group scale,
+//   then the waves' partial tiles are summed in LDS in a fixed order (wave 0..7,
+//   phase 0..) and scaled by the per-token scale: no atomics, so results do
+//   not depend on scheduling.
+// With more than one phase (K > kW8Waves * kW8GW * 128) the per-subtile sums of
+// earlier phases wait in LDS; subtiles are then processed in passes of at most
+// kW8Pass so that this buffer stays bounded.
 //
-// Per group g, lane (q = l/16, c = l%16):
-//   B (weights, row n0+16j+c): 16 bytes at row offset 64g + 16q -> low nibbles are
-//     elements 128g+16q+[0,16), high nibbles 128g+64+16q+[0,16); each byte becomes
-//     the signed int8 (q - z).
-//   A (activations, row m0+16i+c): the int8 codes of those same elements.
-//   Two MFMAs (low half, high half) give the exact group total per tile element.
-template <int TM, int TN, bool EXPORT>
-__global__ __launch_bounds__(kThreads) void w4a8_mfma_kernel(GemmArgs a, int32_t *__restrict__ out) {
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int q = lane >> 4, c = lane & 15;
-  const int M = a.M, N = a.N, Kp = a.Kp, G = Kp / kGroup;
-  const size_t rowbytes = (size_t)(Kp >> 1);
-  const int n0 = blockIdx.x * 16 * TN, m0 = blockIdx.y * 16 * TM;
+// Operand slots: lane (q = l/16, c = l%16) feeds activation row 16i + c and
+// weight row n0 + c with bytes 64g + 16q .. +16 of the group's 64 bytes, i.e.
+// elements 128g + 16q + [0, 16) (low nibbles, first MFMA) and 128g + 64 + 16q +
+// [0, 16) (high nibbles, second MFMA).
 
-  int nrow[TN], mrow[TM];
-  bool nok[TN], mok[TM];
+constexpr int kW8Waves = 8;
+constexpr int kW8Threads = kW8Waves * kWave;
+constexpr int kW8GW = 4;                        // groups per wave per phase
+constexpr int kW8Phase = kW8Waves * kW8GW;      // groups per phase
+constexpr int kW8Pass = 8;                      // subtiles per pass (multi-phase only)
+
+// Weight bytes, scales and zero-points of one wave's groups for one weight row.
+// VEC (G % 4 == 0): the wave's four groups are 4-aligned, so their scales are one
+// 16-byte load and their zero-points one dword. Otherwise each group loads its
+// scale and the aligned dword holding its zero-point byte (the zero-point
+// descriptor is rounded up to whole dwords: the word holding the last byte lies in
+// the same page as that byte).
+struct W8Stage {
+  uint4 w[kW8GW];
+  float s[kW8GW];
+  uint32_t zw[kW8GW];
+};
+
+template <bool VEC>
+__device__ __forceinline__ void w8_load(W8Stage &st, Rsrc rw, Rsrc rs, Rsrc rz, int n, int N, int gb, int gcnt,
+                                        int G, uint32_t rowbytes, int q) {
 #pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const int n = n0 + 16 * j + c;
-    nok[j] = n < N;
-    nrow[j] = nok[j] ? n : N - 1;
+  for (int t = 0; t < kW8GW; t++) {
+    const bool ok = n < N && t < gcnt;
+    const uint32_t g = (uint32_t)(gb + t);
+    st.w[t] = ld_b128(rw, ok ? (uint32_t)n * rowbytes + g * 64u + (uint32_t)q * 16u : 0xFFFFFFF0u);
   }
+  const uint32_t gi0 = (uint32_t)n * (uint32_t)G + (uint32_t)gb;
+  if constexpr (VEC) {
+    const bool ok = n < N && gcnt > 0;
+    const float4 sv = ld_f4(rs, ok ? gi0 * 4u : 0xFFFFFFF0u);
+    st.s[0] = sv.x;
+    st.s[1] = sv.y;
+    st.s[2] = sv.z;
+    st.s[3] = sv.w;
+    st.zw[0] = ld_u32(rz, ok ? gi0 : 0xFFFFFFF0u);
+  } else {
 #pragma unroll
-  for (int i = 0; i < TM; i++) {
-    const int m = m0 + 16 * i + c;
-    mok[i] = m < M;
-    mrow[i] = mok[i] ? m : M - 1;
-  }
-
-  v4f facc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++) facc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const v4i zero4 = {0, 0, 0, 0};
-  for (int g = wave; g < G; g += kWaves) {
-    v4i blo[TN], bhi[TN];
-    float sc[TN];
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const uint4 w = *reinterpret_cast<const uint4 *>(a.qw + nrow[j] * rowbytes + (size_t)g * 64 + q * 16);
-      const uint32_t z = a.zeros ? a.zeros[(size_t)nrow[j] * G + g] : 8u;
-      const uint32_t zrep = z * 0x01010101u;
-      blo[j] = v4i{(int)sub_zero_bytes(lo_nibbles(w.x), zrep), (int)sub_zero_bytes(lo_nibbles(w.y), zrep),
-                   (int)sub_zero_bytes(lo_nibbles(w.z), zrep), (int)sub_zero_bytes(lo_nibbles(w.w), zrep)};
-      bhi[j] = v4i{(int)sub_zero_bytes(hi_nibbles(w.x), zrep), (int)sub_zero_bytes(hi_nibbles(w.y), zrep),
-                   (int)sub_zero_bytes(hi_nibbles(w.z), zrep), (int)sub_zero_bytes(hi_nibbles(w.w), zrep)};
-      if (!nok[j]) { blo[j] = zero4; bhi[j] = zero4; }
-      if constexpr (!EXPORT) sc[j] = a.scales[(size_t)nrow[j] * G + g];
+    for (int t = 0; t < kW8GW; t++) {
+      const bool ok = n < N && t < gcnt;
+      st.s[t] = ld_f32(rs, ok ? (gi0 + t) * 4u : 0xFFFFFFF0u);
+      st.zw[t] = ld_u32(rz, ok ? ((gi0 + t) & ~3u) : 0xFFFFFFF0u);
     }
-    v4i alo[TM], ahi[TM];
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ int w8_zero(const W8Stage &st, int t, int n, int G, int gb) {
+  if constexpr (VEC) return (int)((st.zw[0] >> (8 * t)) & 0xFFu);
+  const uint32_t gi = (uint32_t)n * (uint32_t)G + (uint32_t)(gb + t);
+  return (int)((st.zw[t] >> (8u * (gi & 3u))) & 0xFFu);
+}
+
+template <int TM, bool VEC, bool EXPORT>
+__device__ __forceinline__ void w8_compute(const W8Stage &st, const v4i (&xlo)[kW8GW][TM],
+                                           const v4i (&xhi)[kW8GW][TM], const int32_t *as_lds, int gl0,
+                                           int gcnt, int zadd, v4f (&facc)[TM], int q, int c, int m0,
+                                           int M, int n, int N, int G, int gb, int32_t *__restrict__ out) {
+  const v4i zero4 = {0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < kW8GW; t++) {
+    if (t >= gcnt) break;  // wave-uniform
+    const v4i blo = {(int)lo_nibbles(st.w[t].x), (int)lo_nibbles(st.w[t].y), (int)lo_nibbles(st.w[t].z),
+                     (int)lo_nibbles(st.w[t].w)};
+    const v4i bhi = {(int)hi_nibbles(st.w[t].x), (int)hi_nibbles(st.w[t].y), (int)hi_nibbles(st.w[t].z),
+                     (int)hi_nibbles(st.w[t].w)};
+    const int z = w8_zero<VEC>(st, t, n, G, gb) + zadd;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-      const int8_t *p = a.xq + (size_t)mrow[i] * Kp + (size_t)g * kGroup + q * 16;
-      alo[i] = *reinterpret_cast<const v4i *>(p);
-      ahi[i] = *reinterpret_cast<const v4i *>(p + 64);
-      if (!mok[i]) { alo[i] = zero4; ahi[i] = zero4; }
-    }
+      v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xlo[t][i], blo, zero4, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xhi[t][i], bhi, acc, 0, 0, 0);
+      const v4i as = *reinterpret_cast<const v4i *>(as_lds + (gl0 + t) * (16 * TM) + 16 * i + 4 * q);
 #pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[i], blo[j], zero4, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[i], bhi[j], acc, 0, 0, 0);
+      for (int r = 0; r < 4; r++) {
+        const int gacc = acc[r] - __mul24(z, as[r]);  // exact: |z * asum| < 2^18
         if constexpr (EXPORT) {
-          const int n = n0 + 16 * j + c;
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int m = m0 + 16 * i + 4 * q + r;
-            if (m < M && n < N) out[((size_t)m * N + n) * G + g] = acc[r];
-          }
+          const int m = m0 + 16 * i + 4 * q + r;
+          if (m < M && n < N) out[((size_t)m * N + n) * G + gb + t] = gacc;
         } else {
-#pragma unroll
-          for (int r = 0; r < 4; r++) facc[i][j][r] = __builtin_fmaf((float)acc[r], sc[j], facc[i][j][r]);
+          facc[i][r] = __builtin_fmaf((float)gacc, st.s[t], facc[i][r]);
         }
       }
-  }
-  if constexpr (!EXPORT) {
-    // cross-wave sum through LDS: red[w][idx][lane], then wave w finalises idx = w, w+4, ...
-    constexpr int NV = TM * TN * 4;
-    __shared__ float red[kWaves][NV][kWave];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) red[wave][(i * TN + j) * 4 + r][lane] = facc[i][j][r];
-    __syncthreads();
-    for (int idx = wave; idx < NV; idx += kWaves) {
-      const int i = idx / (TN * 4), j = (idx / 4) % TN, r = idx % 4;
-      const float t = (red[0][idx][lane] + red[1][idx][lane]) + (red[2][idx][lane] + red[3][idx][lane]);
-      const int m = m0 + 16 * i + 4 * q + r, n = n0 + 16 * j + c;
-      if (m < M && n < N) a.y[(size_t)m * N + n] = t * a.xs[m];
     }
   }
+}
+
+template <int TM, bool VEC, bool EXPORT, bool TILED>
+__global__ __launch_bounds__(kW8Threads) void w4a8_mfma_kernel(GemmArgs a, int32_t *__restrict__ out) {
+  constexpr int MB = 16 * TM;                         // activation rows per workgroup
+  __shared__ __align__(16) float red[2][kW8Waves][TM][kWave][4];
+  __shared__ __align__(16) int32_t as_lds[kW8Phase * MB];
+  __shared__ __align__(16) float acc_lds[kW8Pass * MB * 16];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int q = lane >> 4, c = lane & 15;
+  const int M = a.M, N = a.N, Kp = a.Kp, G = Kp / kGroup;
+  const uint32_t rowbytes = (uint32_t)(Kp >> 1);
+  const int m0 = blockIdx.y * MB;
+  const int S = (N + 15) / 16;
+  const int sb = (int)((long long)blockIdx.x * S / gridDim.x);
+  const int se = (int)((long long)(blockIdx.x + 1) * S / gridDim.x);
+  const int nph = (G + kW8Phase - 1) / kW8Phase;
+  const int zadd = a.zeros ? 0 : 8;
+
+  // row-major activations: this workgroup's rows, rows past M read 0.
+  // tiled activations (w4a8_tiled_offset): all row blocks, blocks past the last read 0.
+  const int mblocks = (M + 15) / 16;
+  const Rsrc rx = TILED ? make_rsrc(a.xq, (uint32_t)(mblocks * 16 * Kp))
+                        : make_rsrc(a.xq + (size_t)m0 * Kp, (uint32_t)(min(M - m0, MB) * Kp));
+  const Rsrc ra = TILED ? make_rsrc(a.asum, (uint32_t)(mblocks * G * 16 * 4))
+                        : make_rsrc(a.asum + (size_t)m0 * G, (uint32_t)(min(M - m0, MB) * G * 4));
+  const Rsrc rw = make_rsrc(a.qw, (uint32_t)min((size_t)N * rowbytes, (size_t)0xFFFFFFF0u));
+  const Rsrc rs = make_rsrc(a.scales, (uint32_t)((size_t)N * G * 4));
+  const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, a.zeros ? (uint32_t)(((size_t)N * G + 3) & ~(size_t)3) : 0u);
+
+  // reduction role: thread -> (lane rl of the wave tiles, row block ri, row pair rp);
+  // it sums two outputs of the 16*TM x 16 subtile over the waves
+  const bool red_thread = threadIdx.x < TM * 2 * kWave;
+  const int rl = threadIdx.x % kWave, ri = (threadIdx.x / kWave) >> 1, rp = (threadIdx.x / kWave) & 1;
+  const int lr = 16 * ri + 4 * (rl >> 4) + 2 * rp;  // local row of the first output
+  float xs0 = 0.f, xs1 = 0.f;
+  if constexpr (!EXPORT) {
+    // rows past M read 0 (their outputs are not stored)
+    const Rsrc rxs = make_rsrc(a.xs + m0, (uint32_t)(min(M - m0, MB) * 4));
+    xs0 = ld_f32(rxs, (uint32_t)lr * 4u);
+    xs1 = ld_f32(rxs, (uint32_t)(lr + 1) * 4u);
+  }
+
+  v4i xlo[kW8GW][TM], xhi[kW8GW][TM];
+  int buf = 0;
+  const int pass_len = nph == 1 ? (se - sb) : kW8Pass;
+  for (int p0 = sb; p0 < se; p0 += pass_len) {
+    const int p1 = min(p0 + pass_len, se);
+    for (int ph = 0; ph < nph; ph++) {
+      const int gp = ph * kW8Phase;                    // first group of the phase
+      const int gl0 = wave * kW8GW;                     // first group of this wave, within the phase
+      const int gb = gp + gl0;
+      const int gcnt = max(0, min(kW8GW, G - gb));
+      // weights of the first subtile go out before the activations
+      W8Stage sa, sbuf;
+      w8_load<VEC>(sa, rw, rs, rz, 16 * p0 + c, N, gb, gcnt, G, rowbytes, q);
+      if (nph > 1 || p0 == sb) {
+#pragma unroll
+        for (int t = 0; t < kW8GW; t++)
+#pragma unroll
+          for (int i = 0; i < TM; i++) {
+            const bool ok = t < gcnt;
+            uint32_t off, hstep;
+            if constexpr (TILED) {
+              off = (uint32_t)((((blockIdx.y * TM + i) * G + gb + t) * 2 * kWave + lane) * 16);
+              hstep = kWave * 16;
+            } else {
+              off = (uint32_t)((16 * i + c) * Kp + (gb + t) * kGroup + 16 * q);
+              hstep = 64;
+            }
+            xlo[t][i] = __builtin_bit_cast(v4i, ld_b128(rx, ok ? off : 0xFFFFFFF0u));
+            xhi[t][i] = __builtin_bit_cast(v4i, ld_b128(rx, ok ? off + hstep : 0xFFFFFFF0u));
+          }
+        // group sums of the phase: all loads in flight together, then to LDS
+        constexpr int APT = kW8Phase * MB / kW8Threads;
+        int32_t av[APT];
+#pragma unroll
+        for (int k = 0; k < APT; k++) {
+          const int e = threadIdx.x + k * kW8Threads;
+          const int gl = e / MB, row = e % MB, m = m0 + row, g = gp + gl;
+          uint32_t off;
+          if constexpr (TILED)
+            off = (uint32_t)(((blockIdx.y * TM + row / 16) * G + g) * 16 + row % 16) * 4u;
+          else
+            off = (uint32_t)((m - m0) * G + g) * 4u;
+          av[k] = (int32_t)ld_u32(ra, (m < M && g < G) ? off : 0xFFFFFFF0u);
+        }
+        __syncthreads();  // as_lds of the previous phase is no longer read
+#pragma unroll
+        for (int k = 0; k < APT; k++) as_lds[threadIdx.x + k * kW8Threads] = av[k];
+        __syncthreads();
+      }
+      for (int s = p0; s < p1; s += 2) {
+        // subtile s from sa (prefetch s + 1 into sbuf), then s + 1 from sbuf (prefetch
+        // s + 2 into sa). The prefetch is issued even past the range (as zero-length
+        // reads), so that every path has the same loads in flight.
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+          const int si = s + half;
+          if (si >= p1) break;
+          W8Stage &cur = half ? sbuf : sa;
+          W8Stage &nxt = half ? sa : sbuf;
+          w8_load<VEC>(nxt, rw, rs, rz, si + 1 < p1 ? 16 * (si + 1) + c : N, N, gb, gcnt, G, rowbytes, q);
+          const int n = 16 * si + c;
+          v4f facc[TM];
+#pragma unroll
+          for (int i = 0; i < TM; i++) facc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+          w8_compute<TM, VEC, EXPORT>(cur, xlo, xhi, as_lds, gl0, gcnt, zadd, facc, q, c, m0, M, n, N, G, gb, out);
+          if constexpr (!EXPORT) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) *reinterpret_cast<v4f *>(&red[buf][wave][i][lane][0]) = facc[i];
+            __syncthreads();
+            if (red_thread) {
+              float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+              for (int w = 0; w < kW8Waves; w++) {
+                const v2f t = *reinterpret_cast<const v2f *>(&red[buf][w][ri][rl][2 * rp]);
+                v0 += t.x;
+                v1 += t.y;
+              }
+              const int nn = 16 * si + (rl & 15);
+              float *acc_slot = acc_lds + ((si - p0) * MB + lr) * 16 + (rl & 15);
+              if (ph > 0) {
+                v0 = acc_slot[0] + v0;
+                v1 = acc_slot[16] + v1;
+              }
+              if (ph + 1 < nph) {
+                acc_slot[0] = v0;
+                acc_slot[16] = v1;
+              } else if (nn < N) {
+                if (m0 + lr < M) a.y[(size_t)(m0 + lr) * N + nn] = v0 * xs0;
+                if (m0 + lr + 1 < M) a.y[(size_t)(m0 + lr + 1) * N + nn] = v1 * xs1;
+              }
+            }
+            buf ^= 1;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int TM, bool EXPORT, bool TILED>
+static void launch_w4a8_v(const GemmArgs &a, int32_t *out, dim3 grid, hipStream_t s) {
+  if ((a.Kp / kGroup) % 4 == 0)
+    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, true, EXPORT, TILED>), grid, dim3(kW8Threads), 0, s, a, out);
+  else
+    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, false, EXPORT, TILED>), grid, dim3(kW8Threads), 0, s, a, out);
 }
 
 template <int TM>
-static hipError_t launch_w4a8_tm(const GemmArgs &a, int32_t *out, hipStream_t s) {
-  constexpr int TN = 2;
-  dim3 grid((a.N + 16 * TN - 1) / (16 * TN), (a.M + 16 * TM - 1) / (16 * TM));
+static hipError_t launch_w4a8_tm(const GemmArgs &a, int32_t *out, int num_cus, hipStream_t s) {
+  const int S = (a.N + 15) / 16;
+  const int per_cu = TM == 1 ? 2 : 1;  // workgroups resident per CU (VGPR budget)
+  const int cus = num_cus > 0 ? num_cus : 256;
+  const int gx = S < per_cu * cus ? S : per_cu * cus;
+  dim3 grid(gx, (a.M + 16 * TM - 1) / (16 * TM));
   if (out)
-    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, TN, true>), grid, dim3(kThreads), 0, s, a, out);
+    launch_w4a8_v<TM, true, false>(a, out, grid, s);
+  else if (a.tiled)
+    launch_w4a8_v<TM, false, true>(a, out, grid, s);
   else
-    hipLaunchKernelGGL((w4a8_mfma_kernel<TM, TN, false>), grid, dim3(kThreads), 0, s, a, out);
+    launch_w4a8_v<TM, false, false>(a, out, grid, s);
   return hipGetLastError();
 }
 
-hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, hipStream_t s) {
-  if (a.M <= 16) return launch_w4a8_tm<1>(a, out, s);
-  if (a.M <= 32) return launch_w4a8_tm<2>(a, out, s);
-  return launch_w4a8_tm<4>(a, out, s);
+hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, int num_cus, hipStream_t s) {
+  if (a.M <= 16) return launch_w4a8_tm<1>(a, out, num_cus, s);
+  if (a.M <= 32) return launch_w4a8_tm<2>(a, out, num_cus, s);
+  if (a.M <= 48) return launch_w4a8_tm<3>(a, out, num_cus, s);
+  return launch_w4a8_tm<4>(a, out, num_cus, s);
 }
 
 // ============================================================ W4A16 / MXFP4, fp32 MFMA

@@ -152,6 +152,43 @@ def test_w4a8(rng, isa, shape, asym):
     O.assert_fp_close(K.gemm_w4a8_q(a, W, isa=isa), ref, bound, RTOL)
 
 
+def _random_int4(rng, n, kp, asym):
+    """Random packed int4 weights (any code, any zero-point), without quantizing a matrix."""
+    g = kp // 128
+    return lb.formats.Int4Weights(
+        rng.integers(0, 256, (n, kp // 2), dtype=np.uint8),
+        (rng.standard_normal((n, g)) * 0.05).astype(np.float32),
+        rng.integers(0, 16, (n, g), dtype=np.uint8) if asym else None, kp)
+
+
+# Shapes that give the persistent MFMA kernel several 16-row weight subtiles per
+# workgroup (N = 11008), more than one pass of subtiles and more than one phase of
+# 32 groups (N = 33000, K = 4352: G = 34, not a multiple of 4), and M tails.
+BIG = [(64, 11008, 4096, True), (40, 11008, 4096, False), (16, 11008, 4096, True),
+       (17, 33000, 4352, True), (70, 4100, 4352, False)]
+
+
+@pytest.mark.parametrize("m,n,kp,asym", BIG)
+def test_w4a8_mfma_persistent_schedule(rng, m, n, kp, asym):
+    W = _random_int4(rng, n, kp, asym)
+    x = rng.standard_normal((m, kp)).astype(np.float32)
+    a = lb.quantize_act_int8(x)
+    ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+    O.assert_fp_close(K.gemm_w4a8(x, W, isa="gfx950-mfma"), ref, bound, RTOL)
+    O.assert_fp_close(K.gemm_w4a8_q(a, W, isa="gfx950-mfma"), ref, bound, RTOL)
+
+
+@pytest.mark.parametrize("m,n,kp", [(17, 33000, 4352), (64, 5000, 4096)])
+def test_group_acc_mfma_persistent_schedule(rng, m, n, kp):
+    W = _random_int4(rng, n, kp, True)
+    xq = rng.integers(-128, 128, (m, kp), dtype=np.int8)
+    xq[0, :128] = -128
+    a = lb.formats.Int8Acts(xq, np.ones(m, np.float32),
+                            xq.reshape(m, -1, 128).sum(axis=2, dtype=np.int32))
+    np.testing.assert_array_equal(K.w4a8_group_acc(a, W, isa="gfx950-mfma"),
+                                  cref.c_group_acc(xq, W.qw, W.zeros))
+
+
 @pytest.mark.parametrize("isa", PATHS)
 def test_int4_negative_scales(rng, isa):
     x, w = _problem(rng, 5, 37, 300)
