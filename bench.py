@@ -291,6 +291,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline time budget")
     ap.add_argument("--no-graph", action="store_true", help="time plain launches instead of a graph replay")
     ap.add_argument("--only-headline", action="store_true", help="measure only the headline W4A8 decode")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run the plain 16-byte copy kernel 5 times over MIB MiB (the reference "
+                         "point that scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the hot path has no "
@@ -303,6 +306,14 @@ def main() -> int:
     import lowbit_amd as lb
 
     dev = Dev()
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        src, dst = dev.K.DeviceBuffer(nbytes), dev.K.DeviceBuffer(nbytes)
+        for _ in range(5):
+            dev.check(dev.L.lbd_copy_kernel(dst.ptr, src.ptr, nbytes, dev.stream), "copy kernel")
+        dev.check(dev.L.lb_stream_synchronize(dev.stream), "sync")
+        print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 5}), flush=True)
+        return 0
     info = dev.K.cpu_info()
     log(f"device {info.get('arch')} with {info.get('compute_units')} CUs")
     rng = np.random.default_rng(0)
