@@ -152,10 +152,29 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
     ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp)
     ws = K.DeviceBuffer(ws_bytes)
     s = dev.stream
+    # W4A8 on the matrix cores reads the t16 tile layout (a one-time device repack of
+    # each resident copy, as lowbit_amd.to_device handles do; not timed)
+    layout = "row-major"
+    if fmt == "w4a8" and L.lbd_gemm_path(2, m, W.kp, C.byref(prm)) == K.ISA_GFX950_MFMA:
+        layout = "t16"
+        bq, bs, bz = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+        dev.check(L.lbd_int4_t16_bytes(n, W.kp, C.byref(bq), C.byref(bs), C.byref(bz)), "t16 sizes")
+        tiled = []
+        for b in pool:
+            qwt, st = K.DeviceBuffer(bq.value), K.DeviceBuffer(bs.value)
+            zt = K.DeviceBuffer(bz.value) if len(b) > 2 else None
+            dev.check(L.lbd_repack_int4_t16(b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None, n, W.kp,
+                                            qwt.ptr, st.ptr, zt.ptr if zt else None, s), "t16 repack")
+            tiled.append((qwt, st, zt))
+        dev.check(L.lb_stream_synchronize(s), "sync")
+        pool = tiled
 
     def launch(i):
         b = pool[i % len(pool)]
-        if fmt == "w4a16":
+        if layout == "t16":
+            rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n, dy.ptr,
+                                     C.byref(prm), ws.ptr, ws_bytes, s)
+        elif fmt == "w4a16":
             rc = L.lbd_gemm_w4a16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None,
                                   n, dy.ptr, C.byref(prm), s)
         elif fmt == "mxfp4":
@@ -173,7 +192,7 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
     t = ms * 1e-3
     return {
         "format": fmt, "M": m, "N": n, "K": k, "cache": "cold" if cold else "hot",
-        "path": K.ISA_NAMES.get(path, "?"), "pool_copies": len(pool),
+        "path": K.ISA_NAMES.get(path, "?"), "weight_layout": layout, "pool_copies": len(pool),
         "us_per_call": round(ms * 1e3, 3), "weight_bytes": int(W.nbytes),
         "weight_gbps": round(W.nbytes / t / 1e9, 1),
         "gflops": round(2.0 * m * n * k / t / 1e9, 1),

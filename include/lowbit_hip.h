@@ -155,6 +155,36 @@ int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp,
                        const uint8_t *qw, const uint8_t *zeros, int N,
                        int32_t *out, int isa, void *stream);
 
+/* regime (LB_ISA_GFX950 or LB_ISA_GFX950_MFMA) an lbd_gemm_* of kind 0 = W4A16,
+ * 1 = MXFP4, 2 = W4A8 with this shape and lb_params runs in (no reference
+ * counterpart; the reference's effective ISA does not depend on the shape) */
+int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p);
+
+/* ---- MFMA tile layout ("t16") of int4 g128 weights (no reference counterpart:
+ *      a device-private copy of an Int4Weights matrix, src/lowbit/formats.py:56-87,
+ *      in the order the int8 matrix cores consume it, so that every 16-byte weight
+ *      load of a wave reads one contiguous 1 KiB tile; the role pack_amx plays for
+ *      the reference's AMX path, src/lowbit/formats.py:253-293). With S = ceil(N/16)
+ *      subtiles of 16 rows and G4 = Kp/128 rounded up to a multiple of 4:
+ *        qwt [S][G4][64][16 B]: lane 16q + c of tile (s, g) holds bytes
+ *                               [64g + 16q, 64g + 16q + 16) of row 16s + c
+ *        st  [S][G4/4][16][4]   fp32 scale of row 16s + c, group g (entry g % 4)
+ *        zt  [S][G4/4][16][4]   uint8 zero-point, same order (NULL: z = 8)
+ *      Rows past N and groups past Kp/128 are zero. ---- */
+/* sizes in bytes of the three arrays; returns 0 or LB_ERR_SHAPE */
+int lbd_int4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *st_bytes,
+                       size_t *zt_bytes);
+/* fills qwt / st / zt (zt only when zeros != NULL) from row-major device arrays */
+int lbd_repack_int4_t16(const uint8_t *qw, const float *scales,
+                        const uint8_t *zeros, int N, int Kp, uint8_t *qwt,
+                        float *st, uint8_t *zt, void *stream);
+/* y = x . w^T as lbd_gemm_w4a8 (same workspace contract), weights in the t16
+ * layout; always the int8 matrix-core path (returns LB_ISA_GFX950_MFMA) */
+int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt,
+                      const float *st, const uint8_t *zt, int N, float *y,
+                      const lb_params *p, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
 /* ---- device plumbing for the ctypes layer and benchmarks ---- */
 int lb_dev_malloc(void **ptr, size_t bytes);
 int lb_dev_free(void *ptr);

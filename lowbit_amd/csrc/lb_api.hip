@@ -223,13 +223,30 @@ size_t w4a8_ws_bytes(int M, int Kp) {
   return align256(lbk::tiled_xq_bytes(M, Kp)) + align256((size_t)M * 4) + align256(lbk::tiled_asum_bytes(M, Kp));
 }
 
+// The caller's workspace (checked) or, when it passed none, the per-thread buffer.
+int w4a8_workspace(int M, int Kp, size_t given_bytes, hipStream_t s, char **ws) {
+  const size_t need = w4a8_ws_bytes(M, Kp);
+  if (*ws) {
+    if (given_bytes < need) return fail(LB_ERR_ARG, "workspace too small");
+    if ((reinterpret_cast<uintptr_t>(*ws) & 255) != 0) return fail(LB_ERR_ARG, "workspace must be 256-byte aligned");
+    return 0;
+  }
+  Ctx *c = nullptr;
+  int rc = get_ctx(&c);
+  if (rc < 0) return rc;
+  if ((rc = grow(&c->ws, &c->ws_cap, need, s)) < 0) return rc;
+  *ws = c->ws;
+  return 0;
+}
+
 // fp32 activations in; quantized inside (fused into the GEMV, or a quantizer
 // kernel into `ws` before the MFMA kernel).
 int run_w4a8(const lbk::GemmArgs &a, const lb_params *p, char *ws, hipStream_t s) {
   int cus = 0;
   DevInfo di;
   if (device_info(&di) == 0) cus = di.cus;
-  const int path = choose_path(lbk::F_W4A8, a.M, a.Kp, p);
+  // t16 weights exist only for the matrix-core kernel
+  const int path = a.wt16 ? LB_ISA_GFX950_MFMA : choose_path(lbk::F_W4A8, a.M, a.Kp, p);
   if (path == LB_ISA_GFX950) {
     hipError_t e = lbk::launch_gemv(lbk::F_W4A8, a, cus, s);
     if (e != hipSuccess) return fail_hip(e, "W4A8 GEMV launch");
@@ -380,18 +397,59 @@ int lbd_gemm_w4a8(const float *x, int M, int Kp, const uint8_t *qw, const float 
   a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
   a.M = M; a.Kp = Kp; a.N = N;
   char *ws = static_cast<char *>(workspace);
-  if (choose_path(lbk::F_W4A8, M, Kp, p) == LB_ISA_GFX950_MFMA) {
-    const size_t need = w4a8_ws_bytes(M, Kp);
-    if (ws) {
-      if (workspace_bytes < need) return fail(LB_ERR_ARG, "workspace too small");
-      if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return fail(LB_ERR_ARG, "workspace must be 256-byte aligned");
-    } else {
-      Ctx *c = nullptr;
-      if ((rc = get_ctx(&c)) < 0) return rc;
-      if ((rc = grow(&c->ws, &c->ws_cap, need, s)) < 0) return rc;
-      ws = c->ws;
-    }
-  }
+  if (choose_path(lbk::F_W4A8, M, Kp, p) == LB_ISA_GFX950_MFMA &&
+      (rc = w4a8_workspace(M, Kp, workspace_bytes, s, &ws)) < 0)
+    return rc;
+  return run_w4a8(a, p, ws, s);
+}
+
+int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p) {
+  static const int fmts[] = {lbk::F_W4A16, lbk::F_MXFP4, lbk::F_W4A8};
+  if (kind < 0 || kind > 2) return fail(LB_ERR_ARG, "unknown GEMM kind");
+  if (M <= 0 || Kp <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  return ok(choose_path(fmts[kind], M, Kp, p));
+}
+
+int lbd_int4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *st_bytes, size_t *zt_bytes) {
+  int rc = check_shape(1, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (qwt_bytes) *qwt_bytes = lbk::t16_qw_bytes(N, Kp);
+  if (st_bytes) *st_bytes = lbk::t16_group_entries(N, Kp) * 4;
+  if (zt_bytes) *zt_bytes = lbk::t16_group_entries(N, Kp);
+  return ok(0);
+}
+
+int lbd_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                        uint8_t *qwt, float *st, uint8_t *zt, void *stream) {
+  int rc = check_shape(1, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!qw || !scales || !qwt || !st || (zeros && !zt)) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(qw) || !aligned16(qwt)) return fail(LB_ERR_ARG, "qw and qwt must be 16-byte aligned");
+  if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
+  hipError_t e = lbk::launch_repack_int4_t16(qw, scales, zeros, N, Kp, qwt, st, zeros ? zt : nullptr,
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "t16 repack launch");
+  return ok(0);
+}
+
+int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
+                      int N, float *y, const lb_params *p, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qwt || !st || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qwt) || !aligned16(st))
+    return fail(LB_ERR_ARG, "x, qwt and st must be 16-byte aligned");
+  if (zt && (reinterpret_cast<uintptr_t>(zt) & 3)) return fail(LB_ERR_ARG, "zt must be 4-byte aligned");
+  if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qwt; a.scales = st; a.zeros = zt; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  a.wt16 = true;
+  char *ws = static_cast<char *>(workspace);
+  if ((rc = w4a8_workspace(M, Kp, workspace_bytes, s, &ws)) < 0) return rc;
   return run_w4a8(a, p, ws, s);
 }
 

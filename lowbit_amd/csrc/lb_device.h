@@ -145,37 +145,46 @@ __device__ __forceinline__ int8_t quant_one(float v, float sc) {
   return (int8_t)(int)q;
 }
 
-// rint(fl(v / sc)) without a division on the common path. inv = fl(1 / sc) and
-// t = fl(v * inv) differ from v / sc by at most |v/sc| * (2^-24 + 2^-24 + 2^-48)
-// < 2^-16 (|v/sc| <= 127 * (1 + 2^-23) because |v| <= amax and sc = fl(amax/127)),
-// and fl(v / sc) differs from v / sc by at most 2^-17, so |t - fl(v/sc)| < 2^-15.
-// Unless t lies within 2^-15 of a half-integer, t and fl(v / sc) therefore round
-// to the same integer (and fl(v / sc) cannot itself be a tie). |t - rint(t)| and
-// its distance to 0.5 are exact in float32 (|t| < 256). Near-ties, NaN and an
-// overflowed inv (sc < 2^-126) take the IEEE division.
-__device__ __forceinline__ int8_t quant_one_fast(float v, float sc, float inv) {
-  const float t = v * inv;
-  float q = rintf(t);
-  if (!(fabsf(fabsf(t - q) - 0.5f) > 0x1p-15f)) q = rintf(v / sc);
-  q = q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q);
-  return (int8_t)(int)q;
-}
-
-// Four consecutive elements -> packed int8x4 and their integer sum.
-__device__ __forceinline__ uint32_t quant4(float4 v, float sc, int &sum) {
+// Four consecutive elements -> packed int8x4 (IEEE division for every element).
+__device__ __forceinline__ uint32_t quant4(float4 v, float sc) {
   const int8_t a = quant_one(v.x, sc), b = quant_one(v.y, sc);
   const int8_t c = quant_one(v.z, sc), d = quant_one(v.w, sc);
-  sum = (int)a + (int)b + (int)c + (int)d;
   return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
          ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
 }
 
-__device__ __forceinline__ uint32_t quant4_fast(float4 v, float sc, float inv, int &sum) {
-  const int8_t a = quant_one_fast(v.x, sc, inv), b = quant_one_fast(v.y, sc, inv);
-  const int8_t c = quant_one_fast(v.z, sc, inv), d = quant_one_fast(v.w, sc, inv);
-  sum = (int)a + (int)b + (int)c + (int)d;
-  return (uint32_t)(uint8_t)a | ((uint32_t)(uint8_t)b << 8) |
-         ((uint32_t)(uint8_t)c << 16) | ((uint32_t)(uint8_t)d << 24);
+// Four consecutive elements -> packed int8x4, bit-identical to quant4, without a
+// division on the common path. With inv = fl(1/sc), u = fma(v, inv, 128) (one
+// rounding) differs from fl(v/sc) + 128 by less than 2^-15:
+//   |u - (v*inv + 128)| <= 2^-17 (half an ulp below 256),
+//   |v*inv - v/sc| <= |v/sc| * 2^-24 < 2^-17 (|v/sc| <= 127 (1 + 2^-23) since
+//   |v| <= amax and sc = fl(amax/127)), and |fl(v/sc) - v/sc| <= 2^-18.
+// So unless u lies within 2^-15 of a half-integer, rint(u) - 128 == rint(fl(v/sc))
+// (fl(v/sc) is then no tie either), and |u - rint(u)| is exact in float32. rint(u)
+// is an integer in [1, 255]: v_cvt_pk_u8_f32 packs it exactly and XOR 0x80 turns
+// q + 128 into the two's-complement byte q; the clamp at +-127 can never act.
+// A slot with a near-tie, NaN or an overflowed inv (sc < 2^-128) is redone with
+// the IEEE division (about one slot in 4000 for random data).
+__device__ __forceinline__ uint32_t quant4_fast(float4 v, float sc, float inv) {
+  const float u0 = __builtin_fmaf(v.x, inv, 128.0f), u1 = __builtin_fmaf(v.y, inv, 128.0f);
+  const float u2 = __builtin_fmaf(v.z, inv, 128.0f), u3 = __builtin_fmaf(v.w, inv, 128.0f);
+  const float r0 = __builtin_rintf(u0), r1 = __builtin_rintf(u1);
+  const float r2 = __builtin_rintf(u2), r3 = __builtin_rintf(u3);
+  constexpr float kSafe = 0.5f - 0x1p-15f;
+  const bool ok = (fabsf(u0 - r0) < kSafe) & (fabsf(u1 - r1) < kSafe) &
+                  (fabsf(u2 - r2) < kSafe) & (fabsf(u3 - r3) < kSafe);
+  uint32_t p = __builtin_amdgcn_cvt_pk_u8_f32(r0, 0, 0u);
+  p = __builtin_amdgcn_cvt_pk_u8_f32(r1, 1, p);
+  p = __builtin_amdgcn_cvt_pk_u8_f32(r2, 2, p);
+  p = __builtin_amdgcn_cvt_pk_u8_f32(r3, 3, p);
+  p ^= 0x80808080u;
+  if (!ok) p = quant4(v, sc);
+  return p;
+}
+
+// Sum of the four signed bytes of a packed int8x4.
+__device__ __forceinline__ int sum_i8x4(uint32_t p) {
+  return __builtin_amdgcn_sdot4((int)p, 0x01010101, 0, false);
 }
 
 // amax of one row of Kp floats (Kp % 4 == 0) by a block of NT threads; `red` is

@@ -23,7 +23,22 @@ struct GemmArgs {
   float *y = nullptr;             // [M, N]
   int M = 0, Kp = 0, N = 0;
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
+  bool wt16 = false;              // qw / scales / zeros in the MFMA tile layout (t16)
 };
+
+// MFMA tile layout ("t16") of int4 g128 weights, a device-private copy of the
+// packed matrix in the order the int8 MFMA path consumes it. With S = ceil(N/16)
+// subtiles of 16 rows and G4 = G rounded up to a multiple of 4:
+//   qwt  [S][G4][64][16 B]  lane l = 16q + c of tile (s, g) holds bytes
+//                           [64g + 16q, 64g + 16q + 16) of row 16s + c
+//   st   [S][G4/4][16][4]   fp32 scale of row 16s + c, group 4 (g/4) + g%4
+//   zt   [S][G4/4][16][4]   uint8 zero-point, same order (absent for z = 8)
+// Rows past N and groups past G are zero (zero codes, scale 0, zero-point 0).
+__host__ __device__ inline int t16_groups(int Kp) { return ((Kp / 128) + 3) & ~3; }
+__host__ __device__ inline size_t t16_qw_bytes(int N, int Kp) { return (size_t)((N + 15) / 16) * t16_groups(Kp) * 1024; }
+__host__ __device__ inline size_t t16_group_entries(int N, int Kp) { return (size_t)((N + 15) / 16) * 16 * t16_groups(Kp); }
+hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                                  uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s);
 
 // Small-M VALU kernels: largest M they take and the LDS they need.
 constexpr int kGemvMaxM = 4;

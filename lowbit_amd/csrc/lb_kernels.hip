@@ -25,6 +25,8 @@
 // loads 16 contiguous bytes of a weight row (the natural packed order) and puts
 // the matching activations in the same slots, so weights go from HBM to the
 // matrix cores without an LDS transpose.
+#include <algorithm>
+
 #include "lb_device.h"
 #include "lb_internal.h"
 
@@ -98,9 +100,8 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(
   // thread t handles 4 elements per slot; a group of 128 is one 32-lane half-wave
   // (Kp % 128 == 0, so half-waves enter and leave a slot together)
   auto emit = [&](float4 t, int e) {
-    int s4;
-    const uint32_t qv = quant4_fast(t, sc, inv, s4);
-    const int gs = half_wave_sum(s4);
+    const uint32_t qv = quant4_fast(t, sc, inv);
+    const int gs = half_wave_sum(sum_i8x4(qv));
     if constexpr (TILED) {
       *reinterpret_cast<uint32_t *>(xq + w4a8_tiled_offset(m, e, G)) = qv;
       if ((threadIdx.x & 31) == 31) asum[((m >> 4) * G + (e >> 7)) * 16 + (m & 15)] = gs;
@@ -350,7 +351,7 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 template <int F, int MB, int R, int NIT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ float red[kGemvWaves];
+  __shared__ float red[2][kGemvWaves];
   constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
   constexpr int T = kGemvThreads;
   const int Kp = a.Kp, N = a.N;
@@ -361,7 +362,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int gw = blockIdx.x * kGemvWaves + wave, W = gridDim.x * kGemvWaves;
-  const int r0 = (int)(((long long)gw * N) / W), r1 = (int)(((long long)(gw + 1) * N) / W);
+  // wave gw takes rows [r0, r1): N / W each, one more for the first N % W waves
+  const int rbase = (int)((unsigned)N / (unsigned)W), rrem = N - rbase * W;
+  const int r0 = gw * rbase + min(gw, rrem), r1 = r0 + rbase + (gw < rrem ? 1 : 0);
 
   float *xl = reinterpret_cast<float *>(lds);                           // fp32 planes [MB][8][nchp][4]
   uint8_t *ql = lds;                                                      // int8 planes [MB][2][nchp][16]
@@ -431,13 +434,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
           amax = fmaxf(fmaxf(amax, fabsf(v.z)), fabsf(v.w));
         }
       }
+      // red[m & 1]: row m + 1 writes the other half, and row m + 2 comes after
+      // row m + 1's barrier, by which time every wave has read row m's partials
       amax = wave_max(amax);
-      if (lane == 0) red[wave] = amax;
+      if (lane == 0) red[m & 1][wave] = amax;
       __syncthreads();
-      float rmax = red[0];
+      float rmax = red[m & 1][0];
 #pragma unroll
-      for (int w = 1; w < kGemvWaves; w++) rmax = fmaxf(rmax, red[w]);
-      __syncthreads();
+      for (int w = 1; w < kGemvWaves; w++) rmax = fmaxf(rmax, red[m & 1][w]);
       const float sc = row_scale(rmax);
       const float inv = 1.0f / sc;
       if (threadIdx.x == 0) xsl[m] = sc;
@@ -453,11 +457,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
         } else {
           v = ld_f4(rx, e * 4);
         }
-        int ci, half, within, s4;
+        int ci, half, within;
         chunk_pos(F, e, ci, half, within);
-        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nchp + ci) * 16 + within) =
-            quant4_fast(v, sc, inv, s4);
-        const int gs = half_wave_sum(s4);
+        const uint32_t qv = quant4_fast(v, sc, inv);
+        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nchp + ci) * 16 + within) = qv;
+        const int gs = half_wave_sum(sum_i8x4(qv));
         if ((threadIdx.x & 31) == 31) asl[m * Gp + (e >> 7)] = gs;
       }
     }
@@ -841,6 +845,317 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_mfma_kernel(GemmArgs a, int32
   }
 }
 
+// ------------------------------------------------------------ W4A8 GEMM (int8 MFMA), Y only
+//
+// The kernel above also serves the exact group-accumulator export; this one only
+// produces Y and is arranged around the three limits of the batch regime:
+//   * VALU: per (16x16 tile, group) the int32 accumulator of the raw codes needs a
+//     conversion and one FMA with the group scale (8 VALU for 2 MFMA). The
+//     zero-point term is not subtracted per group: since
+//       sum_g s_g (sum_k q a - z_g asum_g) = sum_g s_g sum_k q a - sum_g (s_g z_g) asum_g,
+//     the second sum over a wave's four groups is one v_mfma_f32_16x16x4_f32 per
+//     row block (A = asum of the 16 rows x 4 groups, B = -s z of the 16 weight rows
+//     x 4 groups), accumulated into the same fp32 tile.
+//   * latency: weights of the next PF subtiles are in flight while one is computed,
+//     and the waves' partial tiles of a whole chunk of NS subtiles are reduced in
+//     LDS once, with one barrier, instead of once per subtile.
+//   * L1/L2 bandwidth: every workgroup reads its 16*TM activation rows once per
+//     K phase into registers; TM is chosen per shape to minimise the bytes each CU
+//     must read (activations + its share of the weights).
+// Waves split the K groups as in the kernel above (wave w: groups 4w..4w+3 of each
+// phase of 32). fp32 rounding of the split terms stays within the reference's W4A8
+// bound, which is built from both magnitudes (sum q|a| and z|sum a|).
+
+constexpr int kW8PF = 2;  // weight subtiles in flight ahead of the one computed
+constexpr int kW8GB = 1;  // groups whose MFMAs are issued together
+
+// Weight operands of one subtile when all four of the wave's groups exist and G % 4
+// == 0 (or the weights are in the t16 layout): four 16-byte loads from one offset
+// register (group offsets are immediates), the four scales as one 16-byte load and
+// the four zero-points as one dword. Rows past N start past the end of their
+// descriptors and read 0.
+template <bool WT>
+__device__ __forceinline__ void w8_load_full(W8Stage &st, Rsrc rw, Rsrc rs, Rsrc rz, uint32_t woff, uint32_t goff) {
+#pragma unroll
+  for (int t = 0; t < kW8GW; t++) st.w[t] = ld_b128(rw, woff + (WT ? 1024u : 64u) * t);
+  const float4 sv = ld_f4(rs, goff * 4u);
+  st.s[0] = sv.x;
+  st.s[1] = sv.y;
+  st.s[2] = sv.z;
+  st.s[3] = sv.w;
+  st.zw[0] = ld_u32(rz, goff);
+}
+
+// One 16-row weight subtile against the wave's activation operands: the zero-point
+// MFMA first (its result is needed only by the FMAs at the end), then all first
+// MFMAs (low nibbles), all second MFMAs (high nibbles, accumulating onto the first:
+// they issue 4*TM MFMAs after their operand, past its latency), then the fp32
+// rescale of every group accumulator.
+template <int TM>
+__device__ __forceinline__ void w8_tile(const W8Stage &cur, const v4i (&xlo)[kW8GW][TM], const v4i (&xhi)[kW8GW][TM],
+                                        const float (&asf)[TM], float bz, v4f (&facc)[TM]) {
+#pragma unroll
+  for (int i = 0; i < TM; i++) facc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(asf[i], bz, facc[i], 0, 0, 0);
+  // groups in batches of kW8GB: all low-nibble MFMAs of the batch, then all
+  // high-nibble ones, then the rescale
+  const v4i zero4 = {0, 0, 0, 0};
+#pragma unroll
+  for (int t0 = 0; t0 < kW8GW; t0 += kW8GB) {
+    v4i bhi[kW8GB], acc[kW8GB][TM];
+#pragma unroll
+    for (int u = 0; u < kW8GB; u++) {
+      const uint4 w = cur.w[t0 + u];
+      const v4i blo = {(int)lo_nibbles(w.x), (int)lo_nibbles(w.y), (int)lo_nibbles(w.z), (int)lo_nibbles(w.w)};
+      bhi[u] = v4i{(int)hi_nibbles(w.x), (int)hi_nibbles(w.y), (int)hi_nibbles(w.z), (int)hi_nibbles(w.w)};
+#pragma unroll
+      for (int i = 0; i < TM; i++) acc[u][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xlo[t0 + u][i], blo, zero4, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kW8GB; u++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        acc[u][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xhi[t0 + u][i], bhi[u], acc[u][i], 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kW8GB; u++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) facc[i][r] = __builtin_fmaf((float)acc[u][i][r], cur.s[t0 + u], facc[i][r]);
+  }
+}
+
+// FULL (G % 32 == 0): every wave has all four groups in every phase, so the weight
+// loads take the vector path with no per-group clamps.
+// WT: weights in the t16 tile layout, so each 16-byte weight load of a wave is one
+// contiguous 1 KiB tile instead of 64 bytes from each of 16 rows (the row-major
+// pattern runs at about half the cache bandwidth). Groups past G hold zeros there.
+template <int TM, int NS, bool VEC, bool FULL, bool TILED, bool WT>
+__global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
+  static_assert(!FULL || VEC, "the full path needs G % 4 == 0");
+  static_assert(!WT || VEC, "the t16 layout pads groups to a multiple of 4");
+  // partial tiles of every wave: [NS][TM][wave][lane] x 4 floats
+  __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int q = lane >> 4, c = lane & 15;
+  const int M = a.M, N = a.N, Kp = a.Kp, G = Kp / kGroup;
+  const uint32_t rowbytes = (uint32_t)(Kp >> 1);
+  constexpr int MB = 16 * TM;
+  const int mb0 = blockIdx.y * TM, m0 = mb0 * 16;
+  const int S = (N + 15) / 16;
+  // subtiles [sb, se): S / gridDim.x each, one more for the first S % gridDim.x
+  const int sbase = (int)((unsigned)S / gridDim.x), srem = S - sbase * (int)gridDim.x;
+  const int bx = blockIdx.x;
+  const int sb = bx * sbase + min(bx, srem), se = sb + sbase + (bx < srem ? 1 : 0);
+  const int nph = (G + kW8Phase - 1) / kW8Phase;
+  const int zadd = a.zeros ? 0 : 8;
+
+  const int mblocks = (M + 15) / 16;
+  const Rsrc rx = TILED ? make_rsrc(a.xq, (uint32_t)(mblocks * 16 * Kp))
+                        : make_rsrc(a.xq + (size_t)m0 * Kp, (uint32_t)(min(M - m0, MB) * Kp));
+  const Rsrc ra = TILED ? make_rsrc(a.asum, (uint32_t)(mblocks * G * 16 * 4))
+                        : make_rsrc(a.asum + (size_t)m0 * G, (uint32_t)(min(M - m0, MB) * G * 4));
+  const int G4 = (G + 3) & ~3;  // groups per subtile in the t16 layout
+  const size_t wbytes = WT ? t16_qw_bytes(N, Kp) : (size_t)N * rowbytes;
+  const size_t gents = WT ? t16_group_entries(N, Kp) : (size_t)N * G;
+  const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(wbytes, (size_t)0xFFFFFFF0u));
+  const Rsrc rs = make_rsrc(a.scales, (uint32_t)(gents * 4));
+  const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, a.zeros ? (uint32_t)((gents + 3) & ~(size_t)3) : 0u);
+  const Rsrc rxs = make_rsrc(a.xs + m0, (uint32_t)(min(M - m0, MB) * 4));
+
+  // per-token scales of the four rows this thread stores in the reduction: its
+  // lane l = threadIdx.x % 64 and row block i = (threadIdx.x / 64) % TM are the same
+  // for every item it takes (512 is a multiple of 64 * TM); loaded up front
+  // because a wait for a load issued after the Y stores would wait for them too
+  static_assert(kW8Waves % TM == 0, "each thread must keep one row block in the reduction");
+  const int rlane = threadIdx.x & (kWave - 1), rblk = (threadIdx.x / kWave) % TM;
+  const int rrow = 16 * rblk + 4 * (rlane >> 4);  // local row of the thread's first output
+  // one dword per row: a 16-byte load straddling the end of the rows would read 0
+  float xsr[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) xsr[r] = ld_f32(rxs, (uint32_t)(rrow + r) * 4u);
+
+  v4i xlo[kW8GW][TM], xhi[kW8GW][TM];
+  float asf[TM];
+  for (int cb = sb; cb < se; cb += NS) {
+    const int ce = min(cb + NS, se);
+    v4f facc[NS][TM];
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++) facc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int ph = 0; ph < nph; ph++) {
+      const int gb = ph * kW8Phase + wave * kW8GW;     // this wave's first group
+      const int gcnt = max(0, min(kW8GW, G - gb));
+      // row-major: row n of subtile s has its weights at n * rowbytes + gb * 64 + q * 16
+      // and its group data at n * G + gb; t16: tile (s, gb + t) at ((s G4 + gb + t) 64 +
+      // lane) 16 and the four groups' data at ((s G4/4 + gb/4) 16 + c) 4
+      const uint32_t wstep = WT ? (uint32_t)G4 * 1024u : 16u * rowbytes;
+      const uint32_t gstep = WT ? (uint32_t)G4 * 16u : 16u * (uint32_t)G;
+      const uint32_t woff0 = WT ? ((uint32_t)cb * G4 + gb) * 1024u + (uint32_t)lane * 16u
+                                : (uint32_t)(16 * cb + c) * rowbytes + (uint32_t)gb * 64u + (uint32_t)q * 16u;
+      const uint32_t goff0 = WT ? ((uint32_t)cb * (G4 / 4) + gb / 4) * 64u + (uint32_t)c * 4u
+                                : (uint32_t)(16 * cb + c) * (uint32_t)G + (uint32_t)gb;
+      auto load = [&](W8Stage &st, int j) {
+        const int sj = cb + j;
+        const bool in = j < NS && sj < ce;  // past the chunk: rows past N, zero-length reads
+        if constexpr (FULL || WT) {
+          // past the matrix: subtile S + 1 starts beyond every descriptor
+          const uint32_t jj = in ? (uint32_t)j : (uint32_t)(S - cb + 1);
+          w8_load_full<WT>(st, rw, rs, rz, woff0 + jj * wstep, goff0 + jj * gstep);
+        } else {
+          w8_load<VEC>(st, rw, rs, rz, in ? 16 * sj + c : N, N, gb, gcnt, G, rowbytes, q);
+        }
+      };
+      // weights of the first PF + 1 subtiles go out before the activations
+      W8Stage st[kW8PF + 1];
+#pragma unroll
+      for (int j = 0; j <= kW8PF; j++) load(st[j], j);
+      if (nph > 1 || cb == sb) {
+        // activation operands of this wave's groups (groups past G read 0, so the
+        // weights of those slots never matter) and the group sums of the
+        // zero-point MFMA (lane (q, c): row c of the block, group gb + q)
+#pragma unroll
+        for (int t = 0; t < kW8GW; t++)
+#pragma unroll
+          for (int i = 0; i < TM; i++) {
+            const bool ok = t < gcnt;
+            uint32_t off, hstep;
+            if constexpr (TILED) {
+              off = (uint32_t)((((mb0 + i) * G + gb + t) * 2 * kWave + lane) * 16);
+              hstep = kWave * 16;
+            } else {
+              off = (uint32_t)((16 * i + c) * Kp + (gb + t) * kGroup + 16 * q);
+              hstep = 64;
+            }
+            xlo[t][i] = __builtin_bit_cast(v4i, ld_b128(rx, ok ? off : 0xFFFFFFF0u));
+            xhi[t][i] = __builtin_bit_cast(v4i, ld_b128(rx, ok ? off + hstep : 0xFFFFFFF0u));
+          }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          uint32_t off;
+          if constexpr (TILED)
+            off = (uint32_t)((((mb0 + i) * G + gb + q) * 16 + c) * 4);
+          else
+            off = (uint32_t)(((16 * i + c) * G + gb + q) * 4);
+          asf[i] = (float)(int32_t)ld_u32(ra, q < gcnt ? off : 0xFFFFFFF0u);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NS; j++) {
+        if (cb + j >= ce) break;  // workgroup-uniform
+        W8Stage &cur = st[j % (kW8PF + 1)];
+        const int n = 16 * (cb + j) + c;
+        if constexpr (!FULL) {
+          // groups past G: zero scales (their activations are zero too)
+#pragma unroll
+          for (int t = 0; t < kW8GW; t++) cur.s[t] = t < gcnt ? cur.s[t] : 0.0f;
+        }
+        // -s * z of group gb + q for weight row n: B operand of the zero-point MFMA
+        float sq = cur.s[0];
+        sq = q == 1 ? cur.s[1] : sq;
+        sq = q == 2 ? cur.s[2] : sq;
+        sq = q == 3 ? cur.s[3] : sq;
+        int zq;
+        if constexpr (VEC) {
+          zq = (int)((cur.zw[0] >> (8 * q)) & 0xFFu);
+        } else {
+          const int z0 = w8_zero<VEC>(cur, 0, n, G, gb), z1 = w8_zero<VEC>(cur, 1, n, G, gb),
+                    z2 = w8_zero<VEC>(cur, 2, n, G, gb), z3 = w8_zero<VEC>(cur, 3, n, G, gb);
+          zq = q == 1 ? z1 : z0;
+          zq = q == 2 ? z2 : zq;
+          zq = q == 3 ? z3 : zq;
+        }
+        const float bz = -sq * (float)(zq + zadd);
+        w8_tile<TM>(cur, xlo, xhi, asf, bz, facc[j]);
+        // refill this stage with subtile j + PF + 1 (zero-length past the chunk)
+        if (j + kW8PF + 1 < NS) load(cur, j + kW8PF + 1);
+      }
+    }
+    // ---- reduce the waves' partial tiles of the chunk, scale by xs, store
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) = facc[j][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < (ce - cb) * TM * kWave; e += kW8Threads) {
+      const int j = e / (kWave * TM);  // e % 64 == rlane, (e / 64) % TM == rblk
+      v4f v = *reinterpret_cast<const v4f *>(&red[(((j * TM + rblk) * kW8Waves + 0) * kWave + rlane) * 4]);
+#pragma unroll
+      for (int w = 1; w < kW8Waves; w++) {
+        const v4f t = *reinterpret_cast<const v4f *>(&red[(((j * TM + rblk) * kW8Waves + w) * kWave + rlane) * 4]);
+        v += t;
+      }
+      const int n = 16 * (cb + j) + (rlane & 15);
+      if (n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (m0 + rrow + r < M) a.y[(size_t)(m0 + rrow + r) * N + n] = v[r] * xsr[r];
+      }
+    }
+    __syncthreads();  // red is rewritten by the next chunk
+  }
+}
+
+// Largest NS (subtiles held per chunk) each TM affords in registers.
+template <int TM> struct W8NS { static constexpr int value = TM >= 4 ? 1 : TM == 2 ? 3 : 6; };
+
+template <int TM, bool TILED>
+static void launch_w4a8_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
+  constexpr int NS = W8NS<TM>::value;
+  const int G = a.Kp / kGroup;
+  if (a.wt16) {
+    if (G % kW8Phase == 0)
+      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, true, true, true>), grid, dim3(kW8Threads), 0, s, a);
+    else
+      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, false, true, true>), grid, dim3(kW8Threads), 0, s, a);
+  } else if (G % kW8Phase == 0) {
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, true, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+  } else if (G % 4 == 0) {
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, false, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+  }
+}
+
+// Per-CU bytes of the (TM) tiling: the workgroup's activation rows plus its share
+// of the weights, with one workgroup per CU.
+static double w4a8_cu_bytes(int tm, int M, int N, int Kp, int cus, int &gx) {
+  const int gy = (M + 16 * tm - 1) / (16 * tm);
+  const int S = (N + 15) / 16;
+  gx = std::max(1, std::min(S, cus / gy));
+  const double spw = (double)((S + gx - 1) / gx);
+  const double wrow = Kp / 2 + (Kp / kGroup) * 5.0;
+  return (double)tm * 16 * Kp + spw * 16 * wrow;
+}
+
+static hipError_t launch_w4a8_gemm(const GemmArgs &a, int num_cus, hipStream_t s) {
+  const int cus = num_cus > 0 ? num_cus : 256;
+  const int mb = (a.M + 15) / 16;
+  int best_tm = 1, best_gx = 1;
+  double best = 1e300;
+  for (int tm : {1, 2, 4}) {
+    if (tm > 1 && tm > mb) break;  // no taller tile than the row blocks there are
+    int gx;
+    const double b = w4a8_cu_bytes(tm, a.M, a.N, a.Kp, cus, gx);
+    if (b < best * 0.97) best = b, best_tm = tm, best_gx = gx;
+  }
+  const dim3 grid(best_gx, (a.M + 16 * best_tm - 1) / (16 * best_tm));
+  if (a.wt16 && !a.tiled) return hipErrorInvalidValue;  // the t16 path reads tiled activations
+  if (a.tiled) {
+    if (best_tm == 1) launch_w4a8_gemm_t<1, true>(a, grid, s);
+    else if (best_tm == 2) launch_w4a8_gemm_t<2, true>(a, grid, s);
+    else launch_w4a8_gemm_t<4, true>(a, grid, s);
+  } else {
+    if (best_tm == 1) launch_w4a8_gemm_t<1, false>(a, grid, s);
+    else if (best_tm == 2) launch_w4a8_gemm_t<2, false>(a, grid, s);
+    else launch_w4a8_gemm_t<4, false>(a, grid, s);
+  }
+  return hipGetLastError();
+}
+
 template <int TM, bool EXPORT, bool TILED>
 static void launch_w4a8_v(const GemmArgs &a, int32_t *out, dim3 grid, hipStream_t s) {
   if ((a.Kp / kGroup) % 4 == 0)
@@ -866,6 +1181,7 @@ static hipError_t launch_w4a8_tm(const GemmArgs &a, int32_t *out, int num_cus, h
 }
 
 hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, int num_cus, hipStream_t s) {
+  if (!out) return launch_w4a8_gemm(a, num_cus, s);
   if (a.M <= 16) return launch_w4a8_tm<1>(a, out, num_cus, s);
   if (a.M <= 32) return launch_w4a8_tm<2>(a, out, num_cus, s);
   if (a.M <= 48) return launch_w4a8_tm<3>(a, out, num_cus, s);
@@ -1081,6 +1397,52 @@ hipError_t launch_groupacc_dot4(const int8_t *xq, const int32_t *asum, int M, in
   if (blocks == 0) blocks = 1;
   hipLaunchKernelGGL(groupacc_dot4_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, xq, asum, M, Kp, qw,
                      zeros, N, out);
+  return hipGetLastError();
+}
+
+// ============================================================ t16 repack
+//
+// One thread per 16-byte lane chunk of qwt (reads the 16 bytes of the row-major
+// matrix it holds, or writes zeros for padding), then one per group entry of
+// st / zt. A one-time layout change of resident weights, not a timed path.
+__global__ __launch_bounds__(kThreads) void repack_int4_t16_kernel(const uint8_t *__restrict__ qw,
+                                                                    const float *__restrict__ scales,
+                                                                    const uint8_t *__restrict__ zeros, int N, int Kp,
+                                                                    uint8_t *__restrict__ qwt, float *__restrict__ st,
+                                                                    uint8_t *__restrict__ zt) {
+  const int G = Kp / kGroup, G4 = t16_groups(Kp);
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const size_t nchunk = t16_qw_bytes(N, Kp) / 16, nent = t16_group_entries(N, Kp);
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < nchunk; t += stride) {
+    const int l = (int)(t % 64), g = (int)((t / 64) % G4);
+    const size_t sub = t / (64 * (size_t)G4);
+    const size_t row = sub * 16 + (l & 15);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < (size_t)N && g < G)
+      v = *reinterpret_cast<const uint4 *>(qw + row * rowbytes + (size_t)g * 64 + (size_t)(l >> 4) * 16);
+    reinterpret_cast<uint4 *>(qwt)[t] = v;
+  }
+  for (size_t e = (size_t)blockIdx.x * kThreads + threadIdx.x; e < nent; e += stride) {
+    // e = ((s * G4/4 + g/4) * 16 + c) * 4 + g % 4
+    const int j = (int)(e % 4), c = (int)((e / 4) % 16);
+    const size_t gq = (e / 64) % (size_t)(G4 / 4), sub = e / (64 * (size_t)(G4 / 4));
+    const size_t row = sub * 16 + c;
+    const int g = (int)(gq * 4) + j;
+    const bool ok = row < (size_t)N && g < G;
+    st[e] = ok ? scales[row * G + g] : 0.0f;
+    if (zt) zt[e] = (ok && zeros) ? zeros[row * G + g] : (uint8_t)0;
+  }
+}
+
+hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                                  uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s) {
+  const size_t work = t16_qw_bytes(N, Kp) / 16;
+  size_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(repack_int4_t16_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, qw, scales, zeros, N, Kp,
+                     qwt, st, zt);
   return hipGetLastError();
 }
 

@@ -112,6 +112,10 @@ SIGNATURES = {
     "lb_graph_launch": ([_vp, _vp], _int),
     "lb_graph_destroy": ([_vp], _int),
     "lbd_copy_kernel": ([_vp, _vp, _sz, _vp], _int),
+    "lbd_gemm_path": ([_int, _int, _int, _pp], _int),
+    "lbd_int4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)], _int),
+    "lbd_repack_int4_t16": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _vp], _int),
+    "lbd_gemm_w4a8_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
 }
 
 
@@ -136,10 +140,12 @@ def _err(rc: int, what: str):
 _LAST = threading.local()
 
 
-def _check(rc: int, what: str) -> int:
+def _check(rc: int, what: str, record: bool = True) -> int:
+    """Raise for rc < 0; a GEMM's rc (record=True) is the path last_path() reports."""
     if rc < 0:
         _err(rc, what)
-    _LAST.rc = rc
+    if record:
+        _LAST.rc = rc
     return rc
 
 
@@ -153,7 +159,7 @@ def device_info() -> dict:
     L = lib()
     name = C.create_string_buffer(64)
     cus, lds = _int(0), _int(0)
-    _check(L.lb_device_info(name, 64, C.byref(cus), C.byref(lds)), "lb_device_info")
+    _check(L.lb_device_info(name, 64, C.byref(cus), C.byref(lds)), "lb_device_info", False)
     return {"arch": name.value.decode(), "compute_units": cus.value, "lds_per_workgroup": lds.value}
 
 
@@ -237,7 +243,7 @@ class DeviceBuffer:
     def __init__(self, nbytes: int):
         self.nbytes = int(nbytes)
         p = _vp()
-        _check(lib().lb_dev_malloc(C.byref(p), max(1, self.nbytes)), "lb_dev_malloc")
+        _check(lib().lb_dev_malloc(C.byref(p), max(1, self.nbytes)), "lb_dev_malloc", False)
         self.ptr = p.value
 
     @classmethod
@@ -245,13 +251,13 @@ class DeviceBuffer:
         a = np.ascontiguousarray(a)
         b = cls(a.nbytes)
         if a.nbytes:
-            _check(lib().lb_memcpy_h2d(b.ptr, a.ctypes.data, a.nbytes), "lb_memcpy_h2d")
+            _check(lib().lb_memcpy_h2d(b.ptr, a.ctypes.data, a.nbytes), "lb_memcpy_h2d", False)
         return b
 
     def to_array(self, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)
         if out.nbytes:
-            _check(lib().lb_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "lb_memcpy_d2h")
+            _check(lib().lb_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "lb_memcpy_d2h", False)
         return out
 
     def __del__(self):
@@ -265,7 +271,13 @@ class DeviceBuffer:
 
 @dataclass
 class DeviceInt4Weights:
-    """int4 g128 weights resident in HBM (same layout as Int4Weights)."""
+    """int4 g128 weights resident in HBM (same layout as Int4Weights).
+
+    `t16` is the matrix-core tile layout of the same matrix (include/lowbit_hip.h,
+    lbd_repack_int4_t16), built on the device the first time a GEMM takes the
+    matrix-core path and kept beside the row-major copy, which the decode kernels
+    read.
+    """
     qw: DeviceBuffer
     scales: DeviceBuffer
     zeros: DeviceBuffer | None
@@ -273,6 +285,23 @@ class DeviceInt4Weights:
     kp: int
     k: int
     nbytes: int
+    t16: tuple | None = None
+
+    def tiles(self) -> tuple:
+        """(qwt, st, zt or None) in the t16 layout, repacked on first use."""
+        if self.t16 is None:
+            L = lib()
+            bq, bs, bz = _sz(0), _sz(0), _sz(0)
+            _check(L.lbd_int4_t16_bytes(self.n, self.kp, C.byref(bq), C.byref(bs), C.byref(bz)),
+                   "lbd_int4_t16_bytes", False)
+            qwt, st = DeviceBuffer(bq.value), DeviceBuffer(bs.value)
+            zt = None if self.zeros is None else DeviceBuffer(bz.value)
+            _check(L.lbd_repack_int4_t16(self.qw.ptr, self.scales.ptr,
+                                         None if self.zeros is None else self.zeros.ptr, self.n, self.kp,
+                                         qwt.ptr, st.ptr, None if zt is None else zt.ptr, None),
+                   "lbd_repack_int4_t16", False)
+            self.t16 = (qwt, st, zt)
+        return self.t16
 
 
 @dataclass
@@ -315,8 +344,13 @@ def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
         rc = L.lbd_gemm_mxfp4(dx.ptr, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, dy.ptr, C.byref(prm), None)
     else:
         ws = DeviceBuffer(L.lbd_w4a8_workspace_bytes(m, w.kp))
-        rc = L.lbd_gemm_w4a8(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm),
-                             ws.ptr, ws.nbytes, None)
+        if _check(L.lbd_gemm_path(KIND_IDS["w4a8"], m, w.kp, C.byref(prm)), "lbd_gemm_path", False) == ISA_GFX950_MFMA:
+            qwt, st, zt = w.tiles()
+            rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n,
+                                     dy.ptr, C.byref(prm), ws.ptr, ws.nbytes, None)
+        else:
+            rc = L.lbd_gemm_w4a8(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm),
+                                 ws.ptr, ws.nbytes, None)
     _check(rc, f"lbd_gemm_{kind}")
     pr.y[...] = dy.to_array(pr.y.shape, np.float32)  # synchronous copy on the null stream
     return pr.y

@@ -115,3 +115,24 @@ def test_no_device_reports_unavailable():
     L = K.lib()
     assert L.lb_cpu_isa() == -4
     assert K.cpu_info()["cpu_isa"] == "none"
+
+
+def test_t16_sizes_and_argument_checks():
+    """t16 array sizes (S = ceil(N/16) subtiles, groups padded to a multiple of 4) and
+    the shape / argument errors of the repack and GEMM entry points, before any
+    device work."""
+    L = K.lib()
+    bq, bs, bz = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+    assert L.lbd_int4_t16_bytes(17, 256, C.byref(bq), C.byref(bs), C.byref(bz)) == 0
+    assert (bq.value, bs.value, bz.value) == (2 * 4 * 1024, 2 * 16 * 4 * 4, 2 * 16 * 4)
+    assert L.lbd_int4_t16_bytes(11008, 4096, C.byref(bq), C.byref(bs), C.byref(bz)) == 0
+    assert bq.value == 11008 * 2048 and bs.value == 11008 * 32 * 4 and bz.value == 11008 * 32
+    assert L.lbd_int4_t16_bytes(17, 200, C.byref(bq), None, None) == -1   # Kp % 128
+    assert L.lbd_int4_t16_bytes(0, 256, None, None, None) == -1
+    assert L.lbd_repack_int4_t16(None, None, None, 16, 256, None, None, None, None) == -6
+    prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
+    assert L.lbd_gemm_w4a8_t16(None, 1, 256, None, None, None, 16, None, C.byref(prm), None, 0, None) == -6
+    assert L.lbd_gemm_w4a8_t16(None, 0, 256, None, None, None, 16, None, C.byref(prm), None, 0, None) == -1
+    assert L.lbd_gemm_path(2, 1, 4096, C.byref(prm)) == K.ISA_GFX950
+    assert L.lbd_gemm_path(2, 64, 4096, C.byref(prm)) == K.ISA_GFX950_MFMA
+    assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6

@@ -163,9 +163,12 @@ def _random_int4(rng, n, kp, asym):
 
 # Shapes that give the persistent MFMA kernel several 16-row weight subtiles per
 # workgroup (N = 11008), more than one pass of subtiles and more than one phase of
-# 32 groups (N = 33000, K = 4352: G = 34, not a multiple of 4), and M tails.
+# 32 groups (N = 33000, K = 4352: G = 34, not a multiple of 4), and M tails. The
+# row-block height follows the shape: 16 rows (M = 16, 17), 32 rows (M = 40, 64 at
+# N = 11008) and 64 rows (M = 64 at N = 33000).
 BIG = [(64, 11008, 4096, True), (40, 11008, 4096, False), (16, 11008, 4096, True),
-       (17, 33000, 4352, True), (70, 4100, 4352, False)]
+       (17, 33000, 4352, True), (70, 4100, 4352, False), (64, 33000, 4352, True),
+       (64, 33000, 4096, False)]
 
 
 @pytest.mark.parametrize("m,n,kp,asym", BIG)
