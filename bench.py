@@ -152,28 +152,46 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
     ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp)
     ws = K.DeviceBuffer(ws_bytes)
     s = dev.stream
-    # W4A8 on the matrix cores reads the t16 tile layout (a one-time device repack of
+    # the matrix-core regime reads the t16 tile layout (a one-time device repack of
     # each resident copy, as lowbit_amd.to_device handles do; not timed)
     layout = "row-major"
-    if fmt == "w4a8" and L.lbd_gemm_path(2, m, W.kp, C.byref(prm)) == K.ISA_GFX950_MFMA:
+    if L.lbd_gemm_path({"w4a16": 0, "mxfp4": 1, "w4a8": 2}[fmt], m, W.kp, C.byref(prm)) == K.ISA_GFX950_MFMA:
         layout = "t16"
-        bq, bs, bz = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
-        dev.check(L.lbd_int4_t16_bytes(n, W.kp, C.byref(bq), C.byref(bs), C.byref(bz)), "t16 sizes")
         tiled = []
-        for b in pool:
-            qwt, st = K.DeviceBuffer(bq.value), K.DeviceBuffer(bs.value)
-            zt = K.DeviceBuffer(bz.value) if len(b) > 2 else None
-            dev.check(L.lbd_repack_int4_t16(b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None, n, W.kp,
-                                            qwt.ptr, st.ptr, zt.ptr if zt else None, s), "t16 repack")
-            tiled.append((qwt, st, zt))
+        if fmt == "mxfp4":
+            bq, be = C.c_size_t(0), C.c_size_t(0)
+            dev.check(L.lbd_mxfp4_t16_bytes(n, W.kp, C.byref(bq), C.byref(be)), "t16 sizes")
+            for b in pool:
+                qwt, et = K.DeviceBuffer(bq.value), K.DeviceBuffer(be.value)
+                dev.check(L.lbd_repack_mxfp4_t16(b[0].ptr, b[1].ptr, n, W.kp, qwt.ptr, et.ptr, s), "t16 repack")
+                tiled.append((qwt, et))
+        else:
+            bq, bs, bz = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
+            dev.check(L.lbd_int4_t16_bytes(n, W.kp, C.byref(bq), C.byref(bs), C.byref(bz)), "t16 sizes")
+            for b in pool:
+                qwt, st = K.DeviceBuffer(bq.value), K.DeviceBuffer(bs.value)
+                zt = K.DeviceBuffer(bz.value) if len(b) > 2 else None
+                dev.check(L.lbd_repack_int4_t16(b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None, n, W.kp,
+                                                qwt.ptr, st.ptr, zt.ptr if zt else None, s), "t16 repack")
+                tiled.append((qwt, st, zt))
         dev.check(L.lb_stream_synchronize(s), "sync")
         pool = tiled
+        if fmt != "w4a8":
+            ws_bytes = L.lbd_bf16x3_workspace_bytes(m, W.kp)
+            ws = K.DeviceBuffer(ws_bytes)
 
     def launch(i):
         b = pool[i % len(pool)]
         if layout == "t16":
-            rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n, dy.ptr,
-                                     C.byref(prm), ws.ptr, ws_bytes, s)
+            if fmt == "w4a8":
+                rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
+                                         dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
+            elif fmt == "w4a16":
+                rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
+                                          dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
+            else:
+                rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, n, dy.ptr, C.byref(prm), ws.ptr,
+                                          ws_bytes, s)
         elif fmt == "w4a16":
             rc = L.lbd_gemm_w4a16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None,
                                   n, dy.ptr, C.byref(prm), s)

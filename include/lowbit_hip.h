@@ -184,6 +184,27 @@ int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                       const float *st, const uint8_t *zt, int N, float *y,
                       const lb_params *p, void *workspace,
                       size_t workspace_bytes, void *stream);
+/* y = x . w^T as lbd_gemm_w4a16, weights in the t16 layout, on bf16 matrix cores
+ * with the float32 semantics of the reference's kernels (src/lowbit/csrc/
+ * kern_scalar.c:10-47): x is split exactly into three bf16 terms (in `workspace`,
+ * lbd_bf16x3_workspace_bytes(M, Kp) bytes, 256-byte aligned, or NULL for the
+ * per-thread buffer) and every weight is exact in bf16, so each product is an
+ * exact float32 value and the sums are float32. Always the matrix-core path. */
+int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt,
+                       const float *st, const uint8_t *zt, int N, float *y,
+                       const lb_params *p, void *workspace,
+                       size_t workspace_bytes, void *stream);
+size_t lbd_bf16x3_workspace_bytes(int M, int Kp);
+/* MXFP4 in the t16 order: qwt as above (lane 16q + c of tile (s, g) holds block
+ * 4g + q of row 16s + c), et [S][G4][64] the E8M0 byte of that block (G = ceil(Kp/128)) */
+int lbd_mxfp4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *et_bytes);
+int lbd_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N, int Kp,
+                         uint8_t *qwt, uint8_t *et, void *stream);
+/* y = x . w^T as lbd_gemm_mxfp4 on t16 weights, the bf16 matrix-core path of
+ * lbd_gemm_w4a16_t16 (block scales 2^(e - 127) exact; E8M0 255 gives NaN) */
+int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt,
+                       const uint8_t *et, int N, float *y, const lb_params *p,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- device plumbing for the ctypes layer and benchmarks ---- */
 int lb_dev_malloc(void **ptr, size_t bytes);

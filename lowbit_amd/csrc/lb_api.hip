@@ -223,9 +223,9 @@ size_t w4a8_ws_bytes(int M, int Kp) {
   return align256(lbk::tiled_xq_bytes(M, Kp)) + align256((size_t)M * 4) + align256(lbk::tiled_asum_bytes(M, Kp));
 }
 
-// The caller's workspace (checked) or, when it passed none, the per-thread buffer.
-int w4a8_workspace(int M, int Kp, size_t given_bytes, hipStream_t s, char **ws) {
-  const size_t need = w4a8_ws_bytes(M, Kp);
+// The caller's workspace of `need` bytes (checked) or, when it passed none, the
+// per-thread buffer.
+int take_workspace(size_t need, size_t given_bytes, hipStream_t s, char **ws) {
   if (*ws) {
     if (given_bytes < need) return fail(LB_ERR_ARG, "workspace too small");
     if ((reinterpret_cast<uintptr_t>(*ws) & 255) != 0) return fail(LB_ERR_ARG, "workspace must be 256-byte aligned");
@@ -236,6 +236,32 @@ int w4a8_workspace(int M, int Kp, size_t given_bytes, hipStream_t s, char **ws) 
   if (rc < 0) return rc;
   if ((rc = grow(&c->ws, &c->ws_cap, need, s)) < 0) return rc;
   *ws = c->ws;
+  return 0;
+}
+
+int w4a8_workspace(int M, int Kp, size_t given_bytes, hipStream_t s, char **ws) {
+  return take_workspace(w4a8_ws_bytes(M, Kp), given_bytes, s, ws);
+}
+
+// bf16x3 GEMM on t16 weights: split the activations into `ws`, then the GEMM.
+int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  lbk::GemmArgs a = a0;
+  a.x3 = reinterpret_cast<const uint4 *>(ws);
+  hipError_t e = lbk::launch_split3(fmt, a.x, a.M, a.Kp, reinterpret_cast<uint4 *>(ws), s);
+  if (e != hipSuccess) return fail_hip(e, "activation split launch");
+  e = lbk::launch_bf3_gemm(fmt, a, cus, s);
+  if (e != hipSuccess) return fail_hip(e, "bf16x3 GEMM launch");
+  return ok(LB_ISA_GFX950_MFMA);
+}
+
+// Shared checks of the t16 GEMM entry points (32-bit offsets inside the kernels).
+int check_t16(int M, int Kp, int N) {
+  if ((size_t)M * Kp * 4 > 0xFFFFFFF0u || lbk::x3_bytes(M, Kp) > 0xFFFFFFF0u)
+    return fail(LB_ERR_SHAPE, "activations above 4 GiB");
+  if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
   return 0;
 }
 
@@ -430,6 +456,68 @@ int lbd_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *z
                                              static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail_hip(e, "t16 repack launch");
   return ok(0);
+}
+
+size_t lbd_bf16x3_workspace_bytes(int M, int Kp) {
+  if (M <= 0 || Kp <= 0) return 0;
+  return lbk::x3_bytes(M, Kp);
+}
+
+int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
+                       int N, float *y, const lb_params *p, void *workspace, size_t workspace_bytes,
+                       void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qwt || !st || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qwt)) return fail(LB_ERR_ARG, "x and qwt must be 16-byte aligned");
+  if ((rc = check_t16(M, Kp, N)) < 0) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qwt; a.scales = st; a.zeros = zt; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  a.wt16 = true;
+  char *ws = static_cast<char *>(workspace);
+  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
+  return run_bf3(lbk::F_W4A16, a, ws, s);
+}
+
+int lbd_mxfp4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *et_bytes) {
+  int rc = check_shape(1, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if (qwt_bytes) *qwt_bytes = lbk::t16_qw_bytes(N, Kp);
+  if (et_bytes) *et_bytes = lbk::t16_e8m0_bytes(N, Kp);
+  return ok(0);
+}
+
+int lbd_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N, int Kp, uint8_t *qwt, uint8_t *et,
+                         void *stream) {
+  int rc = check_shape(1, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if (!qw || !e8m0 || !qwt || !et) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(qw) || !aligned16(qwt)) return fail(LB_ERR_ARG, "qw and qwt must be 16-byte aligned");
+  if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
+  hipError_t e = lbk::launch_repack_mxfp4_t16(qw, e8m0, N, Kp, qwt, et, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "t16 repack launch");
+  return ok(0);
+}
+
+int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt, const uint8_t *et, int N, float *y,
+                       const lb_params *p, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qwt || !et || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qwt)) return fail(LB_ERR_ARG, "x and qwt must be 16-byte aligned");
+  if ((rc = check_t16(M, Kp, N)) < 0) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qwt; a.e8m0 = et; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  a.wt16 = true;
+  char *ws = static_cast<char *>(workspace);
+  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
+  return run_bf3(lbk::F_MXFP4, a, ws, s);
 }
 
 int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,

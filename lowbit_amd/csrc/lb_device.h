@@ -15,6 +15,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- reductions
 //
@@ -130,6 +132,31 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
 template <int SEL>
 __device__ __forceinline__ v2f e2m1_pair(uint32_t w, float scale) {
   return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, SEL);
+}
+
+// ---------------------------------------------------------------- bf16 terms
+//
+// Round-to-nearest-even of x to bf16, returned as the float32 bit pattern with the
+// low 16 bits clear (so it is also the float value of the bf16). Finite x up to the
+// largest bf16 below 2^128; NaN stays NaN.
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+}
+
+// x = hi + mid + lo exactly for normal x (each term keeps 8 significant bits and
+// each remainder is exact in float32), as three float32 bit patterns.
+__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+  hi = bf16_rne(x);
+  const float r1 = x - __uint_as_float(hi);
+  mid = bf16_rne(r1);
+  lo = bf16_rne(r1 - __uint_as_float(mid));
+}
+
+// Two float32 values whose low 16 bits are zero (or may be dropped exactly) ->
+// bf16x2 with `a` in the low half.
+__device__ __forceinline__ uint32_t pack_bf16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
 // ---------------------------------------------------------------- int8 quantizer

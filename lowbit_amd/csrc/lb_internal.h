@@ -22,8 +22,9 @@ struct GemmArgs {
   const uint8_t *e8m0 = nullptr;  // [N, Kp/32]
   float *y = nullptr;             // [M, N]
   int M = 0, Kp = 0, N = 0;
+  const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path)
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
-  bool wt16 = false;              // qw / scales / zeros in the MFMA tile layout (t16)
+  bool wt16 = false;              // qw / scales / zeros / e8m0 in the MFMA tile layout (t16)
 };
 
 // MFMA tile layout ("t16") of int4 g128 weights, a device-private copy of the
@@ -34,9 +35,21 @@ struct GemmArgs {
 //   st   [S][G4/4][16][4]   fp32 scale of row 16s + c, group 4 (g/4) + g%4
 //   zt   [S][G4/4][16][4]   uint8 zero-point, same order (absent for z = 8)
 // Rows past N and groups past G are zero (zero codes, scale 0, zero-point 0).
-__host__ __device__ inline int t16_groups(int Kp) { return ((Kp / 128) + 3) & ~3; }
+// MXFP4 weights use the same qwt order (the 16 bytes of lane (q, c) in group g are
+// block 4g + q of row 16s + c) with G = ceil(Kp/128) and
+//   et   [S][G4][64]        uint8 E8M0 exponent of that block (lane order)
+__host__ __device__ inline int t16_groups(int Kp) { return (((Kp + 127) / 128) + 3) & ~3; }
 __host__ __device__ inline size_t t16_qw_bytes(int N, int Kp) { return (size_t)((N + 15) / 16) * t16_groups(Kp) * 1024; }
 __host__ __device__ inline size_t t16_group_entries(int N, int Kp) { return (size_t)((N + 15) / 16) * 16 * t16_groups(Kp); }
+__host__ __device__ inline size_t t16_e8m0_bytes(int N, int Kp) { return (size_t)((N + 15) / 16) * t16_groups(Kp) * 64; }
+hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N, int Kp, uint8_t *qwt, uint8_t *et,
+                                   hipStream_t s);
+// bf16x3 path (W4A16 / MXFP4 on bf16 matrix cores, fp32-exact products): the
+// activations as three bf16 terms in the A-operand tile order, and the GEMM on t16
+// weights. Bytes of the split activations for M rows:
+__host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
+hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
+hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
 hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
                                   uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s);
 

@@ -1188,6 +1188,272 @@ hipError_t launch_w4a8_mfma(const GemmArgs &a, int32_t *out, int num_cus, hipStr
   return launch_w4a8_tm<4>(a, out, num_cus, s);
 }
 
+// ============================================================ W4A16 / MXFP4, bf16x3 MFMA
+//
+// fp32 semantics on bf16 matrix cores. Each activation is split into three bf16
+// terms, x = hi + mid + lo exactly; each weight is exact in bf16 (W4A16: the integer
+// q - z in [-15, 15]; MXFP4: E2M1 times a power of two). Every product of
+// v_mfma_f32_16x16x32_bf16 is therefore an exact float32 value and the sums are
+// float32, as in the reference's fp32 kernels; three bf16 MFMAs per product run at
+// 16x the fp32 MFMA rate each (2.5 PFLOP/s against 157 TFLOP/s dense).
+//
+// Operand slots (lane l = 16q + c, 8 bf16 per operand, slot s = 0..7, u = 0..3 the
+// four 32-wide MFMAs of a 128-element group g); A and B agree slot by slot:
+//   W4A16: weight bytes [64g + 16q, +16) of row c (t16 tile): u = 0/1 low nibbles of
+//          bytes 0-7 / 8-15, u = 2/3 high nibbles; element 128g + 64 (u>>1) + 16q +
+//          8 (u&1) + s.
+//   MXFP4: the lane's 16 bytes are block b = 4g + q; u takes bytes 4u .. 4u+3, each
+//          byte giving (low, high) nibble = elements (32b + j, 32b + 16 + j): slot s
+//          is element 32b + 4u + (s>>1) + 16 (s&1).
+// The split activations are tiled [row block][group][u][term][lane][16 B], so a
+// wave reads every operand with one contiguous 1 KiB load.
+
+template <int F>
+__global__ __launch_bounds__(kThreads) void split3_kernel(const float *__restrict__ x, int M, int Kp,
+                                                          uint4 *__restrict__ x3) {
+  const int G = (Kp + 127) / 128, mblocks = (M + 15) / 16;
+  const size_t total = (size_t)mblocks * G * 4 * kWave;
+  const Rsrc rx = make_rsrc(x, (uint32_t)((size_t)M * Kp * 4));
+  for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+    const int lane = (int)(t % kWave), u = (int)((t / kWave) % 4);
+    const size_t gi = t / (4 * kWave);  // row block * G + group
+    const int g = (int)(gi % G), mb = (int)(gi / G);
+    const int row = 16 * mb + (lane & 15), q = lane >> 4;
+    float v[8];
+    if constexpr (F == F_W4A16) {
+      const int e0 = 128 * g + 64 * (u >> 1) + 16 * q + 8 * (u & 1);
+      const bool ok = row < M;  // Kp % 128 == 0
+      const uint32_t off = (uint32_t)(((size_t)row * Kp + e0) * 4);
+      const float4 lo = ld_f4(rx, ok ? off : 0xFFFFFFF0u), hi = ld_f4(rx, ok ? off + 16 : 0xFFFFFFF0u);
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    } else {
+      const int b = 4 * g + q, e0 = 32 * b + 4 * u;
+      const bool ok = row < M && 32 * b < Kp;
+      const uint32_t off = (uint32_t)(((size_t)row * Kp + e0) * 4);
+      const float4 lo = ld_f4(rx, ok ? off : 0xFFFFFFF0u), hi = ld_f4(rx, ok ? off + 64 : 0xFFFFFFF0u);
+      v[0] = lo.x; v[1] = hi.x; v[2] = lo.y; v[3] = hi.y;
+      v[4] = lo.z; v[5] = hi.z; v[6] = lo.w; v[7] = hi.w;
+    }
+    uint32_t th[8], tm[8], tl[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) split3(v[k], th[k], tm[k], tl[k]);
+    uint4 *dst = x3 + (gi * 4 + u) * 3 * kWave + lane;
+    dst[0] = make_uint4(pack_bf16(th[0], th[1]), pack_bf16(th[2], th[3]), pack_bf16(th[4], th[5]), pack_bf16(th[6], th[7]));
+    dst[kWave] = make_uint4(pack_bf16(tm[0], tm[1]), pack_bf16(tm[2], tm[3]), pack_bf16(tm[4], tm[5]), pack_bf16(tm[6], tm[7]));
+    dst[2 * kWave] = make_uint4(pack_bf16(tl[0], tl[1]), pack_bf16(tl[2], tl[3]), pack_bf16(tl[4], tl[5]), pack_bf16(tl[6], tl[7]));
+  }
+}
+
+hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s) {
+  const size_t work = (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * kWave;
+  size_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 16384) blocks = 16384;
+  if (fmt == F_W4A16)
+    hipLaunchKernelGGL(split3_kernel<F_W4A16>, dim3((unsigned)blocks), dim3(kThreads), 0, s, x, M, Kp, x3);
+  else
+    hipLaunchKernelGGL(split3_kernel<F_MXFP4>, dim3((unsigned)blocks), dim3(kThreads), 0, s, x, M, Kp, x3);
+  return hipGetLastError();
+}
+
+// Weight stage of one subtile: the lane's 16 bytes of the group's tile and, for
+// W4A16, its row's scale and zero-point; for MXFP4, the E8M0 byte of its block.
+struct B3Stage {
+  uint4 w;
+  float s;
+  uint32_t z;
+};
+
+// Four float32 of (byte k of nib) - zf as two bf16x2 (exact: integers below 16).
+__device__ __forceinline__ void w4_bf16x4(uint32_t nib, float zf, uint32_t &d0, uint32_t &d1) {
+  const uint32_t n = opaque(nib);
+  const float f0 = (float)(n & 0xFF) - zf, f1 = (float)((n >> 8) & 0xFF) - zf;
+  const float f2 = (float)((n >> 16) & 0xFF) - zf, f3 = (float)(n >> 24) - zf;
+  d0 = pack_bf16(__float_as_uint(f0), __float_as_uint(f1));
+  d1 = pack_bf16(__float_as_uint(f2), __float_as_uint(f3));
+}
+
+constexpr int kB3PF = 3;  // weight subtiles in flight ahead of the one computed
+
+// Waves split the K groups (wave w takes group 8 ph + w of phase ph) and keep
+// their activation operands (4 x 3 x TM x 1 KiB) in registers across the
+// workgroup's subtiles; per subtile and row block, 12 MFMAs accumulate the group
+// (W4A16) or the four blocks (MXFP4) and one FMA per output applies the fp32
+// factor. Partial tiles are reduced across waves in LDS once per chunk of NS
+// subtiles, in a fixed order.
+template <int F, int TM, int NS>
+__global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
+  __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int q = lane >> 4, c = lane & 15;
+  const int M = a.M, N = a.N, Kp = a.Kp, G = (Kp + 127) / 128, G4 = t16_groups(Kp);
+  const int mb0 = blockIdx.y * TM, m0 = mb0 * 16;
+  const int S = (N + 15) / 16;
+  const int sbase = (int)((unsigned)S / gridDim.x), srem = S - sbase * (int)gridDim.x;
+  const int bx = blockIdx.x;
+  const int sb = bx * sbase + min(bx, srem), se = sb + sbase + (bx < srem ? 1 : 0);
+  const int nph = (G + kW8Waves - 1) / kW8Waves;
+
+  const Rsrc rx = make_rsrc(a.x3, (uint32_t)min(x3_bytes(M, Kp), (size_t)0xFFFFFFF0u));
+  const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(t16_qw_bytes(N, Kp), (size_t)0xFFFFFFF0u));
+  const size_t gents = t16_group_entries(N, Kp);
+  const Rsrc rs = make_rsrc(F == F_W4A16 ? (const void *)a.scales : (const void *)a.e8m0,
+                            F == F_W4A16 ? (uint32_t)(gents * 4) : (uint32_t)t16_e8m0_bytes(N, Kp));
+  const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, (F == F_W4A16 && a.zeros) ? (uint32_t)gents : 0u);
+  const int zadd = (F == F_W4A16 && !a.zeros) ? 8 : 0;
+
+  v4u xa[4][3][TM];
+  for (int cb = sb; cb < se; cb += NS) {
+    const int ce = min(cb + NS, se);
+    v4f facc[NS][TM];
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++) facc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int ph = 0; ph < nph; ph++) {
+      const int g = ph * kW8Waves + wave;
+      if (g >= G) continue;  // wave-uniform: this wave has no group in the last phase
+      auto load = [&](B3Stage &st, int j) {
+        const int sj = cb + j;
+        const bool in = j < NS && sj < ce;  // past the chunk: zero-length reads
+        const uint32_t tile = (uint32_t)sj * G4 + g;
+        st.w = ld_b128(rw, in ? (tile * kWave + lane) * 16u : 0xFFFFFFF0u);
+        if constexpr (F == F_W4A16) {
+          const uint32_t ge = (((uint32_t)sj * (G4 / 4) + g / 4) * 16 + c) * 4 + (g & 3);
+          st.s = ld_f32(rs, in ? ge * 4u : 0xFFFFFFF0u);
+          st.z = ld_u8(rz, in ? ge : 0xFFFFFFF0u) + zadd;
+        } else {
+          st.s = 0.0f;
+          st.z = ld_u8(rs, in ? tile * kWave + lane : 0xFFFFFFF0u);
+        }
+      };
+      B3Stage st[kB3PF + 1];
+#pragma unroll
+      for (int j = 0; j <= kB3PF; j++) load(st[j], j);
+      if (nph > 1 || cb == sb) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+          for (int p = 0; p < 3; p++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+              // row blocks past the last one read zeros (past the descriptor)
+              const uint32_t off = ((((uint32_t)(mb0 + i) * G + g) * 4 + u) * 3 + p) * kWave * 16 + lane * 16;
+              const uint4 v = ld_b128(rx, off);
+              xa[u][p][i] = v4u{v.x, v.y, v.z, v.w};
+            }
+      }
+#pragma unroll
+      for (int j = 0; j < NS; j++) {
+        if (cb + j >= ce) break;  // workgroup-uniform
+        B3Stage &cur = st[j % (kB3PF + 1)];
+        v4u b[4];
+        float fs;
+        if constexpr (F == F_W4A16) {
+          const float zf = (float)(int)cur.z;
+          const uint32_t wd[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
+#pragma unroll
+          for (int h = 0; h < 2; h++)  // u = h: low nibbles of bytes 8h .. 8h+7; u = 2 + h: high nibbles
+#pragma unroll
+            for (int d = 0; d < 2; d++) {
+              uint32_t x0, x1;
+              w4_bf16x4(lo_nibbles(wd[2 * h + d]), zf, x0, x1);
+              b[h][2 * d] = x0;
+              b[h][2 * d + 1] = x1;
+              w4_bf16x4(hi_nibbles(wd[2 * h + d]), zf, x0, x1);
+              b[2 + h][2 * d] = x0;
+              b[2 + h][2 * d + 1] = x1;
+            }
+          fs = cur.s;
+        } else {
+          // the MFMA sums the four blocks of group g of row c (lanes c, c+16, c+32,
+          // c+48): each block's codes carry 2^(e - emax), exact in bf16 down to
+          // 2^-126; the fp32 factor 2^(emax - 127) (NaN for 255) follows the MFMA
+          const int e = (int)cur.z;
+          int emax = max(e, __shfl_xor(e, 16));
+          emax = max(emax, __shfl_xor(emax, 32));
+          const int dexp = e - emax;
+          const float bs = dexp >= -126 ? __uint_as_float((uint32_t)(dexp + 127) << 23) : 0.0f;
+          const uint32_t wd[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            b[u][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[u], bs, 0));
+            b[u][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[u], bs, 1));
+            b[u][2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[u], bs, 2));
+            b[u][3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd[u], bs, 3));
+          }
+          fs = e8m0_to_f32((uint32_t)emax);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          v4f dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+              dacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[u][p][i]),
+                                                             __builtin_bit_cast(v8bf, b[u]), dacc, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; r++) facc[j][i][r] = __builtin_fmaf(fs, dacc[r], facc[j][i][r]);
+        }
+        if (j + kB3PF + 1 < NS) load(cur, j + kB3PF + 1);
+      }
+    }
+    // ---- reduce the waves' partial tiles of the chunk and store
+#pragma unroll
+    for (int j = 0; j < NS; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) = facc[j][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < (ce - cb) * TM * kWave; e += kW8Threads) {
+      const int l = e % kWave, i = (e / kWave) % TM, j = e / (kWave * TM);
+      v4f v = *reinterpret_cast<const v4f *>(&red[(((j * TM + i) * kW8Waves + 0) * kWave + l) * 4]);
+#pragma unroll
+      for (int w = 1; w < kW8Waves; w++) {
+        const v4f t = *reinterpret_cast<const v4f *>(&red[(((j * TM + i) * kW8Waves + w) * kWave + l) * 4]);
+        v += t;
+      }
+      const int n = 16 * (cb + j) + (l & 15), lr = 16 * i + 4 * (l >> 4);
+      if (n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (m0 + lr + r < M) a.y[(size_t)(m0 + lr + r) * N + n] = v[r];
+      }
+    }
+    __syncthreads();  // red is rewritten by the next chunk
+  }
+}
+
+template <int TM> struct B3NS { static constexpr int value = TM >= 2 ? 4 : 8; };
+
+template <int F, int TM>
+static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
+  constexpr int NS = B3NS<TM>::value;
+  const int gy = (a.M + 16 * TM - 1) / (16 * TM), S = (a.N + 15) / 16;
+  const int gx = std::max(1, std::min(S, cus / gy));
+  hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, NS>), dim3(gx, gy), dim3(kW8Threads), 0, s, a);
+}
+
+hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
+  const int cus = num_cus > 0 ? num_cus : 256;
+  if (!a.x3 || !a.wt16) return hipErrorInvalidValue;
+  // 32-row blocks halve the weight decode per output once there are two row blocks
+  const bool tall = a.M > 16;
+  if (fmt == F_W4A16) {
+    if (tall) launch_bf3_t<F_W4A16, 2>(a, cus, s);
+    else launch_bf3_t<F_W4A16, 1>(a, cus, s);
+  } else if (fmt == F_MXFP4) {
+    if (tall) launch_bf3_t<F_MXFP4, 2>(a, cus, s);
+    else launch_bf3_t<F_MXFP4, 1>(a, cus, s);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // ============================================================ W4A16 / MXFP4, fp32 MFMA
 //
 // K is walked in chunks of 128 elements (one int4 group, or four MXFP4 blocks);
@@ -1433,6 +1699,39 @@ __global__ __launch_bounds__(kThreads) void repack_int4_t16_kernel(const uint8_t
     st[e] = ok ? scales[row * G + g] : 0.0f;
     if (zt) zt[e] = (ok && zeros) ? zeros[row * G + g] : (uint8_t)0;
   }
+}
+
+// MXFP4: the same qwt order over rows of Kp/2 bytes (a multiple of 16; chunks past
+// the row are zero), then the E8M0 byte of each lane's block in lane order.
+__global__ __launch_bounds__(kThreads) void repack_mxfp4_t16_kernel(const uint8_t *__restrict__ qw,
+                                                                     const uint8_t *__restrict__ e8m0, int N, int Kp,
+                                                                     uint8_t *__restrict__ qwt,
+                                                                     uint8_t *__restrict__ et) {
+  const int G4 = t16_groups(Kp), B = Kp / kMxBlock;
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const size_t nchunk = t16_qw_bytes(N, Kp) / 16;  // = entries of et
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < nchunk; t += stride) {
+    const int l = (int)(t % 64), g = (int)((t / 64) % G4);
+    const size_t sub = t / (64 * (size_t)G4);
+    const size_t row = sub * 16 + (l & 15);
+    const int blk = 4 * g + (l >> 4);
+    const bool ok = row < (size_t)N && blk < B;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (ok) v = *reinterpret_cast<const uint4 *>(qw + row * rowbytes + (size_t)blk * 16);
+    reinterpret_cast<uint4 *>(qwt)[t] = v;
+    et[t] = ok ? e8m0[row * B + blk] : (uint8_t)0;
+  }
+}
+
+hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N, int Kp, uint8_t *qwt, uint8_t *et,
+                                   hipStream_t s) {
+  const size_t work = t16_qw_bytes(N, Kp) / 16;
+  size_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(repack_mxfp4_t16_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, qw, e8m0, N, Kp, qwt, et);
+  return hipGetLastError();
 }
 
 hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,

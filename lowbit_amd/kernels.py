@@ -116,6 +116,11 @@ SIGNATURES = {
     "lbd_int4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_int4_t16": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _vp], _int),
     "lbd_gemm_w4a8_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_gemm_w4a16_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_bf16x3_workspace_bytes": ([_int, _int], _sz),
+    "lbd_mxfp4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
+    "lbd_repack_mxfp4_t16": ([_vp, _vp, _int, _int, _vp, _vp, _vp], _int),
+    "lbd_gemm_mxfp4_t16": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
 }
 
 
@@ -306,13 +311,27 @@ class DeviceInt4Weights:
 
 @dataclass
 class DeviceMXFP4Weights:
-    """MXFP4 weights resident in HBM (same layout as MXFP4Weights)."""
+    """MXFP4 weights resident in HBM (same layout as MXFP4Weights); `t16` as for
+    DeviceInt4Weights (lbd_repack_mxfp4_t16)."""
     qw: DeviceBuffer
     e8m0: DeviceBuffer
     n: int
     kp: int
     k: int
     nbytes: int
+    t16: tuple | None = None
+
+    def tiles(self) -> tuple:
+        """(qwt, et) in the t16 layout, repacked on first use."""
+        if self.t16 is None:
+            L = lib()
+            bq, be = _sz(0), _sz(0)
+            _check(L.lbd_mxfp4_t16_bytes(self.n, self.kp, C.byref(bq), C.byref(be)), "lbd_mxfp4_t16_bytes", False)
+            qwt, et = DeviceBuffer(bq.value), DeviceBuffer(be.value)
+            _check(L.lbd_repack_mxfp4_t16(self.qw.ptr, self.e8m0.ptr, self.n, self.kp, qwt.ptr, et.ptr, None),
+                   "lbd_repack_mxfp4_t16", False)
+            self.t16 = (qwt, et)
+        return self.t16
 
 
 def to_device(w):
@@ -338,13 +357,25 @@ def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
     dx = DeviceBuffer.from_array(pr.x)
     dy = DeviceBuffer(pr.y.nbytes)
     zp = None if getattr(w, "zeros", None) is None else w.zeros.ptr
-    if kind == "w4a16":
+    # the matrix-core regime reads the t16 tile layout of the resident matrix
+    mfma = _check(L.lbd_gemm_path(KIND_IDS[kind], m, w.kp, C.byref(prm)), "lbd_gemm_path", False) == ISA_GFX950_MFMA
+    if kind in ("w4a16", "mxfp4") and mfma:
+        ws = DeviceBuffer(L.lbd_bf16x3_workspace_bytes(m, w.kp))
+        if kind == "w4a16":
+            qwt, st, zt = w.tiles()
+            rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n,
+                                      dy.ptr, C.byref(prm), ws.ptr, ws.nbytes, None)
+        else:
+            qwt, et = w.tiles()
+            rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, w.kp, qwt.ptr, et.ptr, w.n, dy.ptr, C.byref(prm), ws.ptr,
+                                      ws.nbytes, None)
+    elif kind == "w4a16":
         rc = L.lbd_gemm_w4a16(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm), None)
     elif kind == "mxfp4":
         rc = L.lbd_gemm_mxfp4(dx.ptr, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, dy.ptr, C.byref(prm), None)
     else:
         ws = DeviceBuffer(L.lbd_w4a8_workspace_bytes(m, w.kp))
-        if _check(L.lbd_gemm_path(KIND_IDS["w4a8"], m, w.kp, C.byref(prm)), "lbd_gemm_path", False) == ISA_GFX950_MFMA:
+        if mfma:
             qwt, st, zt = w.tiles()
             rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n,
                                      dy.ptr, C.byref(prm), ws.ptr, ws.nbytes, None)

@@ -98,3 +98,117 @@ def test_w4a8_t16_entry_point_any_m(rng):
         a = lb.quantize_act_int8(x)
         ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
         O.assert_fp_close(y, ref, bound, 1e-5)
+
+
+# ---------------------------------------------------------------- W4A16 / MXFP4, bf16x3 path
+
+def mx_t16_expected(W):
+    """The documented MXFP4 t16 order: qwt tiles of block 4g + q, et in lane order."""
+    n, kp = W.n, W.kp
+    g = -(-kp // 128)
+    g4 = (g + 3) // 4 * 4
+    s = (n + 15) // 16
+    qw = np.zeros((s * 16, g4 * 64), np.uint8)
+    qw[:n, :kp // 2] = W.qw
+    qwt = qw.reshape(s, 16, g4, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+    e = np.zeros((s * 16, g4 * 4), np.uint8)
+    e[:n, :kp // 32] = W.e8m0
+    et = e.reshape(s, 16, g4, 4).transpose(0, 2, 3, 1).reshape(-1)  # [s][g][q][c]
+    return qwt, et
+
+
+def _random_mx(rng, n, kp, lo=118, hi=136):
+    return lb.formats.MXFP4Weights(rng.integers(0, 256, (n, kp // 2), dtype=np.uint8),
+                                   rng.integers(lo, hi, (n, kp // 32), dtype=np.uint8), kp)
+
+
+@pytest.mark.parametrize("n,kp", [(16, 128), (33, 288), (70, 4128)])
+def test_mxfp4_t16_repack_matches_documented_layout(rng, n, kp):
+    W = _random_mx(rng, n, kp)
+    qwt, et = lb.to_device(W).tiles()
+    eq, ee = mx_t16_expected(W)
+    np.testing.assert_array_equal(qwt.to_array(eq.shape, np.uint8), eq)
+    np.testing.assert_array_equal(et.to_array(ee.shape, np.uint8), ee)
+
+
+# (M, N, K): M tails and both row-block heights, N tails, the LLaMA up- and down-proj
+# shapes (K = 11008: 86 groups, 11 per wave over 2 phases) and MXFP4 K not a multiple of 128.
+BF3 = [(5, 33, 256), (16, 11008, 4096), (17, 70, 1152), (64, 11008, 4096), (64, 4096, 11008),
+       (70, 300, 4352), (33, 20, 256), (1, 64, 128), (4, 100, 1024)]
+
+
+def _lognormal_rows(rng, n, k):
+    # config 4: W ~ N(0,1) scaled per row by LogNormal(0, 0.5) to spread the block exponents
+    return (rng.standard_normal((n, k)) * rng.lognormal(0, 0.5, (n, 1))).astype(np.float32)
+
+
+@pytest.mark.parametrize("m,n,k", BF3)
+@pytest.mark.parametrize("asym", [False, True])
+def test_w4a16_bf16x3_within_bound(rng, m, n, k, asym):
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    W = lb.quantize_int4(_lognormal_rows(rng, n, k), asym=asym)
+    D = lb.to_device(W)
+    y = K.gemm_w4a16(x, D, isa="gfx950-mfma")
+    assert K.last_path() == "gfx950-mfma" and D.t16 is not None
+    xp = lb.formats.pad_acts(x, W.kp)
+    ref = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros)
+    bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
+    O.assert_fp_close(y, ref, bound, 1e-5)
+
+
+@pytest.mark.parametrize("m,n,k", BF3 + [(64, 40, 4096 + 32), (20, 17, 96)])
+def test_mxfp4_bf16x3_within_bound(rng, m, n, k):
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    W = lb.quantize_mxfp4(_lognormal_rows(rng, n, k))
+    D = lb.to_device(W)
+    y = K.gemm_mxfp4(x, D, isa="gfx950-mfma")
+    assert K.last_path() == "gfx950-mfma" and D.t16 is not None
+    xp = lb.formats.pad_acts(x, W.kp)
+    ref = cref.c_gemm_mxfp4(xp, W.qw, W.e8m0)
+    bound = cref.c_gemm_mxfp4(xp, W.qw, W.e8m0, absval=True)
+    O.assert_fp_close(y, ref, bound, 1e-5)
+
+
+def test_bf16x3_zero_rows_and_negative_scales_exact(rng):
+    """Zero weight rows give exact zeros (q - z = 0 / E2M1 0 in every product) and
+    signed-max (negative) scales stay within the bound."""
+    x = rng.standard_normal((24, 512)).astype(np.float32)
+    w = rng.standard_normal((40, 512)).astype(np.float32)
+    w[3] = 0.0
+    w[17] = 0.0
+    for W in (lb.quantize_int4(w), lb.quantize_int4(w, asym=True), lb.quantize_int4(w, scale="signed-max")):
+        y = K.gemm_w4a16(x, lb.to_device(W), isa="gfx950-mfma")
+        assert np.all(y[:, 3] == 0) and np.all(y[:, 17] == 0)
+        ref = cref.c_gemm_w4a16(x, W.qw, W.scales, W.zeros)
+        bound = cref.c_gemm_w4a16(x, W.qw, W.scales, W.zeros, absval=True)
+        O.assert_fp_close(y, ref, bound, 1e-5)
+    Wm = lb.quantize_mxfp4(w)
+    y = K.gemm_mxfp4(x, lb.to_device(Wm), isa="gfx950-mfma")
+    assert np.all(y[:, 3] == 0) and np.all(y[:, 17] == 0)
+
+
+def test_mxfp4_bf16x3_extreme_exponents(rng):
+    """E8M0 0 (2^-127, a float32 subnormal scale), 1 and 2, 230 and 254 within the
+    bound, blocks 2^126 apart in one group, and 255 (NaN) propagating to exactly the
+    rows the float64 oracle makes NaN. (Sums stay below the float32 range, where
+    the reference's fp32 kernels would overflow too.)"""
+    m, n, kp = 20, 48, 512
+    x = rng.standard_normal((m, kp)).astype(np.float32)
+    W = _random_mx(rng, n, kp)
+    e = W.e8m0
+    e[0, :] = 0                          # whole row at 2^-127
+    e[1, :] = rng.integers(0, 3, kp // 32)
+    e[2, ::2] = 1                        # tiny and normal blocks in the same groups
+    e[3, :] = 230
+    e[4, 0] = 254                        # one huge block next to normal ones:
+    W.qw[4, :16] = 0
+    W.qw[4, 0] = 0x01                    # a single 0.5 there, 2^126 * x stays finite
+    e[5, 7] = 255                        # NaN block
+    y = K.gemm_mxfp4(x, lb.to_device(W), isa="gfx950-mfma")
+    ref = cref.c_gemm_mxfp4(x, W.qw, W.e8m0)
+    bound = cref.c_gemm_mxfp4(x, W.qw, W.e8m0, absval=True)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(y), nan)
+    assert nan[:, 5].all() and nan.sum() == m
+    keep = ~nan
+    assert np.all(np.abs(y[keep] - ref[keep]) <= 1e-5 * bound[keep])
