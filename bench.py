@@ -41,6 +41,8 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, published (POP/s -> TOP/s here)
 FP32_PEAK_TFLOPS = 157.3     # dense fp32 matrix, published
+BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA, published
+BF16X3_TERMS = 3             # bf16 products per fp32 product on the bf16x3 path
 COLD_POOL_BYTES = 1280 << 20  # > 2 x (256 MB MALL + 32 MB L2)
 DECODE = (1, 11008, 4096)
 BATCH = (64, 11008, 4096)
@@ -382,11 +384,20 @@ def main() -> int:
             r = measure(dev, fmt, BATCH, W, xb, cold=False, steps=max(20, args.steps // 4),
                         warmup=max(2, args.warmup // 4), graph=graph)
             r["max_rel_err"] = float(f"{rel_err(fmt, W, xb, r.pop('y')):.3g}")
-            peak = INT8_PEAK_TOPS if fmt == "w4a8" else FP32_PEAK_TFLOPS
-            r["mfma_frac"] = round(r["gflops"] / 1e3 / peak, 4)
+            if fmt == "w4a8":
+                r["mfma"] = "int8"
+                r["mfma_frac"] = round(r["gflops"] / 1e3 / INT8_PEAK_TOPS, 4)
+            elif r["weight_layout"] == "t16":
+                # fp32 semantics on bf16 matrix cores: three bf16 products per fp32 product
+                r["mfma"] = "bf16x3"
+                r["mfma_frac"] = round(BF16X3_TERMS * r["gflops"] / 1e3 / BF16_PEAK_TFLOPS, 4)
+                r["fp32_equiv_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
+            else:
+                r["mfma"] = "fp32"
+                r["mfma_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
             results[f"{fmt}_m64"] = r
             log(f"{fmt:6s} M=64 hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
-                f"({100 * r['mfma_frac']:.1f}% of {'int8' if fmt == 'w4a8' else 'fp32'} peak)  path {r['path']}")
+                f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}")
 
     head = results["w4a8_decode"]
     t_launch_s = head["us_per_call"] * 1e-6
