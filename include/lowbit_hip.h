@@ -206,6 +206,39 @@ int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                        const uint8_t *et, int N, float *y, const lb_params *p,
                        void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- decoder-layer operations for a device-resident decoder (no lowbit.h
+ *      counterpart: the building blocks of the reference's numpy model,
+ *      src/lowbit/model.py:190-230 and 353-435, on the device; fp32 [T, width]
+ *      row-major activations, asynchronous on `stream`). `pos` and `tok` are device
+ *      int32: kernels read the decode position from `pos`, so a decode step is a
+ *      fixed launch sequence a HIP graph can replay. ---- */
+/* x[t] = table[tok[t]] (ids clamped into [0, vocab)) */
+int lbd_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T,
+              float *x, void *stream);
+/* y = x / sqrt(mean(x^2) + eps) * w per row (model.py:190-192) */
+int lbd_rmsnorm(const float *x, const float *w, int T, int hidden, float eps,
+                float *y, void *stream);
+/* qkv [T, (H + 2 KV) D]: + bias (NULL: none), rotary embedding of q and k at
+ * position *pos + t from cos/sin [max_pos, D/2] ("rotate_half", model.py:201-210),
+ * q left in place, k and v written to the caches [KV, cap, D]; D in {32, 64, 128} */
+int lbd_qkv_rope(float *qkv, const float *bias, int T, int H, int KV, int D,
+                 const float *cos_table, const float *sin_table, const int32_t *pos,
+                 int max_pos, float *k_cache, float *v_cache, int cap, void *stream);
+/* out [T, H D] = causal grouped-query attention of the q rows (row stride qstride
+ * floats) over cache positions 0 .. *pos + t (model.py:353-378); cap <= 16000 */
+int lbd_attention(const float *q, int qstride, const float *k_cache,
+                  const float *v_cache, int T, int H, int KV, int D, const int32_t *pos,
+                  int cap, float *out, void *stream);
+/* out [T, I] = silu(gu[:, :I]) * gu[:, I:] (model.py:213, 416-417) */
+int lbd_swiglu(const float *gu, int T, int I, float *out, void *stream);
+/* x += y over n floats (the residual adds) */
+int lbd_add(float *x, const float *y, size_t n, void *stream);
+/* tok[0] = numpy's argmax of v[0..n) (the first NaN if any, else the first maximum);
+ * with pos != NULL also hist[*pos + inc] = tok[0] (inside [0, hist_len)) and
+ * *pos += inc */
+int lbd_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc,
+               int32_t *hist, int hist_len, void *stream);
+
 /* ---- device plumbing for the ctypes layer and benchmarks ---- */
 int lb_dev_malloc(void **ptr, size_t bytes);
 int lb_dev_free(void *ptr);

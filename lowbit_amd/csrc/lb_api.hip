@@ -574,6 +574,69 @@ int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, con
   return run_group_acc(xq, asum, M, Kp, qw, zeros, N, out, isa, static_cast<hipStream_t>(stream));
 }
 
+// ---------------------------------------------------------------- decoder-layer operations
+
+#define LB_LAUNCH(call, what)                    \
+  do {                                           \
+    hipError_t e_ = (call);                      \
+    if (e_ != hipSuccess) return fail_hip(e_, what); \
+    return ok(0);                                \
+  } while (0)
+
+int lbd_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, void *stream) {
+  if (vocab <= 0 || hidden <= 0 || T <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!table || !tok || !x) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_embed(table, vocab, hidden, tok, T, x, static_cast<hipStream_t>(stream)), "embed launch");
+}
+
+int lbd_rmsnorm(const float *x, const float *w, int T, int hidden, float eps, float *y, void *stream) {
+  if (T <= 0 || hidden <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!x || !w || !y) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_rmsnorm(x, w, T, hidden, eps, y, static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
+int lbd_qkv_rope(float *qkv, const float *bias, int T, int H, int KV, int D, const float *cos_table,
+                 const float *sin_table, const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap,
+                 void *stream) {
+  if (T <= 0 || H <= 0 || KV <= 0 || H % KV || (D != 32 && D != 64 && D != 128) || max_pos <= 0 || cap <= 0)
+    return fail(LB_ERR_SHAPE, "bad shape");
+  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_qkv_rope(qkv, bias, T, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap,
+                                 static_cast<hipStream_t>(stream)),
+            "qkv rope launch");
+}
+
+int lbd_attention(const float *q, int qstride, const float *k_cache, const float *v_cache, int T, int H, int KV, int D,
+                  const int32_t *pos, int cap, float *out, void *stream) {
+  if (T <= 0 || H <= 0 || KV <= 0 || H % KV || (D != 32 && D != 64 && D != 128) || cap <= 0 || cap > 16000 ||
+      qstride < H * D)
+    return fail(LB_ERR_SHAPE, "bad shape");
+  if (!q || !k_cache || !v_cache || !pos || !out) return fail(LB_ERR_ARG, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) != 0) return fail(LB_ERR_ARG, "k_cache must be 16-byte aligned");
+  LB_LAUNCH(lbk::launch_attention(q, qstride, k_cache, v_cache, T, H, KV, D, pos, cap, out,
+                                  static_cast<hipStream_t>(stream)),
+            "attention launch");
+}
+
+int lbd_swiglu(const float *gu, int T, int I, float *out, void *stream) {
+  if (T <= 0 || I <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!gu || !out) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_swiglu(gu, T, I, out, static_cast<hipStream_t>(stream)), "swiglu launch");
+}
+
+int lbd_add(float *x, const float *y, size_t n, void *stream) {
+  if (!x || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (n == 0) return ok(0);
+  LB_LAUNCH(lbk::launch_add(x, y, n, static_cast<hipStream_t>(stream)), "add launch");
+}
+
+int lbd_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len, void *stream) {
+  if (n <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!v || !tok) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_argmax(v, n, tok, pos, inc, hist, hist_len, static_cast<hipStream_t>(stream)),
+            "argmax launch");
+}
+
 // ---------------------------------------------------------------- host-pointer GEMMs
 
 int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,

@@ -78,4 +78,17 @@ hipError_t launch_groupacc_dot4(const int8_t *xq, const int32_t *asum, int M, in
                                 int32_t *out, hipStream_t s);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 
+// Decoder-layer kernels (lb_model.hip).
+hipError_t launch_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, hipStream_t s);
+hipError_t launch_rmsnorm(const float *x, const float *w, int T, int hidden, float eps, float *y, hipStream_t s);
+hipError_t launch_qkv_rope(float *qkv, const float *bias, int T, int H, int KV, int D, const float *cosT,
+                           const float *sinT, const int32_t *pos, int max_pos, float *kc, float *vc, int cap,
+                           hipStream_t s);
+hipError_t launch_attention(const float *q, int qstride, const float *kc, const float *vc, int T, int H, int KV, int D,
+                            const int32_t *pos, int cap, float *out, hipStream_t s);
+hipError_t launch_swiglu(const float *gu, int T, int I, float *out, hipStream_t s);
+hipError_t launch_add(float *x, const float *y, size_t n, hipStream_t s);
+hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
+                         hipStream_t s);
+
 }  // namespace lbk

@@ -1,0 +1,279 @@
+// Decoder-layer kernels around the fused GEMMs, for a device-resident decoder
+// (Qwen2 / Llama architecture of the reference's numpy model, src/lowbit/model.py):
+// embedding gather, RMSNorm, q/k/v bias + rotary embedding + KV-cache write,
+// grouped-query causal attention, SwiGLU, residual add and greedy argmax.
+//
+// Activations are fp32 row-major [T, width]. The decode position and the current
+// token live in device memory (`pos`, `tok`), so one decode step is a fixed
+// sequence of launches that a HIP graph can replay: the kernels read the position
+// from `pos`, and the argmax writes the next token and advances `pos`.
+#include <math.h>
+
+#include "lb_device.h"
+#include "lb_internal.h"
+
+namespace lbk {
+
+constexpr int kMT = 256;  // threads of the row kernels
+
+// Sum over a workgroup of kMT threads; every thread gets the result.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();  // red may still be read from a previous call
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kMT / kWave; i++) r += red[i];
+  return r;
+}
+
+// x[t] = table[tok[t]] (token ids clamped into the table).
+__global__ __launch_bounds__(kMT) void embed_kernel(const float *__restrict__ table, int vocab, int hidden,
+                                                     const int32_t *__restrict__ tok, float *__restrict__ x) {
+  const int t = blockIdx.x;
+  int id = tok[t];
+  id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+  const float *src = table + (size_t)id * hidden;
+  for (int i = threadIdx.x; i < hidden; i += kMT) x[(size_t)t * hidden + i] = src[i];
+}
+
+// y = x * (1 / sqrt(mean(x^2) + eps)) * w, one workgroup per row (the reference's
+// rms_norm, src/lowbit/model.py:190-192, in float32).
+__global__ __launch_bounds__(kMT) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                       int hidden, float eps, float *__restrict__ y) {
+  __shared__ float red[kMT / kWave];
+  const float *xr = x + (size_t)blockIdx.x * hidden;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < hidden; i += kMT) ss = __builtin_fmaf(xr[i], xr[i], ss);
+  const float var = block_sum(ss, red) / (float)hidden;
+  const float r = 1.0f / sqrtf(var + eps);
+  for (int i = threadIdx.x; i < hidden; i += kMT) y[(size_t)blockIdx.x * hidden + i] = xr[i] * r * w[i];
+}
+
+// qkv [T, (H + 2 KV) D]: adds the bias, rotates q and k at absolute position
+// pos + t (the "rotate_half" convention: element i pairs with i + D/2,
+// src/lowbit/model.py:201-210) with the float32 tables cos/sin [max_pos, D/2], leaves
+// q in place and writes k and v into the caches [KV, cap, D]. One workgroup per
+// (token, head), D/2 threads.
+__global__ void qkv_rope_kernel(float *__restrict__ qkv, const float *__restrict__ bias, int H, int KV, int D,
+                                const float *__restrict__ cosT, const float *__restrict__ sinT,
+                                const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc,
+                                float *__restrict__ vc, int cap) {
+  const int t = blockIdx.x, hd = blockIdx.y, i = threadIdx.x, half = D / 2;
+  const int p = *pos + t;
+  if (p < 0) return;  // no position before the start of the cache
+  const int width = (H + 2 * KV) * D;
+  float *row = qkv + (size_t)t * width + (size_t)hd * D;
+  const float *b = bias ? bias + (size_t)hd * D : nullptr;
+  float x1 = row[i], x2 = row[i + half];
+  if (b) {
+    x1 += b[i];
+    x2 += b[i + half];
+  }
+  if (hd < H + KV) {  // q or k: rotate
+    const int pp = p < max_pos ? p : max_pos - 1;  // positions past the tables reuse the last angle
+    const float c = cosT[(size_t)pp * half + i], s = sinT[(size_t)pp * half + i];
+    const float y1 = x1 * c - x2 * s, y2 = x2 * c + x1 * s;
+    x1 = y1;
+    x2 = y2;
+  }
+  if (hd < H) {
+    row[i] = x1;
+    row[i + half] = x2;
+  } else if (p < cap) {
+    const int kvh = hd < H + KV ? hd - H : hd - H - KV;
+    float *dst = (hd < H + KV ? kc : vc) + ((size_t)kvh * cap + p) * D;
+    dst[i] = x1;
+    dst[i + half] = x2;
+  }
+}
+
+// Causal grouped-query attention: query t (absolute position pos + t) of head h
+// against keys 0 .. pos + t of KV head h / (H / KV), softmax(q k^T / sqrt(D)) v
+// (src/lowbit/model.py:353-378). One workgroup of one wave per (token, head):
+// scores one key per lane into LDS, wave max and sum, then lane l owns output
+// elements l, l + 64, ... below D. q rows have stride qstride floats; out is [T, H D].
+template <int D>
+__global__ __launch_bounds__(kWave) void attention_kernel(const float *__restrict__ q, int qstride,
+                                                          const float *__restrict__ kc,
+                                                          const float *__restrict__ vc, int H, int KV,
+                                                          const int32_t *__restrict__ pos, int cap,
+                                                          float *__restrict__ out) {
+  extern __shared__ float sc[];  // [cap] scores, then [D] query
+  constexpr int DPL = (D + kWave - 1) / kWave;
+  const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int kvh = h / (H / KV);
+  int S = *pos + t + 1;
+  S = S < cap ? S : cap;
+  float *qs = sc + cap;
+  const float *qr = q + (size_t)t * qstride + (size_t)h * D;
+  for (int e = lane; e < D; e += kWave) qs[e] = qr[e];
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((float)D);
+  const float *kb = kc + (size_t)kvh * cap * D;
+  float mx = -INFINITY;
+  for (int s = lane; s < S; s += kWave) {
+    const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)s * D);
+    float d = 0.0f;
+#pragma unroll 4
+    for (int e = 0; e < D / 4; e++) {
+      const float4 kv = kr[e];
+      d = __builtin_fmaf(qs[4 * e], kv.x, d);
+      d = __builtin_fmaf(qs[4 * e + 1], kv.y, d);
+      d = __builtin_fmaf(qs[4 * e + 2], kv.z, d);
+      d = __builtin_fmaf(qs[4 * e + 3], kv.w, d);
+    }
+    d *= scale;
+    sc[s] = d;
+    mx = fmaxf(mx, d);
+  }
+  mx = wave_max(mx);
+  float sum = 0.0f;
+  for (int s = lane; s < S; s += kWave) {
+    const float e = expf(sc[s] - mx);
+    sc[s] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  __syncthreads();
+  const float inv = 1.0f / sum;
+  const float *vb = vc + (size_t)kvh * cap * D;
+  const bool own = D >= kWave || lane < D;  // D = 32: lanes 32..63 hold no output
+  const int l = own ? lane : 0;
+  float acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; j++) acc[j] = 0.0f;
+  for (int s = 0; s < S; s++) {
+    const float ps = sc[s];
+#pragma unroll
+    for (int j = 0; j < DPL; j++) acc[j] = __builtin_fmaf(ps, vb[(size_t)s * D + l + kWave * j], acc[j]);
+  }
+  if (own) {
+#pragma unroll
+    for (int j = 0; j < DPL; j++) out[(size_t)t * H * D + (size_t)h * D + l + kWave * j] = acc[j] * inv;
+  }
+}
+
+// out[t, i] = silu(gu[t, i]) * gu[t, I + i], silu(g) = g / (1 + exp(-g))
+// (src/lowbit/model.py:213, 416-417).
+__global__ __launch_bounds__(kMT) void swiglu_kernel(const float *__restrict__ gu, int T, int I,
+                                                      float *__restrict__ out) {
+  const size_t n = (size_t)T * I;
+  for (size_t e = (size_t)blockIdx.x * kMT + threadIdx.x; e < n; e += (size_t)gridDim.x * kMT) {
+    const size_t t = e / I, i = e % I;
+    const float g = gu[t * 2 * I + i], u = gu[t * 2 * I + I + i];
+    out[e] = g / (1.0f + expf(-g)) * u;
+  }
+}
+
+__global__ __launch_bounds__(kMT) void add_kernel(float *__restrict__ x, const float *__restrict__ y, size_t n) {
+  for (size_t e = (size_t)blockIdx.x * kMT + threadIdx.x; e < n; e += (size_t)gridDim.x * kMT) x[e] += y[e];
+}
+
+// numpy's argmax order: NaN above every number, then larger values, then the
+// smaller index among equals.
+__device__ __forceinline__ bool argmax_before(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+// Index of the largest value as numpy's argmax picks it (the first NaN if there is
+// one, else the first maximum). One workgroup of 1024 threads. Writes the index to
+// tok[0] and, with pos != null, stores it into hist[*pos + inc] (when inside
+// hist_len) and advances *pos by inc.
+constexpr int kAT = 1024;
+__global__ __launch_bounds__(kAT) void argmax_kernel(const float *__restrict__ v, int n, int32_t *__restrict__ tok,
+                                                      int32_t *__restrict__ pos, int inc, int32_t *__restrict__ hist,
+                                                      int hist_len) {
+  __shared__ float bv[kAT / kWave];
+  __shared__ int bi[kAT / kWave];
+  float best = -INFINITY;
+  int bidx = 0x7FFFFFFF;
+  for (int i = threadIdx.x; i < n; i += kAT) {
+    const float x = v[i];
+    if (argmax_before(x, i, best, bidx)) best = x, bidx = i;
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(bidx, off);
+    if (argmax_before(ov, oi, best, bidx)) best = ov, bidx = oi;
+  }
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) bv[w] = best, bi[w] = bidx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = bv[0];
+    int ix = bi[0];
+    for (int k = 1; k < kAT / kWave; k++)
+      if (argmax_before(bv[k], bi[k], b, ix)) b = bv[k], ix = bi[k];
+    if (ix == 0x7FFFFFFF) ix = 0;  // n == 0
+    tok[0] = ix;
+    if (pos) {
+      const int p = *pos + inc;
+      if (hist && p >= 0 && p < hist_len) hist[p] = ix;
+      *pos = p;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+
+static unsigned grid_for(size_t n) {
+  size_t b = (n + kMT - 1) / kMT;
+  if (b > 16384) b = 16384;
+  return (unsigned)(b ? b : 1);
+}
+
+hipError_t launch_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(kMT), 0, s, table, vocab, hidden, tok, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, int T, int hidden, float eps, float *y, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kMT), 0, s, x, w, hidden, eps, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_rope(float *qkv, const float *bias, int T, int H, int KV, int D, const float *cosT,
+                           const float *sinT, const int32_t *pos, int max_pos, float *kc, float *vc, int cap,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(qkv_rope_kernel, dim3(T, H + 2 * KV), dim3(D / 2), 0, s, qkv, bias, H, KV, D, cosT, sinT, pos,
+                     max_pos, kc, vc, cap);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention(const float *q, int qstride, const float *kc, const float *vc, int T, int H, int KV, int D,
+                            const int32_t *pos, int cap, float *out, hipStream_t s) {
+  const size_t lds = ((size_t)cap + D) * sizeof(float);
+  if (D == 32)
+    hipLaunchKernelGGL(attention_kernel<32>, dim3(T, H), dim3(kWave), lds, s, q, qstride, kc, vc, H, KV, pos, cap, out);
+  else if (D == 64)
+    hipLaunchKernelGGL(attention_kernel<64>, dim3(T, H), dim3(kWave), lds, s, q, qstride, kc, vc, H, KV, pos, cap, out);
+  else if (D == 128)
+    hipLaunchKernelGGL(attention_kernel<128>, dim3(T, H), dim3(kWave), lds, s, q, qstride, kc, vc, H, KV, pos, cap,
+                       out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float *gu, int T, int I, float *out, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((size_t)T * I)), dim3(kMT), 0, s, gu, T, I, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float *x, const float *y, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(kMT), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kAT), 0, s, v, n, tok, pos, inc, hist, hist_len);
+  return hipGetLastError();
+}
+
+}  // namespace lbk

@@ -121,6 +121,13 @@ SIGNATURES = {
     "lbd_mxfp4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_mxfp4_t16": ([_vp, _vp, _int, _int, _vp, _vp, _vp], _int),
     "lbd_gemm_mxfp4_t16": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_embed": ([_vp, _int, _int, _vp, _int, _vp, _vp], _int),
+    "lbd_rmsnorm": ([_vp, _vp, _int, _int, C.c_float, _vp, _vp], _int),
+    "lbd_qkv_rope": ([_vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp], _int),
+    "lbd_attention": ([_vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _int, _vp, _vp], _int),
+    "lbd_swiglu": ([_vp, _int, _int, _vp, _vp], _int),
+    "lbd_add": ([_vp, _vp, _sz, _vp], _int),
+    "lbd_argmax": ([_vp, _int, _vp, _vp, _int, _vp, _int, _vp], _int),
 }
 
 
