@@ -206,6 +206,19 @@ int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                        const uint8_t *et, int N, float *y, const lb_params *p,
                        void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- weight quantizers on the device: fp32 w [N, K] row-major (device memory)
+ *      -> the public packed formats, byte for byte what the host packers write
+ *      (quantize_int4 / quantize_mxfp4, src/lowbit/formats.py:90-142, 197-212) for
+ *      finite weights. K is padded to the block; padded elements decode to 0. ---- */
+/* int4 g128 -> qw [N, Kp/2], scales [N, Kp/128], zeros [N, Kp/128] (asym only; NULL
+ * otherwise). asym: s = (max(w,0) - min(w,0)) / 15 with a zero point; signed_max: s =
+ * m / -8 for the element m of largest magnitude; neither: s = max|w| / 7 */
+int lbd_quantize_int4(const float *w, int N, int K, int asym, int signed_max, uint8_t *qw,
+                      float *scales, uint8_t *zeros, void *stream);
+/* MXFP4 -> qw [N, Kp/2], e8m0 [N, Kp/32]; Kp = K rounded up to 32 */
+int lbd_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0,
+                       void *stream);
+
 /* ---- decoder-layer operations for a device-resident decoder (no lowbit.h
  *      counterpart: the building blocks of the reference's numpy model,
  *      src/lowbit/model.py:190-230 and 353-435, on the device; fp32 [T, width]

@@ -436,6 +436,25 @@ int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p) {
   return ok(choose_path(fmts[kind], M, Kp, p));
 }
 
+int lbd_quantize_int4(const float *w, int N, int K, int asym, int signed_max, uint8_t *qw, float *scales,
+                      uint8_t *zeros, void *stream) {
+  if (N <= 0 || K <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (asym && signed_max) return fail(LB_ERR_ARG, "signed-max is a symmetric rule");
+  if (!w || !qw || !scales || (asym && !zeros)) return fail(LB_ERR_ARG, "null pointer");
+  const int mode = asym ? 2 : (signed_max ? 1 : 0);
+  hipError_t e = lbk::launch_quantize_int4(w, N, K, mode, qw, scales, zeros, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "int4 quantizer launch");
+  return ok(0);
+}
+
+int lbd_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0, void *stream) {
+  if (N <= 0 || K <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!w || !qw || !e8m0) return fail(LB_ERR_ARG, "null pointer");
+  hipError_t e = lbk::launch_quantize_mxfp4(w, N, K, qw, e8m0, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "MXFP4 quantizer launch");
+  return ok(0);
+}
+
 int lbd_int4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *st_bytes, size_t *zt_bytes) {
   int rc = check_shape(1, Kp, N, LB_GROUP);
   if (rc < 0) return rc;

@@ -50,6 +50,11 @@ hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N
 __host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
 hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
+// weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 g128 (mode 0 absmax,
+// 1 signed-max, 2 asym) or MXFP4
+hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, uint8_t *qw, float *scales, uint8_t *zeros,
+                                hipStream_t s);
+hipError_t launch_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0, hipStream_t s);
 hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
                                   uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s);
 

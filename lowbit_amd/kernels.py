@@ -24,7 +24,7 @@ from functools import lru_cache
 import numpy as np
 
 from ._build import lib_path
-from .formats import GROUP, MXBLOCK, Int4Weights, Int8Acts, MXFP4Weights, pad_acts
+from .formats import GROUP, MXBLOCK, Int4Weights, Int8Acts, MXFP4Weights, pad_acts, pad_to
 
 ISA_GFX950 = 16
 ISA_GFX950_MFMA = 17
@@ -121,6 +121,8 @@ SIGNATURES = {
     "lbd_mxfp4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_mxfp4_t16": ([_vp, _vp, _int, _int, _vp, _vp, _vp], _int),
     "lbd_gemm_mxfp4_t16": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_quantize_int4": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),
+    "lbd_quantize_mxfp4": ([_vp, _int, _int, _vp, _vp, _vp], _int),
     "lbd_embed": ([_vp, _int, _int, _vp, _int, _vp, _vp], _int),
     "lbd_rmsnorm": ([_vp, _vp, _int, _int, C.c_float, _vp, _vp], _int),
     "lbd_qkv_rope": ([_vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp], _int),
@@ -356,6 +358,57 @@ def to_device(w):
     if isinstance(w, (DeviceInt4Weights, DeviceMXFP4Weights)):
         return w
     raise TypeError(f"cannot upload {type(w).__name__}")
+
+
+def _device_fp32(w, shape):
+    """(DeviceBuffer of fp32 [N, K], N, K) from a host array or a DeviceBuffer + shape."""
+    if isinstance(w, DeviceBuffer):
+        if shape is None or len(shape) != 2:
+            raise ValueError("a DeviceBuffer needs shape=(N, K)")
+        n, k = int(shape[0]), int(shape[1])
+        if n * k * 4 > w.nbytes:
+            raise ValueError(f"DeviceBuffer of {w.nbytes} bytes is smaller than fp32 {n}x{k}")
+        return w, n, k
+    a = np.ascontiguousarray(w, np.float32)
+    if a.ndim != 2:
+        raise ValueError("weights must be 2-D [N, K]")
+    return DeviceBuffer.from_array(a), a.shape[0], a.shape[1]
+
+
+def quantize_int4_device(w, asym: bool = False, scale: str = "absmax", shape=None,
+                         stream=None) -> "DeviceInt4Weights":
+    """quantize_int4 run on the device (lbd_quantize_int4): the same packed bytes,
+    scales and zero points as the host packer (src/lowbit/formats.py:90-142) for
+    finite weights, left in HBM as a handle the GEMMs accept. `w` is a host array
+    [N, K] (uploaded as fp32) or a DeviceBuffer holding fp32 [N, K] with shape=(N, K)."""
+    if scale not in ("absmax", "signed-max"):
+        raise ValueError(f"scale must be 'absmax' or 'signed-max', not {scale!r}")
+    if asym and scale != "absmax":
+        raise ValueError("scale='signed-max' is a symmetric rule (asym=False)")
+    src, n, k = _device_fp32(w, shape)
+    kp = pad_to(k, GROUP)
+    g = kp // GROUP
+    qw, sc = DeviceBuffer(n * kp // 2), DeviceBuffer(n * g * 4)
+    z = DeviceBuffer(n * g) if asym else None
+    _check(lib().lbd_quantize_int4(src.ptr, n, k, int(asym), int(scale == "signed-max"), qw.ptr, sc.ptr,
+                                   None if z is None else z.ptr, stream), "lbd_quantize_int4", False)
+    if stream is not None:
+        _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)  # src may be freed next
+    nbytes = n * kp // 2 + n * g * 4 + (n * g if asym else 0)
+    return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes)
+
+
+def quantize_mxfp4_device(w, shape=None, stream=None) -> "DeviceMXFP4Weights":
+    """quantize_mxfp4 run on the device (lbd_quantize_mxfp4): the same packed codes
+    and E8M0 exponents as the host packer (src/lowbit/formats.py:197-212) for finite
+    weights; `w` as for quantize_int4_device."""
+    src, n, k = _device_fp32(w, shape)
+    kp = pad_to(k, MXBLOCK)
+    qw, e = DeviceBuffer(n * kp // 2), DeviceBuffer(n * kp // MXBLOCK)
+    _check(lib().lbd_quantize_mxfp4(src.ptr, n, k, qw.ptr, e.ptr, stream), "lbd_quantize_mxfp4", False)
+    if stream is not None:
+        _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)
+    return DeviceMXFP4Weights(qw, e, n, kp, k, n * kp // 2 + n * kp // MXBLOCK)
 
 
 def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
