@@ -252,6 +252,53 @@ int lbd_add(float *x, const float *y, size_t n, void *stream);
 int lbd_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc,
                int32_t *hist, int hist_len, void *stream);
 
+/* ---- fused decode GEMVs (no lowbit.h counterpart: the reference's decoder runs a
+ *      Linear as GEMM + bias in numpy, src/lowbit/model.py:120-124, with RMSNorm,
+ *      SwiGLU and the residual adds as separate numpy steps, model.py:190-192,
+ *      213, 398-431; a device-resident decode step folds them into the small-M
+ *      kernels so each linear layer is one launch). Same operands and arithmetic
+ *      as lbd_gemm_w4a16 / lbd_gemm_mxfp4 / lbd_gemm_w4a8 (W4A8 quantizes the
+ *      prologue's output per token), small-M kernels only: M <= 4 and Kp within
+ *      their limit (lbd_gemm_path gives LB_ISA_GFX950), else LB_ERR_SHAPE. ---- */
+typedef struct {
+  /* prologue, M == 1 only, at most one of the two:
+   *   norm_w != NULL: x <- x * (1 / sqrt(mean(x^2) + norm_eps)) * norm_w, the mean
+   *                   over the Kp elements of the row (model.py:190-192)
+   *   swiglu != 0:    the x row holds 2 Kp floats [gate | up] and the activation
+   *                   is silu(gate) * up, silu(g) = g / (1 + exp(-g)) (model.py:213) */
+  const float *norm_w;
+  float norm_eps;
+  int swiglu;
+  /* epilogue: y[m, n] = residual[m, n] + ((x . w^T)[m, n] + bias[n]); NULL skips a
+   * term; residual may be y itself (each element is read before it is written) */
+  const float *bias;
+  const float *residual;
+  /* M == 1: each finished y[0, n] is folded with 64-bit atomic max operations into
+   * argmax_key[0 .. LBD_ARGMAX_SLOTS), as a key ordered as numpy's argmax (first NaN,
+   * else first maximum); the slots must be 0 before the call (lbd_argmax_finalize
+   * reads the index and clears them). 8-byte aligned device memory. */
+  unsigned long long *argmax_key;
+} lbd_fusion;
+#define LBD_ARGMAX_SLOTS 1024
+int lbd_gemv_w4a16_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                         const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream);
+int lbd_gemv_mxfp4_fused(const float *x, int M, int Kp, const uint8_t *qw, const uint8_t *e8m0,
+                         int N, float *y, const lbd_fusion *f, void *stream);
+int lbd_gemv_w4a8_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                        const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream);
+/* tok[0] = the index held by the largest of the LBD_ARGMAX_SLOTS keys (0 if all are
+ * 0), then as lbd_argmax: with pos != NULL hist[*pos + inc] = tok[0] (inside
+ * [0, hist_len)) and *pos += inc; finally every slot is cleared for the next step */
+int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc,
+                        int32_t *hist, int hist_len, void *stream);
+/* One token at position *pos: lbd_qkv_rope (without the bias, which the qkv GEMV's
+ * epilogue adds) and lbd_attention with T = 1 in one launch, one workgroup per KV
+ * head (model.py:353-378). qkv [(H + 2 KV) D] is read only; k and v are written to
+ * the caches; out [H D]. H / KV <= 16, D in {32, 64, 128}, cap <= 16000. */
+int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table,
+                         const float *sin_table, const int32_t *pos, int max_pos,
+                         float *k_cache, float *v_cache, int cap, float *out, void *stream);
+
 /* ---- device plumbing for the ctypes layer and benchmarks ---- */
 int lb_dev_malloc(void **ptr, size_t bytes);
 int lb_dev_free(void *ptr);

@@ -46,21 +46,39 @@ def _hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile the library for gfx950 into lowbit_amd/_lib (always recompiles)."""
+    """Compile the library for gfx950 into lowbit_amd/_lib (always recompiles).
+    Each source is compiled to an object in parallel, then they are linked."""
     LIBDIR.mkdir(parents=True, exist_ok=True)
     arch = os.environ.get("LOWBIT_ARCH", "gfx950")
     out = LIBDIR / LIBNAME
-    tmp = LIBDIR / (LIBNAME + f".tmp{os.getpid()}")
-    cmd = [_hipcc(), f"--offload-arch={arch}", *FLAGS, f"-I{INCLUDE}",
-           *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd))
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        tmp.unlink(missing_ok=True)
-        raise RuntimeError(f"building {LIBNAME} failed:\n{r.stderr}")
-    if verbose and r.stderr.strip():
-        print(r.stderr, file=sys.stderr)
+    tag = f".tmp{os.getpid()}"
+    tmp = LIBDIR / (LIBNAME + tag)
+    objs = [LIBDIR / (Path(s).stem + f"{tag}.o") for s in SOURCES]
+    cflags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for src, obj in zip(SOURCES, objs):
+        cmd = [_hipcc(), f"--offload-arch={arch}", *cflags, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd))
+        jobs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    errs = []
+    for j in jobs:
+        _, err = j.communicate()
+        if j.returncode != 0:
+            errs.append(err)
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    try:
+        if errs:
+            raise RuntimeError(f"building {LIBNAME} failed:\n" + "\n".join(errs))
+        cmd = [_hipcc(), f"--offload-arch={arch}", "-shared", "-fPIC", *[str(o) for o in objs], "-o", str(tmp)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            tmp.unlink(missing_ok=True)
+            raise RuntimeError(f"linking {LIBNAME} failed:\n{r.stderr}")
+    finally:
+        for o in objs:
+            o.unlink(missing_ok=True)
     os.replace(tmp, out)  # atomic: a concurrent loader sees the old or the new file
     return out
 

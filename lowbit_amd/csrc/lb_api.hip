@@ -656,6 +656,107 @@ int lbd_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32
             "argmax launch");
 }
 
+// ---------------------------------------------------------------- fused decode GEMVs
+
+}  // extern "C"
+
+namespace {
+
+static_assert(LBD_ARGMAX_SLOTS == lbk::kArgmaxSlots, "argmax slot count of the ABI and the kernels");
+
+// Checks shared by the fused GEMVs; fills the fusion fields of `a`.
+int fused_args(int fmt, const lbd_fusion *f, lbk::GemmArgs &a) {
+  if (!lbk::gemv_eligible(fmt, a.M, a.Kp))
+    return fail(LB_ERR_SHAPE, "fused GEMVs take the small-M kernels only (M <= 4, Kp within their limit)");
+  if (!f) return 0;
+  if (f->norm_w && f->swiglu) return fail(LB_ERR_ARG, "RMSNorm and SwiGLU prologues are exclusive");
+  if ((f->norm_w || f->swiglu || f->argmax_key) && a.M != 1)
+    return fail(LB_ERR_ARG, "prologues and the argmax key need M == 1");
+  if (f->norm_w && !aligned16(f->norm_w)) return fail(LB_ERR_ARG, "norm_w must be 16-byte aligned");
+  if (f->argmax_key && (reinterpret_cast<uintptr_t>(f->argmax_key) & 7) != 0)
+    return fail(LB_ERR_ARG, "argmax_key must be 8-byte aligned");
+  a.norm_w = f->norm_w;
+  a.norm_eps = f->norm_eps;
+  a.swiglu = f->swiglu != 0;
+  a.bias = f->bias;
+  a.res = f->residual;
+  a.amax_key = f->argmax_key;
+  return 0;
+}
+
+int run_fused(int fmt, const lbk::GemmArgs &a, const char *what, hipStream_t s) {
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  hipError_t e = lbk::launch_gemv(fmt, a, cus, s);
+  if (e != hipSuccess) return fail_hip(e, what);
+  return ok(LB_ISA_GFX950);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lbd_gemv_w4a16_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                         const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  if ((rc = fused_args(lbk::F_W4A16, f, a)) < 0) return rc;
+  return run_fused(lbk::F_W4A16, a, "fused W4A16 GEMV launch", static_cast<hipStream_t>(stream));
+}
+
+int lbd_gemv_mxfp4_fused(const float *x, int M, int Kp, const uint8_t *qw, const uint8_t *e8m0,
+                         int N, float *y, const lbd_fusion *f, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_MXBLOCK);
+  if (rc < 0) return rc;
+  if (!x || !qw || !e8m0 || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.e8m0 = e8m0; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  if ((rc = fused_args(lbk::F_MXFP4, f, a)) < 0) return rc;
+  return run_fused(lbk::F_MXFP4, a, "fused MXFP4 GEMV launch", static_cast<hipStream_t>(stream));
+}
+
+int lbd_gemv_w4a8_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                        const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  if ((rc = fused_args(lbk::F_W4A8, f, a)) < 0) return rc;
+  return run_fused(lbk::F_W4A8, a, "fused W4A8 GEMV launch", static_cast<hipStream_t>(stream));
+}
+
+int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
+                        void *stream) {
+  if (!key || !tok) return fail(LB_ERR_ARG, "null pointer");
+  LB_LAUNCH(lbk::launch_argmax_finalize(key, tok, pos, inc, hist, hist_len, static_cast<hipStream_t>(stream)),
+            "argmax finalize launch");
+}
+
+int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
+                         const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *out,
+                         void *stream) {
+  if (H <= 0 || KV <= 0 || H % KV || H / KV > lbk::kAttnMaxGroup || (D != 32 && D != 64 && D != 128) ||
+      max_pos <= 0 || cap <= 0 || cap > 16000)
+    return fail(LB_ERR_SHAPE, "bad shape");
+  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out)
+    return fail(LB_ERR_ARG, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) != 0) return fail(LB_ERR_ARG, "k_cache must be 16-byte aligned");
+  LB_LAUNCH(lbk::launch_attention_decode(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap,
+                                         out, static_cast<hipStream_t>(stream)),
+            "attention decode launch");
+}
+
 // ---------------------------------------------------------------- host-pointer GEMMs
 
 int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,

@@ -198,8 +198,8 @@ __device__ __forceinline__ uint32_t quant4_fast(float4 v, float sc, float inv) {
   const float r0 = __builtin_rintf(u0), r1 = __builtin_rintf(u1);
   const float r2 = __builtin_rintf(u2), r3 = __builtin_rintf(u3);
   constexpr float kSafe = 0.5f - 0x1p-15f;
-  const bool ok = (fabsf(u0 - r0) < kSafe) & (fabsf(u1 - r1) < kSafe) &
-                  (fabsf(u2 - r2) < kSafe) & (fabsf(u3 - r3) < kSafe);
+  const bool ok = ((int)(fabsf(u0 - r0) < kSafe) & (int)(fabsf(u1 - r1) < kSafe) &
+                   (int)(fabsf(u2 - r2) < kSafe) & (int)(fabsf(u3 - r3) < kSafe)) != 0;
   uint32_t p = __builtin_amdgcn_cvt_pk_u8_f32(r0, 0, 0u);
   p = __builtin_amdgcn_cvt_pk_u8_f32(r1, 1, p);
   p = __builtin_amdgcn_cvt_pk_u8_f32(r2, 2, p);
@@ -238,6 +238,30 @@ __device__ __forceinline__ float block_row_amax(const float *__restrict__ xr, in
 
 __device__ __forceinline__ float row_scale(float amax) {
   return amax > 0.0f ? amax / 127.0f : 1.0f;
+}
+
+// ---------------------------------------------------------------- argmax keys
+//
+// (value, index) as one unsigned 64-bit key whose unsigned order is numpy's
+// argmax order: any NaN above every number, then larger values, then the smaller
+// index. The high word maps the float's bits to an unsigned order (-0 counts as
+// +0, as numpy compares them equal), the low word is 0xFFFFFFFF - index. Every
+// key is above 0, so 0 means "no value yet" and a 64-bit atomic max combines keys
+// from any number of waves.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t k;
+  if (v != v) {
+    k = 0xFFFFFFFFu;
+  } else {
+    if (v == 0.0f) u = 0;
+    k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((unsigned long long)k << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ int argmax_key_index(unsigned long long key) {
+  return key ? (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull)) : 0;
 }
 
 }  // namespace lbk

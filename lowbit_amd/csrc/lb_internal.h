@@ -25,7 +25,22 @@ struct GemmArgs {
   const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path)
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
   bool wt16 = false;              // qw / scales / zeros / e8m0 in the MFMA tile layout (t16)
+  // Decode fusions of the small-M kernels (gemv regime). Prologues (M == 1):
+  const float *norm_w = nullptr;  // RMSNorm of the activation row over Kp elements, times norm_w
+  float norm_eps = 0.0f;
+  bool swiglu = false;            // x row is [gate (Kp) | up (Kp)]; the activation is silu(gate) * up
+  // Epilogue: y = res + (x . w^T + bias); res may alias y.
+  const float *bias = nullptr;    // [N]
+  const float *res = nullptr;     // [M, N]
+  unsigned long long *amax_key = nullptr;  // M == 1: kArgmaxSlots argmax keys of the y row, max-combined
 };
+
+// Argmax keys are max-combined into this many slots (global wave index modulo the
+// slot count), so that no single address serialises thousands of atomics.
+constexpr int kArgmaxSlots = 1024;
+
+// Prologue of a fused GEMV: 0 none, 1 RMSNorm, 2 SwiGLU.
+inline int gemv_prologue(const GemmArgs &a) { return a.norm_w ? 1 : (a.swiglu ? 2 : 0); }
 
 // MFMA tile layout ("t16") of int4 g128 weights, a device-private copy of the
 // packed matrix in the order the int8 MFMA path consumes it. With S = ceil(N/16)
@@ -95,5 +110,12 @@ hipError_t launch_swiglu(const float *gu, int T, int I, float *out, hipStream_t 
 hipError_t launch_add(float *x, const float *y, size_t n, hipStream_t s);
 hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
                          hipStream_t s);
+hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist,
+                                  int hist_len, hipStream_t s);
+// One-token attention with the rotary embedding and the KV-cache write folded in.
+constexpr int kAttnMaxGroup = 16;  // query heads per KV head
+hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
+                                   const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
+                                   hipStream_t s);
 
 }  // namespace lbk

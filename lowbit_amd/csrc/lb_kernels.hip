@@ -348,7 +348,11 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
   }
 }
 
-template <int F, int MB, int R, int NIT>
+// PRO selects a fused prologue on the (single, register-held) activation row:
+// 0 none, 1 RMSNorm (x * (1 / sqrt(mean(x^2) + eps)) * norm_w, the mean over Kp),
+// 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
+// adds `bias` and `res` when given and max-combines argmax keys into `amax_key`.
+template <int F, int MB, int R, int NIT, int PRO>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[2][kGemvWaves];
@@ -375,7 +379,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
   //         row (slots past Kp read 0 through the row's buffer descriptor)
   constexpr int S = NIT;
   constexpr bool kXReg = (F != F_W4A8Q) && MB * S <= kXRegs;
+  static_assert(PRO == 0 || (MB == 1 && kXReg), "prologues take one register-held activation row");
   float4 xr[kXReg ? MB * S : 1];
+  float4 xe[PRO ? S : 1];  // RMSNorm weights, or the up half of a SwiGLU row
   if constexpr (kXReg) {
 #pragma unroll
     for (int m = 0; m < MB; m++) {
@@ -383,17 +389,68 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < S; i++) xr[m * S + i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
     }
+    if constexpr (PRO != 0) {
+      const Rsrc re = make_rsrc(PRO == 1 ? a.norm_w : a.x + Kp, (uint32_t)Kp * 4);
+#pragma unroll
+      for (int i = 0; i < S; i++) xe[i] = ld_f4(re, (threadIdx.x + i * T) * 16);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
 
-  // ---- 2. the weight stream of this wave's first R rows
+  // ---- 2. the weight stream of this wave's first R rows, then their epilogue
+  //         operands (bias, residual), so that the epilogue waits for no load
   GemvRegs<F, R, NIT> g;
+  float bv[R], rv[MB][R];
+  auto epi_load = [&](int rb) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int n = rb + r < N ? rb + r : N - 1;  // rows past the share are never stored
+      bv[r] = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+      for (int m = 0; m < MB; m++) rv[m][r] = a.res ? a.res[(size_t)m * N + n] : 0.0f;
+    }
+  };
   gemv_load<F, R, NIT>(a, g, r0, r1, lane, nch, G);
+  epi_load(r0);
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 3. stage the activations into LDS while the weights are in flight
-  //         (slot i covers elements [2048 i, 2048 i + 2048); slots past the padded
-  //         plane length are skipped on a block-uniform branch)
+  // ---- 3. fused prologue, then stage the activations into LDS while the weights
+  //         are in flight (slot i covers elements [2048 i, 2048 i + 2048); slots
+  //         past the padded plane length are skipped on a block-uniform branch;
+  //         elements past Kp are 0 and stay 0 under both prologues)
+  if constexpr (PRO == 1) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      ss = __builtin_fmaf(xr[i].x, xr[i].x, ss);
+      ss = __builtin_fmaf(xr[i].y, xr[i].y, ss);
+      ss = __builtin_fmaf(xr[i].z, xr[i].z, ss);
+      ss = __builtin_fmaf(xr[i].w, xr[i].w, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[0][wave] = ss;
+    __syncthreads();
+    float tot = red[0][0];
+#pragma unroll
+    for (int w = 1; w < kGemvWaves; w++) tot += red[0][w];
+    __syncthreads();  // red is reused by the quantizer below
+    const float rn = 1.0f / sqrtf(tot / (float)Kp + a.norm_eps);
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      xr[i].x = xr[i].x * rn * xe[i].x;
+      xr[i].y = xr[i].y * rn * xe[i].y;
+      xr[i].z = xr[i].z * rn * xe[i].z;
+      xr[i].w = xr[i].w * rn * xe[i].w;
+    }
+  } else if constexpr (PRO == 2) {
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      xr[i].x = xr[i].x / (1.0f + expf(-xr[i].x)) * xe[i].x;
+      xr[i].y = xr[i].y / (1.0f + expf(-xr[i].y)) * xe[i].y;
+      xr[i].z = xr[i].z / (1.0f + expf(-xr[i].z)) * xe[i].z;
+      xr[i].w = xr[i].w / (1.0f + expf(-xr[i].w)) * xe[i].w;
+    }
+  }
   if constexpr (!kInt8) {
     if constexpr (kXReg) {
 #pragma unroll
@@ -481,8 +538,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
 
   // ---- 4. decode + accumulate R rows at a time; later batches load as the
   //         previous one finishes
+  unsigned long long best = 0;  // argmax key of this wave's outputs
   for (int rb = r0; rb < r1; rb += R) {
-    if (rb != r0) gemv_load<F, R, NIT>(a, g, rb, r1, lane, nch, G);
+    if (rb != r0) {
+      gemv_load<F, R, NIT>(a, g, rb, r1, lane, nch, G);
+      epi_load(rb);
+    }
     const int nr = min(R, r1 - rb);
     float acc[MB][R];
 #pragma unroll
@@ -490,22 +551,38 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
     gemv_compute<F, MB, R, NIT>(g, acc, nr, lane, nchp, Gp, xl, ql, asl);
-    // ---- 5. one wave reduction per output; lane m*R + r stores it
+    // ---- 5. one wave reduction per output (every lane gets it), the epilogue,
+    //         and lane m*R + r stores it
 #pragma unroll
     for (int m = 0; m < MB; m++)
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (r >= nr) break;
         float t = wave_sum(acc[m][r]);
-        if constexpr (kInt8) t *= xsl[m];
-        if (lane == m * R + r) a.y[(size_t)m * N + rb + r] = t;
+        const int n = rb + r;
+        const size_t o = (size_t)m * N + n;
+        {
+          // y is rounded before the bias and the residual are added, as separate
+          // float32 adds after the GEMM would round it (no fused multiply-add)
+#pragma clang fp contract(off)
+          if constexpr (kInt8) t *= xsl[m];
+          if (a.bias) t += bv[r];
+          if (a.res) t = rv[m][r] + t;
+        }
+        if (lane == m * R + r) a.y[o] = t;
+        if (a.amax_key) {
+          const unsigned long long k = argmax_key(t, n);
+          best = k > best ? k : best;
+        }
       }
   }
+  // spread over the slots so that no address takes more than a few atomics
+  if (a.amax_key && lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
 }
 
 // Register-held chunks per lane (NIT) from the row length; rows per wave (R)
 // from the share of rows each wave gets under the persistent grid.
-template <int F, int MB, int NIT>
+template <int F, int MB, int NIT, int PRO>
 static hipError_t launch_gemv_nit(const GemmArgs &a, int grid, int rpw, size_t lds, hipStream_t s) {
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kGemvThreads), lds, s, a);
@@ -515,19 +592,19 @@ static hipError_t launch_gemv_nit(const GemmArgs &a, int grid, int rpw, size_t l
   // activations (larger shares are processed R rows at a time)
   constexpr int RMAX = MB == 1 ? (NIT >= 8 ? 1 : NIT >= 4 ? 2 : 4) : MB == 2 ? (NIT >= 4 ? 1 : 2) : 1;
   if constexpr (RMAX == 1) {
-    return go(gemv_kernel<F, MB, 1, NIT>);
+    return go(gemv_kernel<F, MB, 1, NIT, PRO>);
   } else if constexpr (RMAX == 2) {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT>);
-    return go(gemv_kernel<F, MB, 2, NIT>);
+    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
+    return go(gemv_kernel<F, MB, 2, NIT, PRO>);
   } else {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT>);
-    if (rpw <= 2) return go(gemv_kernel<F, MB, 2, NIT>);
-    if (rpw <= 3) return go(gemv_kernel<F, MB, 3, NIT>);
-    return go(gemv_kernel<F, MB, 4, NIT>);
+    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
+    if (rpw <= 2) return go(gemv_kernel<F, MB, 2, NIT, PRO>);
+    if (rpw <= 3) return go(gemv_kernel<F, MB, 3, NIT, PRO>);
+    return go(gemv_kernel<F, MB, 4, NIT, PRO>);
   }
 }
 
-template <int F, int MB>
+template <int F, int MB, int PRO>
 static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
   const int cus = num_cus > 0 ? num_cus : 256;
@@ -536,21 +613,28 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
   grid = grid < 2 * cus ? grid : 2 * cus;
   const int waves = grid * kGemvWaves;
   const int rpw = (a.N + waves - 1) / waves;
-  if (nit <= 1) return launch_gemv_nit<F, MB, 1>(a, grid, rpw, lds, s);
-  if (nit <= 2) return launch_gemv_nit<F, MB, 2>(a, grid, rpw, lds, s);
-  if (nit <= 4) return launch_gemv_nit<F, MB, 4>(a, grid, rpw, lds, s);
+  if (nit <= 1) return launch_gemv_nit<F, MB, 1, PRO>(a, grid, rpw, lds, s);
+  if (nit <= 2) return launch_gemv_nit<F, MB, 2, PRO>(a, grid, rpw, lds, s);
+  if (nit <= 4) return launch_gemv_nit<F, MB, 4, PRO>(a, grid, rpw, lds, s);
   // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
   if constexpr ((F == F_W4A16 || F == F_MXFP4) && MB >= 2) return hipErrorInvalidValue;
-  else return launch_gemv_nit<F, MB, 8>(a, grid, rpw, lds, s);
+  else return launch_gemv_nit<F, MB, 8, PRO>(a, grid, rpw, lds, s);
 }
 
 template <int F>
 static hipError_t launch_gemv_f(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
+  const int pro = gemv_prologue(a);
+  if (pro != 0) {
+    if (a.M != 1 || (a.norm_w && a.swiglu)) return hipErrorInvalidValue;
+    if constexpr (F == F_W4A8Q) return hipErrorInvalidValue;  // the prologues act on fp32 rows
+    else if (pro == 1) return launch_gemv_mb<F, 1, 1>(a, num_cus, lds, s);
+    else return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s);
+  }
   switch (a.M) {
-    case 1: return launch_gemv_mb<F, 1>(a, num_cus, lds, s);
-    case 2: return launch_gemv_mb<F, 2>(a, num_cus, lds, s);
-    case 3: return launch_gemv_mb<F, 3>(a, num_cus, lds, s);
-    case 4: return launch_gemv_mb<F, 4>(a, num_cus, lds, s);
+    case 1: return launch_gemv_mb<F, 1, 0>(a, num_cus, lds, s);
+    case 2: return launch_gemv_mb<F, 2, 0>(a, num_cus, lds, s);
+    case 3: return launch_gemv_mb<F, 3, 0>(a, num_cus, lds, s);
+    case 4: return launch_gemv_mb<F, 4, 0>(a, num_cus, lds, s);
   }
   return hipErrorInvalidValue;
 }
@@ -1286,7 +1370,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int q = lane >> 4, c = lane & 15;
+  const int c = lane & 15;
   const int M = a.M, N = a.N, Kp = a.Kp, G = (Kp + 127) / 128, G4 = t16_groups(Kp);
   const int mb0 = blockIdx.y * TM, m0 = mb0 * 16;
   const int S = (N + 15) / 16;

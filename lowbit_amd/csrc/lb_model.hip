@@ -156,6 +156,246 @@ __global__ __launch_bounds__(kWave) void attention_kernel(const float *__restric
   }
 }
 
+// One-token attention (the decode step) with the rotary embedding and the KV-cache
+// write folded in: the q / k / v row of the token (bias already added by the GEMM
+// epilogue) sits in qkv [(H + 2 KV) D] at absolute position p = *pos. One workgroup
+// per query head h (grid KV x H/KV; KV head g = h / (H/KV)). The step is a chain
+// of memory round trips, so the kernel is laid out to need as few as possible:
+//   0. before anything else (and before *pos arrives) thread t loads key row t and
+//      wave w the value rows 64 w .. 64 w + 63 of the first chunk into registers
+//      (rows below cap; D <= 64);
+//   1. rotate the query head and the key ("rotate_half", src/lowbit/model.py:
+//      201-210) into LDS; the group's first workgroup writes the rotated key and
+//      the value to the caches at p (when p < cap);
+//   2. over chunks of kAttChunk keys (online softmax, src/lowbit/model.py:353-378):
+//      thread t scores key c0 + t, the chunk maximum updates the running maximum,
+//      and wave w accumulates p * v over its 64 keys, lane l owning output
+//      elements l, l + 64, ...;
+//   3. the waves' partial sums are added in LDS and divided by the softmax sum.
+// Keys 0 .. S-1 with S = min(p + 1, cap) take part; when p < cap key p is the new
+// one (from LDS, never read back from the cache), otherwise all S come from the
+// cache, as lbd_qkv_rope + lbd_attention behave. Output out [H D].
+constexpr int kAttThreads = 256;
+constexpr int kAttWaves = kAttThreads / kWave;
+constexpr int kAttChunk = kAttThreads;
+constexpr int kAttVB = 16;  // values in flight per lane in the p * v loop past the first chunk
+
+template <int D>
+__global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
+    const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
+    const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc, float *__restrict__ vc, int cap,
+    float *__restrict__ out) {
+  constexpr int half = D / 2, DPL = (D + kWave - 1) / kWave, NK4 = D / 4;
+  constexpr bool kPre = D <= 64;
+  __shared__ __align__(16) float qs[D];
+  __shared__ __align__(16) float kn[D];
+  __shared__ float vn[D];
+  __shared__ float pb[kAttChunk];
+  __shared__ float red[kAttWaves];
+  __shared__ float part[kAttWaves][D];
+  __shared__ float lsw[kAttWaves];
+  const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const float *kb = kc + (size_t)g * cap * D;
+  const float *vb = vc + (size_t)g * cap * D;
+  const bool own = D >= kWave || lane < D;  // D = 32: lanes 32..63 hold no output
+  const int l = own ? lane : 0;
+
+  // ---- 0. prefetch of the first chunk's keys and values (rows clamped below cap)
+  float4 kpre[kPre ? NK4 : 1];
+  float vpre[kPre ? kWave * DPL : 1];
+  if constexpr (kPre) {
+    const int t = tid < cap ? tid : cap - 1;
+    const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)t * D);
+#pragma unroll
+    for (int e = 0; e < NK4; e++) kpre[e] = kr[e];
+#pragma unroll
+    for (int u = 0; u < kWave; u++) {
+      const int row = wave * kWave + u < cap ? wave * kWave + u : cap - 1;
+#pragma unroll
+      for (int q = 0; q < DPL; q++) vpre[u * DPL + q] = vb[(size_t)row * D + l + kWave * q];
+    }
+  }
+
+  const int p = *pos;
+  const int pc = p < 0 ? 0 : (p < max_pos ? p : max_pos - 1);  // positions past the tables reuse the last angle
+  const bool newk = p >= 0 && p < cap;
+  const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
+  const int Sc = newk ? S - 1 : S;  // keys read from the cache; key Sc is the new one when newk
+
+  // ---- 1. rotary embedding of the query head and of the key; the value
+  for (int e = tid; e < 2 * half; e += kAttThreads) {
+    const int which = e / half, i = e - which * half;  // 0: query head h, 1: key head g
+    const int hd = which == 0 ? h : H + g;
+    const float x1 = qkv[(size_t)hd * D + i], x2 = qkv[(size_t)hd * D + i + half];
+    const float c = cosT[(size_t)pc * half + i], sn = sinT[(size_t)pc * half + i];
+    const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+    if (which == 0) {
+      qs[i] = y1;
+      qs[i + half] = y2;
+    } else {
+      kn[i] = y1;
+      kn[i + half] = y2;
+      if (newk && j == 0) {
+        kc[((size_t)g * cap + p) * D + i] = y1;
+        kc[((size_t)g * cap + p) * D + i + half] = y2;
+      }
+    }
+  }
+  for (int e = tid; e < D; e += kAttThreads) {
+    const float v = qkv[(size_t)(H + KV + g) * D + e];
+    vn[e] = v;
+    if (newk && j == 0) vc[((size_t)g * cap + p) * D + e] = v;
+  }
+  __syncthreads();
+
+  const float scale = 1.0f / sqrtf((float)D);
+  float acc[DPL], lsum = 0.0f, mrun = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < DPL; q++) acc[q] = 0.0f;
+
+  for (int c0 = 0; c0 < S; c0 += kAttChunk) {
+    const bool pre = kPre && c0 == 0;
+    // ---- 2a. score of key c0 + tid
+    const int s = c0 + tid;
+    float d = 0.0f;
+    if (s < S) {
+      float4 kv[NK4];
+      if (s >= Sc) {
+#pragma unroll
+        for (int e = 0; e < NK4; e++) kv[e] = reinterpret_cast<const float4 *>(kn)[e];
+      } else if (pre) {
+#pragma unroll
+        for (int e = 0; e < NK4; e++) kv[e] = kpre[e < (kPre ? NK4 : 1) ? e : 0];
+      } else {
+        const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)s * D);
+#pragma unroll
+        for (int e = 0; e < NK4; e++) kv[e] = kr[e];
+      }
+#pragma unroll
+      for (int e = 0; e < NK4; e++) {
+        const float4 qv = reinterpret_cast<const float4 *>(qs)[e];
+        d = __builtin_fmaf(qv.x, kv[e].x, d);
+        d = __builtin_fmaf(qv.y, kv[e].y, d);
+        d = __builtin_fmaf(qv.z, kv[e].z, d);
+        d = __builtin_fmaf(qv.w, kv[e].w, d);
+      }
+    }
+    d = s < S ? d * scale : -INFINITY;
+    const float mw = wave_max(d);
+    if (lane == 0) red[wave] = mw;
+    __syncthreads();
+    // ---- 2b. running maximum, probabilities of this chunk, rescaled accumulators
+    float cm = red[0];
+#pragma unroll
+    for (int w = 1; w < kAttWaves; w++) cm = fmaxf(cm, red[w]);
+    const float mnew = fmaxf(mrun, cm);
+    const float alpha = expf(mrun - mnew);  // 0 on the first chunk
+    mrun = mnew;
+    lsum *= alpha;
+#pragma unroll
+    for (int q = 0; q < DPL; q++) acc[q] *= alpha;
+    pb[tid] = s < S ? expf(d - mnew) : 0.0f;
+    __syncthreads();
+    // ---- 2c. wave w: p * v over keys c0 + 64 w .. c0 + 64 w + 63; the new key's
+    //          value from LDS
+    const int sb = c0 + wave * kWave;
+    const int se = sb + kWave < S ? sb + kWave : S;
+    const int sce = se < Sc ? se : Sc;
+    if (pre) {
+#pragma unroll
+      for (int u = 0; u < kWave; u++) {
+        if (sb + u < sce) {
+          const float pr = pb[sb + u - c0];
+          lsum += pr;
+#pragma unroll
+          for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, vpre[(u * DPL + q) % (kPre ? kWave * DPL : 1)], acc[q]);
+        }
+      }
+    } else {
+      for (int k0 = sb; k0 < sce; k0 += kAttVB) {
+        float v[kAttVB][DPL];
+#pragma unroll
+        for (int u = 0; u < kAttVB; u++) {
+          const int k = k0 + u < sce ? k0 + u : sce - 1;  // in-range row; its weight is dropped below
+#pragma unroll
+          for (int q = 0; q < DPL; q++) v[u][q] = vb[(size_t)k * D + l + kWave * q];
+        }
+#pragma unroll
+        for (int u = 0; u < kAttVB; u++) {
+          if (k0 + u < sce) {
+            const float pr = pb[k0 + u - c0];
+            lsum += pr;
+#pragma unroll
+            for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, v[u][q], acc[q]);
+          }
+        }
+      }
+    }
+    if (newk && Sc >= sb && Sc < se) {
+      const float pr = pb[Sc - c0];
+      lsum += pr;
+#pragma unroll
+      for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, vn[l + kWave * q], acc[q]);
+    }
+    __syncthreads();  // pb is rewritten by the next chunk
+  }
+
+  // ---- 3. add the waves' partial sums
+  if (own) {
+#pragma unroll
+    for (int q = 0; q < DPL; q++) part[wave][l + kWave * q] = acc[q];
+  }
+  if (lane == 0) lsw[wave] = lsum;
+  __syncthreads();
+  for (int e = tid; e < D; e += kAttThreads) {
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttWaves; w++) {
+      num += part[w][e];
+      den += lsw[w];
+    }
+    out[(size_t)h * D + e] = num / den;
+  }
+}
+
+// tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
+// max-combined (the one argmax_kernel would pick from the logits); advances *pos
+// and records hist[*pos] like argmax_kernel, and clears every slot for the next
+// step. One workgroup of 256 threads, four slots each.
+constexpr int kFinT = 256;
+__global__ __launch_bounds__(kFinT) void argmax_finalize_kernel(unsigned long long *__restrict__ key,
+                                                                int32_t *__restrict__ tok, int32_t *__restrict__ pos,
+                                                                int inc, int32_t *__restrict__ hist, int hist_len) {
+  static_assert(kArgmaxSlots == 4 * kFinT, "four slots per thread");
+  __shared__ unsigned long long wbest[kFinT / kWave];
+  unsigned long long b = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const unsigned long long k = key[threadIdx.x + i * kFinT];
+    b = k > b ? k : b;
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(b, off);
+    b = o > b ? o : b;
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) wbest[threadIdx.x / kWave] = b;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; i++) key[threadIdx.x + i * kFinT] = 0;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kFinT / kWave; w++) b = wbest[w] > b ? wbest[w] : b;
+    const int ix = argmax_key_index(b);
+    tok[0] = ix;
+    if (pos) {
+      const int p = *pos + inc;
+      if (hist && p >= 0 && p < hist_len) hist[p] = ix;
+      *pos = p;
+    }
+  }
+}
+
 // out[t, i] = silu(gu[t, i]) * gu[t, I + i], silu(g) = g / (1 + exp(-g))
 // (src/lowbit/model.py:213, 416-417).
 __global__ __launch_bounds__(kMT) void swiglu_kernel(const float *__restrict__ gu, int T, int I,
@@ -273,6 +513,31 @@ hipError_t launch_add(float *x, const float *y, size_t n, hipStream_t s) {
 hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
                          hipStream_t s) {
   hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kAT), 0, s, v, n, tok, pos, inc, hist, hist_len);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
+                                   const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
+                                   hipStream_t s) {
+  if (KV <= 0 || H % KV || H / KV > kAttnMaxGroup || cap <= 0) return hipErrorInvalidValue;
+  const dim3 grid(KV, H / KV);
+  if (D == 32)
+    hipLaunchKernelGGL(attention_decode_kernel<32>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else if (D == 64)
+    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else if (D == 128)
+    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist,
+                                  int hist_len, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(kFinT), 0, s, key, tok, pos, inc, hist, hist_len);
   return hipGetLastError();
 }
 

@@ -130,7 +130,19 @@ SIGNATURES = {
     "lbd_swiglu": ([_vp, _int, _int, _vp, _vp], _int),
     "lbd_add": ([_vp, _vp, _sz, _vp], _int),
     "lbd_argmax": ([_vp, _int, _vp, _vp, _int, _vp, _int, _vp], _int),
+    "lbd_gemv_w4a16_fused": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
+    "lbd_gemv_mxfp4_fused": ([_vp, _int, _int, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
+    "lbd_gemv_w4a8_fused": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
+    "lbd_argmax_finalize": ([_vp, _vp, _vp, _int, _vp, _int, _vp], _int),
+    "lbd_attention_decode": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _vp], _int),
 }
+
+
+class LbdFusion(C.Structure):
+    """lbd_fusion of include/lowbit_hip.h: the prologue / epilogue of a fused GEMV
+    (pass C.byref(f) as the `f` argument)."""
+    _fields_ = [("norm_w", C.c_void_p), ("norm_eps", C.c_float), ("swiglu", C.c_int),
+                ("bias", C.c_void_p), ("residual", C.c_void_p), ("argmax_key", C.c_void_p)]
 
 
 @lru_cache(maxsize=1)

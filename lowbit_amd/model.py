@@ -13,6 +13,15 @@ The decode position lives in device memory and the argmax writes the next token
 id where the embedding lookup reads it, so one decode step is a fixed sequence
 of launches: `generate` records it once as a HIP graph and replays it per token.
 
+A one-token step (fused=True, the default) runs five launches per layer: each
+linear layer is one fused GEMV (`lbd_gemv_*_fused`) whose prologue applies the
+RMSNorm (q/k/v, gate/up, LM head) or the SwiGLU (down) to its activation row and
+whose epilogue adds the q/k/v bias or the residual in place; the rotary embedding
+and the KV-cache write run inside the one-token attention
+(`lbd_attention_decode`); the LM head's epilogue folds the greedy argmax into a
+64-bit key that `lbd_argmax_finalize` turns into the next token. Prompts (T > 1)
+run the unfused sequence on the matrix-core GEMMs.
+
 Same architecture and arithmetic as the reference model: RMSNorm in fp32, q/k/v
 and gate/up projections concatenated along N (quantization is per output row,
 so no quantized value changes), rotary embedding in the "rotate_half"
@@ -35,6 +44,7 @@ from . import kernels as K
 
 BACKENDS = ("w4a16", "w4a8", "mxfp4")
 _KIND = {"w4a16": 0, "mxfp4": 1, "w4a8": 2}
+ARGMAX_SLOTS = 1024  # LBD_ARGMAX_SLOTS of include/lowbit_hip.h
 
 
 # ---------------------------------------------------------------- config (src/lowbit/model.py:42-77)
@@ -158,7 +168,7 @@ class Model:
 
     def __init__(self, cfg: ModelConfig, weights: dict, backend: str = "w4a8", asym: bool = False,
                  quantize_lm_head: bool = True, int4_scale: str = "absmax", max_tokens: int = 512,
-                 quantize_on_device: bool = True):
+                 quantize_on_device: bool = True, fused: bool = True):
         if backend not in BACKENDS:
             raise ValueError(f"backend must be one of {BACKENDS}")
         if not quantize_lm_head:
@@ -208,6 +218,16 @@ class Model:
         self.tok = _buf(4 * max(max_tokens, 1))
         self.pos = _buf(4)
         self.hist: K.DeviceBuffer | None = None
+        # argmax key slots of the fused LM head; lbd_argmax_finalize clears them
+        self.key = _buf(8 * ARGMAX_SLOTS)
+        _check(self.L.lb_memset_d(self.key.ptr, 0, 8 * ARGMAX_SLOTS), "key clear")
+        # one-token steps fuse when every linear takes the small-M kernels and the
+        # attention shape fits the one-token kernel
+        D = cfg.head_dim
+        widths = {cfg.hidden_size, cfg.intermediate_size, cfg.num_heads * D}
+        prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
+        self.fused = bool(fused) and D in (32, 64, 128) and cfg.num_heads // cfg.num_kv_heads <= 16 and all(
+            self.L.lbd_gemm_path(_KIND[backend], 1, k, C.byref(prm)) == K.ISA_GFX950 for k in widths)
 
     # ------------------------------------------------------------ buffers
 
@@ -263,8 +283,53 @@ class Model:
                                      ws.nbytes, s)
         _check(rc, f"{self.backend} linear")
 
+    def _fused_linear(self, w, x: int, y: int, norm: int | None = None, swiglu: bool = False,
+                      bias: int | None = None, res: int | None = None, key: int | None = None):
+        """y[0, n] = res[n] + (act(x) . w^T)[n] + bias[n] for one token, one launch;
+        act is the RMSNorm with weights `norm` or the SwiGLU of x = [gate | up]."""
+        f = K.LbdFusion(norm, self.cfg.rms_norm_eps if norm else 0.0, int(swiglu), bias, res, key)
+        L, s = self.L, self.stream
+        if self.backend == "mxfp4":
+            rc = L.lbd_gemv_mxfp4_fused(x, 1, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, y, C.byref(f), s)
+        else:
+            zp = None if w.zeros is None else w.zeros.ptr
+            fn = L.lbd_gemv_w4a16_fused if self.backend == "w4a16" else L.lbd_gemv_w4a8_fused
+            rc = fn(x, 1, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, y, C.byref(f), s)
+        _check(rc, f"fused {self.backend} linear")
+
+    def _step_fused(self, cache: KVCache, logits: str, argmax_hist: bool):
+        """Enqueue one forward of the single token in self.tok at position *pos,
+        five launches per layer."""
+        cfg, L, s = self.cfg, self.L, self.stream
+        h, H, KV, D = cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        x = self.x.ptr
+        _check(L.lbd_embed(self.embed.ptr, cfg.vocab_size, h, self.tok.ptr, 1, x, s), "embed")
+        for li, ly in enumerate(self.layers):
+            self._fused_linear(ly.qkv, x, self.qkv.ptr, norm=ly.ln1.ptr,
+                               bias=None if ly.qkv_bias is None else ly.qkv_bias.ptr)
+            _check(L.lbd_attention_decode(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
+                                          cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
+                                          self.att.ptr, s), "attention decode")
+            self._fused_linear(ly.o, self.att.ptr, x, res=x)
+            self._fused_linear(ly.gate_up, x, self.gu.ptr, norm=ly.ln2.ptr)
+            self._fused_linear(ly.down, self.gu.ptr, x, swiglu=True, res=x)
+        if logits == "none":
+            _check(L.lbd_rmsnorm(x, self.norm.ptr, 1, h, cfg.rms_norm_eps, self.h.ptr, s), "rmsnorm")
+        elif logits == "last":
+            key = self.key.ptr if argmax_hist else None
+            self._fused_linear(self.lm_head, x, self.logits.ptr, norm=self.norm.ptr, key=key)
+            if argmax_hist:
+                hist = self.hist.ptr if self.hist is not None else None
+                n = self.hist.nbytes // 4 if self.hist is not None else 0
+                _check(L.lbd_argmax_finalize(self.key.ptr, self.tok.ptr, self.pos.ptr, 1, hist, n, s),
+                       "argmax finalize")
+        else:
+            self._fused_linear(self.lm_head, x, self.all_logits.ptr, norm=self.norm.ptr)
+
     def _step(self, T: int, cache: KVCache, logits: str, argmax_hist: bool):
         """Enqueue one forward of the T tokens in self.tok at position *pos."""
+        if T == 1 and self.fused:
+            return self._step_fused(cache, logits, argmax_hist)
         cfg, L, s = self.cfg, self.L, self.stream
         h, I, H, KV, D = cfg.hidden_size, cfg.intermediate_size, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
         qkvw = (H + 2 * KV) * D

@@ -136,3 +136,11 @@ def test_t16_sizes_and_argument_checks():
     assert L.lbd_gemm_path(2, 1, 4096, C.byref(prm)) == K.ISA_GFX950
     assert L.lbd_gemm_path(2, 64, 4096, C.byref(prm)) == K.ISA_GFX950_MFMA
     assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6
+
+
+def test_argmax_slot_count_matches_header():
+    import re
+
+    from lowbit_amd import model as DM
+    m = re.search(r"#define LBD_ARGMAX_SLOTS (\d+)", HEADER.read_text())
+    assert m and int(m.group(1)) == DM.ARGMAX_SLOTS
