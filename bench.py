@@ -19,7 +19,11 @@ The CPU baseline times the reference's own C library (oracle/_ref, built from
 the reference sources) on this host's cores on a bounded sample of the same
 workload; it is a reported baseline only.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+The config-5 decoder (a Qwen2.5-0.5B-shaped model with random weights, every
+linear layer W4A8 or MXFP4) is timed as tokens/s of greedy decoding under
+"decoder", beside the reference's published CPU tokens/s.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--no-decoder]
 """
 from __future__ import annotations
 
@@ -309,6 +313,53 @@ def cpu_baseline(W, x: np.ndarray, budget_s: float) -> dict | None:
     }
 
 
+# Qwen2.5-0.5B-shaped decoder, 64-token random prompt, 128 greedy
+# decode steps (src/lowbit/e2e.py:119-122,194: tok/s = decode forwards / decode time).
+# The reference's published decode tok/s on its Xeon (README.md:199-200, real weights,
+# 1 / 4 threads).
+DECODER_REF_TOKS = {"w4a8": (25.87, 63.80), "mxfp4": (19.74, 50.13)}
+
+
+def measure_decoder(backends, n_decode: int = 128, prompt_len: int = 64, reps: int = 3, graph: bool = True) -> dict:
+    """Greedy decode of the config-5 decoder with random weights (the shapes of
+    Qwen2.5-0.5B), device-resident, each decode step one replayed HIP graph
+    (graph=False: the same kernels launched one by one)."""
+    from lowbit_amd import model as DM
+    cfg = DM.qwen2_config()
+    t0 = time.perf_counter()
+    W = DM.random_weights(cfg, seed=0, float32_draws=True)
+    log(f"decoder: random weights in {time.perf_counter() - t0:.1f} s")
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab_size, prompt_len).tolist()
+    out = {}
+    for be in backends:
+        m = DM.Model(cfg, W, be, max_tokens=prompt_len)
+        m.generate(prompt[:8], 4, graph=graph)  # warm-up: kernels loaded, t16 copies built
+        best = None
+        for _ in range(reps):
+            tim = {}
+            toks = m.generate(prompt, n_decode + 1, timings=tim, graph=graph)
+            dec = tim["decode_s"] / tim["decode_forwards"]
+            if best is None or dec < best[0]:
+                best = (dec, tim["prefill_s"], toks)
+        dec, pre, toks = best
+        wb = m.linear_weight_bytes
+        ref1, ref4 = DECODER_REF_TOKS[be]
+        out[be] = {
+            "decode_tok_s": round(1.0 / dec, 1), "ms_per_token": round(dec * 1e3, 4),
+            "prefill_tok_s": round(prompt_len / pre, 1), "prompt": prompt_len, "decode_steps": n_decode,
+            "fused_decode": m.fused, "graph": graph, "linear_weight_bytes": wb,
+            # weight stream per token against HBM: the bound is wb / 8 TB/s
+            "weight_gbps": round(wb / dec / 1e9, 1), "hbm_frac": round(wb / dec / 1e9 / HBM_PEAK_GBS, 4),
+            "hbm_bound_tok_s": round(HBM_PEAK_GBS * 1e9 / wb, 1),
+            "reference_cpu_tok_s": {"1_thread": ref1, "4_threads": ref4},
+            "first_tokens": toks[:4],
+        }
+        log(f"decoder {be}: decode {1.0 / dec:8.1f} tok/s ({dec * 1e3:.3f} ms/token, "
+            f"{wb / dec / 1e9:.0f} GB/s of weights), prefill {prompt_len / pre:8.1f} tok/s")
+        del m
+    return out
+
+
 def traffic_bytes() -> int | None:
     """HBM bytes per launch of the headline kernel, from the committed counter summary."""
     if not TRAFFIC_FILE.exists():
@@ -330,6 +381,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=6.0, help="CPU baseline time budget")
     ap.add_argument("--no-graph", action="store_true", help="time plain launches instead of a graph replay")
     ap.add_argument("--only-headline", action="store_true", help="measure only the headline W4A8 decode")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the config-5 decoder (tokens/s)")
+    ap.add_argument("--only-decoder", action="store_true",
+                    help="measure only the config-5 decoder and print its JSON (for kernel traces)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the plain 16-byte copy kernel 5 times over MIB MiB (the reference "
                          "point that scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
@@ -355,9 +409,12 @@ def main() -> int:
         return 0
     info = dev.K.cpu_info()
     log(f"device {info.get('arch')} with {info.get('compute_units')} CUs")
+    graph = not args.no_graph
+    if args.only_decoder:
+        print(json.dumps({"decoder": measure_decoder(["w4a8", "mxfp4"], graph=graph)}), flush=True)
+        return 0
     rng = np.random.default_rng(0)
     results = {}
-    graph = not args.no_graph
 
     # decode: all three formats at 1 x 11008 x 4096, cold
     m, n, k = DECODE
@@ -399,6 +456,10 @@ def main() -> int:
             log(f"{fmt:6s} M=64 hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
                 f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}")
 
+    decoder = None
+    if not (args.only_headline or args.no_decoder):
+        decoder = measure_decoder(["w4a8", "mxfp4"], graph=graph)
+
     head = results["w4a8_decode"]
     t_launch_s = head["us_per_call"] * 1e-6
     # algorithmic bytes of one launch: packed weights + fp32 X + fp32 Y
@@ -434,6 +495,7 @@ def main() -> int:
                      "algorithmic_bytes": int(algo_bytes)},
         "cpu_baseline": cpu,
         "per_format": {kk: {f: v for f, v in vv.items() if f not in ("N", "K")} for kk, vv in results.items()},
+        "decoder": decoder,
     }
     print(json.dumps(line), flush=True)
     return 0
