@@ -212,3 +212,32 @@ def test_mxfp4_bf16x3_extreme_exponents(rng):
     assert nan[:, 5].all() and nan.sum() == m
     keep = ~nan
     assert np.all(np.abs(y[keep] - ref[keep]) <= 1e-5 * bound[keep])
+
+
+# ---------------------------------------------------------------- prefill-sized M
+
+@pytest.mark.parametrize("m,n,k", [(512, 300, 4096), (2048, 48, 1024), (1000, 70, 1152)])
+def test_prefill_m_within_bound(rng, m, n, k):
+    """Prompt-sized M (many 16-row blocks per column of workgroups) on all three
+    matrix-core paths: W4A8 int8 MFMA, W4A16 / MXFP4 bf16x3 on t16 weights, and the
+    fp32 MFMA kernel of the pointer ABI (row-major weights)."""
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = _lognormal_rows(rng, n, k)
+    W4 = lb.quantize_int4(w, asym=True)
+    y8 = K.gemm_w4a8(x, lb.to_device(W4))
+    assert K.last_path() == "gfx950-mfma"
+    a = lb.quantize_act_int8(x, W4.kp)
+    ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W4.qw, W4.scales, W4.zeros)
+    O.assert_fp_close(y8, ref, bound, 1e-5)
+    xp = lb.formats.pad_acts(x, W4.kp)
+    ref = cref.c_gemm_w4a16(xp, W4.qw, W4.scales, W4.zeros)
+    bound = cref.c_gemm_w4a16(xp, W4.qw, W4.scales, W4.zeros, absval=True)
+    for y in (K.gemm_w4a16(x, lb.to_device(W4)), K.gemm_w4a16(x, W4)):
+        assert K.last_path() == "gfx950-mfma"
+        O.assert_fp_close(y, ref, bound, 1e-5)
+    Wm = lb.quantize_mxfp4(w)
+    xp = lb.formats.pad_acts(x, Wm.kp)
+    ref = cref.c_gemm_mxfp4(xp, Wm.qw, Wm.e8m0)
+    bound = cref.c_gemm_mxfp4(xp, Wm.qw, Wm.e8m0, absval=True)
+    for y in (K.gemm_mxfp4(x, lb.to_device(Wm)), K.gemm_mxfp4(x, Wm)):
+        O.assert_fp_close(y, ref, bound, 1e-5)
