@@ -50,6 +50,7 @@ extern "C" {
 
 #define LB_GROUP 128  /* int4 group size (elements) */
 #define LB_MXBLOCK 32 /* MXFP4 block size (elements) */
+#define LB_G32 32     /* the group size of the group-32 int4 entry points */
 
 /* Path ids, returned by the GEMMs like the reference returns its ISA id
  * (src/lowbit/csrc/dispatch.c:202). The reference's CPU ids 0..2 (scalar, avx2,
@@ -218,6 +219,26 @@ int lbd_quantize_int4(const float *w, int N, int K, int asym, int signed_max, ui
 /* MXFP4 -> qw [N, Kp/2], e8m0 [N, Kp/32]; Kp = K rounded up to 32 */
 int lbd_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0,
                        void *stream);
+
+/* ---- int4 with groups of 32 (no lowbit.h counterpart: the reference ships group 128
+ *      only and names groups of 32 as its main quality lever, README.md:300-304,
+ *      511-512). Layout of each row: group g is bytes [16g, 16g+16); byte j holds
+ *      element 32g+j (low nibble) and 32g+16+j (high nibble), the arrangement of the
+ *      MXFP4 blocks; value = (q - z) * s with fp32 scales[N, Kp/32] and uint8
+ *      zeros[N, Kp/32] (NULL: z = 8). Kp is a multiple of 32, at most 14336 for
+ *      W4A16 (fp32 activations staged in LDS) and 16384 for W4A8. ---- */
+/* y = x . w^T, fp32 activations and accumulation (the W4A16 semantics); device
+ * pointers, asynchronous on `stream`. Any M: the small-M kernels run on slices of
+ * at most four rows (there is no matrix-core path for groups of 32). */
+int lbd_gemm_w4a16_g32(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                       const uint8_t *zeros, int N, float *y, void *stream);
+/* W4A8: x quantized per token to int8 inside the call (the reference's quantizer),
+ * exact int32 sums per group of 32, then s and the token scale in fp32 */
+int lbd_gemm_w4a8_g32(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
+                      const uint8_t *zeros, int N, float *y, void *stream);
+/* lbd_quantize_int4 with groups of 32: scales / zeros [N, Kp/32], Kp = K rounded up to 32 */
+int lbd_quantize_int4_g32(const float *w, int N, int K, int asym, int signed_max, uint8_t *qw,
+                          float *scales, uint8_t *zeros, void *stream);
 
 /* ---- decoder-layer operations for a device-resident decoder (no lowbit.h
  *      counterpart: the building blocks of the reference's numpy model,

@@ -7,6 +7,7 @@
 // stage their operands through device memory owned by the calling thread.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -442,8 +443,21 @@ int lbd_quantize_int4(const float *w, int N, int K, int asym, int signed_max, ui
   if (asym && signed_max) return fail(LB_ERR_ARG, "signed-max is a symmetric rule");
   if (!w || !qw || !scales || (asym && !zeros)) return fail(LB_ERR_ARG, "null pointer");
   const int mode = asym ? 2 : (signed_max ? 1 : 0);
-  hipError_t e = lbk::launch_quantize_int4(w, N, K, mode, qw, scales, zeros, static_cast<hipStream_t>(stream));
+  hipError_t e = lbk::launch_quantize_int4(w, N, K, mode, LB_GROUP, qw, scales, zeros,
+                                           static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail_hip(e, "int4 quantizer launch");
+  return ok(0);
+}
+
+int lbd_quantize_int4_g32(const float *w, int N, int K, int asym, int signed_max, uint8_t *qw, float *scales,
+                          uint8_t *zeros, void *stream) {
+  if (N <= 0 || K <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (asym && signed_max) return fail(LB_ERR_ARG, "signed-max is a symmetric rule");
+  if (!w || !qw || !scales || (asym && !zeros)) return fail(LB_ERR_ARG, "null pointer");
+  const int mode = asym ? 2 : (signed_max ? 1 : 0);
+  hipError_t e = lbk::launch_quantize_int4(w, N, K, mode, LB_G32, qw, scales, zeros,
+                                           static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "int4 g32 quantizer launch");
   return ok(0);
 }
 
@@ -734,6 +748,64 @@ int lbd_gemv_w4a8_fused(const float *x, int M, int Kp, const uint8_t *qw, const 
   a.M = M; a.Kp = Kp; a.N = N;
   if ((rc = fused_args(lbk::F_W4A8, f, a)) < 0) return rc;
   return run_fused(lbk::F_W4A8, a, "fused W4A8 GEMV launch", static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+
+// Group-32 int4 GEMMs: the small-M kernels over slices of at most four activation
+// rows (every slice reads the weights again; there is no matrix-core path for
+// groups of 32).
+int run_g32(int fmt, const lbk::GemmArgs &a0, hipStream_t s) {
+  int mb = 0;
+  const int nit = ((a0.Kp >> 5) + 63) / 64;
+  for (int m = 4; m >= 1 && !mb; m--) {
+    const bool fp32_rows = fmt == lbk::F_W4A16G32 && m >= 2 && nit > 4;  // no such instantiation
+    if (!fp32_rows && lbk::gemv_eligible(fmt, m, a0.Kp)) mb = m;
+  }
+  if (!mb) return fail(LB_ERR_SHAPE, "group-32 GEMMs take Kp up to 14336 (W4A16) / 16384 (W4A8)");
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  for (int m0 = 0; m0 < a0.M; m0 += mb) {
+    lbk::GemmArgs a = a0;
+    a.x = a0.x + (size_t)m0 * a0.Kp;
+    a.y = a0.y + (size_t)m0 * a0.N;
+    a.M = std::min(mb, a0.M - m0);
+    hipError_t e = lbk::launch_gemv(fmt, a, cus, s);
+    if (e != hipSuccess) return fail_hip(e, "group-32 GEMV launch");
+  }
+  return ok(LB_ISA_GFX950);
+}
+
+int g32_args(const float *x, int M, int Kp, const uint8_t *qw, const float *scales, const uint8_t *zeros, int N,
+             float *y, lbk::GemmArgs &a) {
+  int rc = check_shape(M, Kp, N, LB_G32);
+  if (rc < 0) return rc;
+  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lbd_gemm_w4a16_g32(const float *x, int M, int Kp, const uint8_t *qw, const float *scales, const uint8_t *zeros,
+                       int N, float *y, void *stream) {
+  lbk::GemmArgs a;
+  const int rc = g32_args(x, M, Kp, qw, scales, zeros, N, y, a);
+  return rc < 0 ? rc : run_g32(lbk::F_W4A16G32, a, static_cast<hipStream_t>(stream));
+}
+
+int lbd_gemm_w4a8_g32(const float *x, int M, int Kp, const uint8_t *qw, const float *scales, const uint8_t *zeros,
+                      int N, float *y, void *stream) {
+  lbk::GemmArgs a;
+  const int rc = g32_args(x, M, Kp, qw, scales, zeros, N, y, a);
+  return rc < 0 ? rc : run_g32(lbk::F_W4A8G32, a, static_cast<hipStream_t>(stream));
 }
 
 int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,

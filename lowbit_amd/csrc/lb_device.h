@@ -72,6 +72,15 @@ __device__ __forceinline__ int half_wave_sum(int v) {
   return v;
 }
 
+// Sum over each group of eight lanes; every lane of the group gets it (quad sums,
+// then the mirrored quad of the same half-row).
+__device__ __forceinline__ int eighth_wave_sum(int v) {
+  v += dpp_i<kDppQuad1032>(v, 0);
+  v += dpp_i<kDppQuad2301>(v, 0);
+  v += dpp_i<kDppRowHalfMirror>(v, 0);
+  return v;
+}
+
 // ---------------------------------------------------------------- buffer loads
 //
 // Raw buffer loads through a resource descriptor (base, byte count): offsets at

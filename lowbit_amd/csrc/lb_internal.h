@@ -8,7 +8,13 @@
 
 namespace lbk {
 
-enum Fmt { F_W4A16 = 0, F_MXFP4 = 1, F_W4A8 = 2, F_W4A8Q = 3 };
+enum Fmt { F_W4A16 = 0, F_MXFP4 = 1, F_W4A8 = 2, F_W4A8Q = 3, F_W4A16G32 = 4, F_W4A8G32 = 5 };
+
+// int4 with groups of 32 (F_W4A16G32, F_W4A8G32): the block layout of MXFP4 (byte j
+// of group g holds elements 32g + j and 32g + 16 + j) with an fp32 scale and
+// optional uint8 zero-point per group.
+__host__ __device__ constexpr bool fmt_g32(int f) { return f == F_W4A16G32 || f == F_W4A8G32; }
+__host__ __device__ constexpr int fmt_group(int f) { return fmt_g32(f) || f == F_MXFP4 ? 32 : 128; }
 
 // Operands of one GEMM; unused pointers are null. All pointers are device memory.
 struct GemmArgs {
@@ -65,10 +71,10 @@ hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N
 __host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
 hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
-// weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 g128 (mode 0 absmax,
-// 1 signed-max, 2 asym) or MXFP4
-hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, uint8_t *qw, float *scales, uint8_t *zeros,
-                                hipStream_t s);
+// weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 with groups of `group`
+// (128 or 32; mode 0 absmax, 1 signed-max, 2 asym) or MXFP4
+hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, int group, uint8_t *qw, float *scales,
+                                uint8_t *zeros, hipStream_t s);
 hipError_t launch_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0, hipStream_t s);
 hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
                                   uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s);
@@ -80,6 +86,8 @@ size_t gemv_lds_bytes(int fmt, int M, int Kp);
 bool gemv_eligible(int fmt, int M, int Kp);
 
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
+// the group-32 instantiations of the small-M kernels (lb_gemv_g32.hip)
+hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s);
 // Per-token int8 quantizer: xq, xs, asum as lb_quant_act_int8, or (tiled) xq and asum
 // in the MFMA path's tiled layout over ceil(M/16)*16 rows, padding rows zero.
 hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum, bool tiled,

@@ -28,6 +28,7 @@
 #include <algorithm>
 
 #include "lb_device.h"
+#include "lb_gemv.h"
 #include "lb_internal.h"
 
 namespace lbk {
@@ -123,520 +124,19 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(
 
 // ============================================================ small-M GEMV (VALU)
 //
-// Decode is a pure HBM stream that lasts a few microseconds; the kernel is built
-// around three facts:
-//   * every weight byte should be requested as early as possible;
-//   * the activation prologue (staging X, or quantizing it for W4A8) is the same
-//     for every workgroup, so it should run as few times as possible;
-//   * the VALU issue rate, not HBM, is the next limit, so tails and bounds must
-//     cost no instructions.
-// The grid is persistent: two 512-thread workgroups per CU. Each workgroup
-// stages (or quantizes) the activations once, and its 8 waves take an even
-// share of the weight rows (rows [gw*N/W, (gw+1)*N/W) for global wave gw of W).
-// A wave first loads its activation slice into registers, then issues all the
-// loads of its first R rows (16 bytes per lane per chunk, plus scales), and only
-// then writes the activations to LDS: loads retire in issue order (s_waitcnt
-// vmcnt), so the prologue waits for the activations alone while the weight
-// stream is in flight. Decode and FMAs run from registers as chunks land, then
-// one DPP wave reduction per (activation row, weight row) gives the output.
-// All global reads are buffer loads through per-row descriptors: chunks past a
-// row's end, rows past the wave's share and activations past Kp read as 0.
-//
-// Chunk ci of a row is bytes [16ci, 16ci+16) = 32 elements; lane l holds chunks
-// ci = l, l + 64, ... (NIT of them; the regime is limited to rows that fit):
-//   int4 : group g = ci / 4, bytes b = 16 (ci % 4): low nibbles are elements
-//          128g + b + [0,16), high nibbles 128g + 64 + b + [0,16)
-//   MXFP4: block ci: low nibbles 32ci + [0,16), high nibbles 32ci + 16 + [0,16)
-//
-// LDS plane layout of the activations: for fp32 X, eight planes of float4,
-// plane p = half * 4 + (position within the 16-element half) / 4, entry ci; for
-// int8 codes, two planes of 16 bytes (half 0 / 1). Planes hold nchp = nit * 64
-// entries (whole steps of 64 chunks), so padding lanes read zeros. Lane reads of
-// one plane are consecutive 16-byte words: no bank conflicts.
-
-constexpr int kGemvThreads = 512;
-constexpr int kGemvWaves = kGemvThreads / kWave;
-constexpr int kGemvMaxNit = 8;   // chunks per lane held in registers (rows up to 16384 elements)
-constexpr int kXRegs = 16;       // float4 of activations a thread may hold across the weight loads
-
-__device__ __forceinline__ void chunk_pos(int fmt, int e, int &ci, int &half, int &within) {
-  if (fmt == F_MXFP4) {
-    const int r = e & 31;
-    ci = e >> 5;
-    half = r >> 4;
-    within = r & 15;
-  } else {
-    const int r = e & 127;
-    ci = ((e >> 7) << 2) + ((r & 63) >> 4);
-    half = r >> 6;
-    within = r & 15;
-  }
-}
-
-static int gemv_nchp(int Kp) { return ((Kp / 32 + kWave - 1) / kWave) * kWave; }
+// The kernels live in lb_gemv.h (shared with the group-32 instantiations).
 
 // Activation planes, then (int8 formats) group sums and row scales.
 size_t gemv_lds_bytes(int fmt, int M, int Kp) {
   const size_t nchp = gemv_nchp(Kp);
-  if (fmt == F_W4A16 || fmt == F_MXFP4) return (size_t)M * nchp * 32 * sizeof(float);
-  return (size_t)M * nchp * 32 + (size_t)M * (nchp / 4) * sizeof(int32_t) + 16;
+  if (fmt == F_W4A16 || fmt == F_MXFP4 || fmt == F_W4A16G32) return (size_t)M * nchp * 32 * sizeof(float);
+  const size_t groups = fmt_g32(fmt) ? nchp : nchp / 4;  // padded group sums per row
+  return (size_t)M * nchp * 32 + (size_t)M * groups * sizeof(int32_t) + 16;
 }
 
 bool gemv_eligible(int fmt, int M, int Kp) {
   return M >= 1 && M <= kGemvMaxM && Kp <= kGemvMaxNit * kWave * 32 &&
          gemv_lds_bytes(fmt, M, Kp) <= kGemvLdsLimit;
-}
-
-// Weights of R rows x NIT chunks per lane, with their scales.
-template <int F, int R, int NIT>
-struct GemvRegs {
-  uint4 w[R][NIT];
-  float sc[R][NIT];
-  int zi[R][NIT];
-};
-
-// Rows rb .. rb+R-1; rows at or past `rend` get zero-length descriptors (read 0).
-template <int F, int R, int NIT>
-__device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT> &g, int rb, int rend, int lane,
-                                          int nch, int G) {
-  const uint32_t rowbytes = (uint32_t)(a.Kp >> 1);
-  const int zadd = a.zeros ? 0 : 8;  // symmetric weights: z = 8
-#pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int row = rb + r;
-    const bool ok = row < rend;
-    const size_t rr = ok ? (size_t)row : 0;
-    const Rsrc rw = make_rsrc(a.qw + rr * rowbytes, ok ? rowbytes : 0);
-    if constexpr (F == F_MXFP4) {
-      const Rsrc re = make_rsrc(a.e8m0 + rr * nch, ok ? (uint32_t)nch : 0);
-#pragma unroll
-      for (int it = 0; it < NIT; it++) {
-        const uint32_t ci = lane + kWave * it;
-        g.w[r][it] = ld_b128(rw, ci * 16);
-        g.sc[r][it] = e8m0_to_f32(ld_u8(re, ci));
-        g.zi[r][it] = 0;
-      }
-    } else {
-      const Rsrc rs = make_rsrc(a.scales + rr * G, ok ? (uint32_t)G * 4 : 0);
-      const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (ok && a.zeros) ? (uint32_t)G : 0);
-#pragma unroll
-      for (int it = 0; it < NIT; it++) {
-        const uint32_t ci = lane + kWave * it;
-        g.w[r][it] = ld_b128(rw, ci * 16);
-        g.sc[r][it] = ld_f32(rs, (ci >> 2) * 4);
-        g.zi[r][it] = (int)ld_u8(rz, ci >> 2) + zadd;
-      }
-    }
-  }
-}
-
-// acc[m][r] += this lane's share of row r (r < nr) against activation row m.
-// Chunks past the row end hold zero weights, zero scales and zero activations.
-template <int F, int MB, int R, int NIT>
-__device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float (&acc)[MB][R], int nr, int lane,
-                                             int nchp, int Gp, const float *xl, const uint8_t *ql,
-                                             const int32_t *asl) {
-#pragma unroll
-  for (int it = 0; it < NIT; it++) {
-    const int ci = lane + kWave * it;
-    if (it * kWave >= nchp) break;  // uniform: this row length needs fewer chunks
-    if constexpr (F == F_W4A16) {
-#pragma unroll
-      for (int m = 0; m < MB; m++) {
-        float4 xv[8];
-#pragma unroll
-        for (int p = 0; p < 8; p++)
-          xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-        // sum of the 32 activations in the same order as the products below, so
-        // that sum(q*x) - z*sum(x) is exactly 0 when every q == z and z is a power
-        // of two (z = 8: symmetric zero rows and padding)
-        float sl = 0.0f, sh = 0.0f;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-          sl += xv[p].x; sl += xv[p].y; sl += xv[p].z; sl += xv[p].w;
-          sh += xv[4 + p].x; sh += xv[4 + p].y; sh += xv[4 + p].z; sh += xv[4 + p].w;
-        }
-        const float xsum = sl + sh;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          if (r >= nr) break;
-          const uint32_t wd[4] = {g.w[r][it].x, g.w[r][it].y, g.w[r][it].z, g.w[r][it].w};
-          float pl = 0.0f, ph = 0.0f;
-#pragma unroll
-          for (int d = 0; d < 4; d++) {
-            const uint32_t lo = opaque(lo_nibbles(wd[d])), hi = opaque(hi_nibbles(wd[d]));
-            pl = __builtin_fmaf((float)(lo & 0xFF), xv[d].x, pl);
-            pl = __builtin_fmaf((float)((lo >> 8) & 0xFF), xv[d].y, pl);
-            pl = __builtin_fmaf((float)((lo >> 16) & 0xFF), xv[d].z, pl);
-            pl = __builtin_fmaf((float)(lo >> 24), xv[d].w, pl);
-            ph = __builtin_fmaf((float)(hi & 0xFF), xv[4 + d].x, ph);
-            ph = __builtin_fmaf((float)((hi >> 8) & 0xFF), xv[4 + d].y, ph);
-            ph = __builtin_fmaf((float)((hi >> 16) & 0xFF), xv[4 + d].z, ph);
-            ph = __builtin_fmaf((float)(hi >> 24), xv[4 + d].w, ph);
-          }
-          const float part = __builtin_fmaf(-(float)g.zi[r][it], xsum, pl + ph);
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], part, acc[m][r]);
-        }
-      }
-    } else if constexpr (F == F_MXFP4) {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        if (r >= nr) break;
-        // E2M1 pairs (low nibble, high nibble) of each byte, exact in fp32
-        float wl[16], wh[16];
-        const uint32_t wd[4] = {g.w[r][it].x, g.w[r][it].y, g.w[r][it].z, g.w[r][it].w};
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const v2f p0 = e2m1_pair<0>(wd[d], 1.0f), p1 = e2m1_pair<1>(wd[d], 1.0f);
-          const v2f p2 = e2m1_pair<2>(wd[d], 1.0f), p3 = e2m1_pair<3>(wd[d], 1.0f);
-          wl[4 * d + 0] = p0.x; wh[4 * d + 0] = p0.y;
-          wl[4 * d + 1] = p1.x; wh[4 * d + 1] = p1.y;
-          wl[4 * d + 2] = p2.x; wh[4 * d + 2] = p2.y;
-          wl[4 * d + 3] = p3.x; wh[4 * d + 3] = p3.y;
-        }
-#pragma unroll
-        for (int m = 0; m < MB; m++) {
-          float4 xv[8];
-#pragma unroll
-          for (int p = 0; p < 8; p++)
-            xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-          float pl = 0.0f, ph = 0.0f;
-#pragma unroll
-          for (int d = 0; d < 4; d++) {
-            pl = __builtin_fmaf(wl[4 * d + 0], xv[d].x, pl);
-            pl = __builtin_fmaf(wl[4 * d + 1], xv[d].y, pl);
-            pl = __builtin_fmaf(wl[4 * d + 2], xv[d].z, pl);
-            pl = __builtin_fmaf(wl[4 * d + 3], xv[d].w, pl);
-            ph = __builtin_fmaf(wh[4 * d + 0], xv[4 + d].x, ph);
-            ph = __builtin_fmaf(wh[4 * d + 1], xv[4 + d].y, ph);
-            ph = __builtin_fmaf(wh[4 * d + 2], xv[4 + d].z, ph);
-            ph = __builtin_fmaf(wh[4 * d + 3], xv[4 + d].w, ph);
-          }
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], pl + ph, acc[m][r]);
-        }
-      }
-    } else {
-      // W4A8: int8 dot4 on unsigned codes (0..15 are non-negative int8) and the
-      // int8 activations; the group's zero-point term z * sum(a) is taken once,
-      // by the lane holding the group's first 16 bytes. Each lane's integer is
-      // exact and below 2^24, so its conversion to fp32 is exact.
-      const int gi = ci >> 2;
-      const bool first = (ci & 3) == 0;
-#pragma unroll
-      for (int m = 0; m < MB; m++) {
-        const uint4 al = *reinterpret_cast<const uint4 *>(ql + ((size_t)(m * 2 + 0) * nchp + ci) * 16);
-        const uint4 ah = *reinterpret_cast<const uint4 *>(ql + ((size_t)(m * 2 + 1) * nchp + ci) * 16);
-        const int as = first ? asl[m * Gp + gi] : 0;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          if (r >= nr) break;
-          const uint4 w = g.w[r][it];
-          int d = 0;
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.x), (int)al.x, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.x), (int)ah.x, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.y), (int)al.y, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.y), (int)ah.y, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.z), (int)al.z, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.z), (int)ah.z, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.w), (int)al.w, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.w), (int)ah.w, d, false);
-          d -= g.zi[r][it] * as;
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], (float)d, acc[m][r]);
-        }
-      }
-    }
-  }
-}
-
-// PRO selects a fused prologue on the (single, register-held) activation row:
-// 0 none, 1 RMSNorm (x * (1 / sqrt(mean(x^2) + eps)) * norm_w, the mean over Kp),
-// 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
-// adds `bias` and `res` when given and max-combines argmax keys into `amax_key`.
-template <int F, int MB, int R, int NIT, int PRO>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
-  extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ float red[2][kGemvWaves];
-  constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
-  constexpr int T = kGemvThreads;
-  const int Kp = a.Kp, N = a.N;
-  const int nch = Kp >> 5;                        // 16-byte chunks per weight row
-  const int nit = (nch + kWave - 1) / kWave;      // <= NIT
-  const int nchp = nit * kWave;                   // plane entries (padded)
-  const int G = Kp / kGroup, Gp = nchp / 4;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int gw = blockIdx.x * kGemvWaves + wave, W = gridDim.x * kGemvWaves;
-  // wave gw takes rows [r0, r1): N / W each, one more for the first N % W waves
-  const int rbase = (int)((unsigned)N / (unsigned)W), rrem = N - rbase * W;
-  const int r0 = gw * rbase + min(gw, rrem), r1 = r0 + rbase + (gw < rrem ? 1 : 0);
-
-  float *xl = reinterpret_cast<float *>(lds);                           // fp32 planes [MB][8][nchp][4]
-  uint8_t *ql = lds;                                                      // int8 planes [MB][2][nchp][16]
-  int32_t *asl = reinterpret_cast<int32_t *>(lds + (size_t)MB * nchp * 32);  // [MB][Gp]
-  float *xsl = reinterpret_cast<float *>(asl + (size_t)MB * Gp);         // [MB]
-
-  // ---- 1. activations into registers, issued first: NIT float4 per thread per
-  //         row (slots past Kp read 0 through the row's buffer descriptor)
-  constexpr int S = NIT;
-  constexpr bool kXReg = (F != F_W4A8Q) && MB * S <= kXRegs;
-  static_assert(PRO == 0 || (MB == 1 && kXReg), "prologues take one register-held activation row");
-  float4 xr[kXReg ? MB * S : 1];
-  float4 xe[PRO ? S : 1];  // RMSNorm weights, or the up half of a SwiGLU row
-  if constexpr (kXReg) {
-#pragma unroll
-    for (int m = 0; m < MB; m++) {
-      const Rsrc rx = make_rsrc(a.x + (size_t)m * Kp, (uint32_t)Kp * 4);
-#pragma unroll
-      for (int i = 0; i < S; i++) xr[m * S + i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
-    }
-    if constexpr (PRO != 0) {
-      const Rsrc re = make_rsrc(PRO == 1 ? a.norm_w : a.x + Kp, (uint32_t)Kp * 4);
-#pragma unroll
-      for (int i = 0; i < S; i++) xe[i] = ld_f4(re, (threadIdx.x + i * T) * 16);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight stream
-
-  // ---- 2. the weight stream of this wave's first R rows, then their epilogue
-  //         operands (bias, residual), so that the epilogue waits for no load
-  GemvRegs<F, R, NIT> g;
-  float bv[R], rv[MB][R];
-  auto epi_load = [&](int rb) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int n = rb + r < N ? rb + r : N - 1;  // rows past the share are never stored
-      bv[r] = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-      for (int m = 0; m < MB; m++) rv[m][r] = a.res ? a.res[(size_t)m * N + n] : 0.0f;
-    }
-  };
-  gemv_load<F, R, NIT>(a, g, r0, r1, lane, nch, G);
-  epi_load(r0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- 3. fused prologue, then stage the activations into LDS while the weights
-  //         are in flight (slot i covers elements [2048 i, 2048 i + 2048); slots
-  //         past the padded plane length are skipped on a block-uniform branch;
-  //         elements past Kp are 0 and stay 0 under both prologues)
-  if constexpr (PRO == 1) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < S; i++) {
-      ss = __builtin_fmaf(xr[i].x, xr[i].x, ss);
-      ss = __builtin_fmaf(xr[i].y, xr[i].y, ss);
-      ss = __builtin_fmaf(xr[i].z, xr[i].z, ss);
-      ss = __builtin_fmaf(xr[i].w, xr[i].w, ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) red[0][wave] = ss;
-    __syncthreads();
-    float tot = red[0][0];
-#pragma unroll
-    for (int w = 1; w < kGemvWaves; w++) tot += red[0][w];
-    __syncthreads();  // red is reused by the quantizer below
-    const float rn = 1.0f / sqrtf(tot / (float)Kp + a.norm_eps);
-#pragma unroll
-    for (int i = 0; i < S; i++) {
-      xr[i].x = xr[i].x * rn * xe[i].x;
-      xr[i].y = xr[i].y * rn * xe[i].y;
-      xr[i].z = xr[i].z * rn * xe[i].z;
-      xr[i].w = xr[i].w * rn * xe[i].w;
-    }
-  } else if constexpr (PRO == 2) {
-#pragma unroll
-    for (int i = 0; i < S; i++) {
-      xr[i].x = xr[i].x / (1.0f + expf(-xr[i].x)) * xe[i].x;
-      xr[i].y = xr[i].y / (1.0f + expf(-xr[i].y)) * xe[i].y;
-      xr[i].z = xr[i].z / (1.0f + expf(-xr[i].z)) * xe[i].z;
-      xr[i].w = xr[i].w / (1.0f + expf(-xr[i].w)) * xe[i].w;
-    }
-  }
-  if constexpr (!kInt8) {
-    if constexpr (kXReg) {
-#pragma unroll
-      for (int j = 0; j < MB * S; j++) {
-        const int m = j / S, i = j % S;
-        if (i >= nit) continue;
-        int ci, half, within;
-        chunk_pos(F, threadIdx.x * 4 + i * T * 4, ci, half, within);
-        *reinterpret_cast<float4 *>(xl + ((size_t)(m * 8 + half * 4 + (within >> 2)) * nchp + ci) * 4) = xr[j];
-      }
-    } else {
-      for (int m = 0; m < MB; m++) {
-        const Rsrc rx = make_rsrc(a.x + (size_t)m * Kp, (uint32_t)Kp * 4);
-        for (int e = threadIdx.x * 4; e < nchp * 32; e += T * 4) {
-          int ci, half, within;
-          chunk_pos(F, e, ci, half, within);
-          *reinterpret_cast<float4 *>(xl + ((size_t)(m * 8 + half * 4 + (within >> 2)) * nchp + ci) * 4) =
-              ld_f4(rx, e * 4);
-        }
-      }
-    }
-  } else if constexpr (F == F_W4A8) {
-    // fused per-token quantizer: bit-identical to quant_rows_kernel
-    for (int m = 0; m < MB; m++) {
-      const Rsrc rx = make_rsrc(a.x + (size_t)m * Kp, (uint32_t)Kp * 4);
-      float amax = 0.0f;  // padding reads +0 and cannot raise it
-      if constexpr (kXReg) {
-#pragma unroll
-        for (int i = 0; i < S; i++) {
-          const float4 v = xr[m * S + i];
-          amax = fmaxf(fmaxf(amax, fabsf(v.x)), fabsf(v.y));
-          amax = fmaxf(fmaxf(amax, fabsf(v.z)), fabsf(v.w));
-        }
-      } else {
-        for (int e = threadIdx.x * 4; e < Kp; e += T * 4) {
-          const float4 v = ld_f4(rx, e * 4);
-          amax = fmaxf(fmaxf(amax, fabsf(v.x)), fabsf(v.y));
-          amax = fmaxf(fmaxf(amax, fabsf(v.z)), fabsf(v.w));
-        }
-      }
-      // red[m & 1]: row m + 1 writes the other half, and row m + 2 comes after
-      // row m + 1's barrier, by which time every wave has read row m's partials
-      amax = wave_max(amax);
-      if (lane == 0) red[m & 1][wave] = amax;
-      __syncthreads();
-      float rmax = red[m & 1][0];
-#pragma unroll
-      for (int w = 1; w < kGemvWaves; w++) rmax = fmaxf(rmax, red[m & 1][w]);
-      const float sc = row_scale(rmax);
-      const float inv = 1.0f / sc;
-      if (threadIdx.x == 0) xsl[m] = sc;
-      // thread t quantizes 4 elements per slot; a group of 128 is one half-wave
-      for (int i = 0; i < nit; i++) {
-        const int e = threadIdx.x * 4 + i * T * 4;
-        float4 v;
-        if constexpr (kXReg) {
-          v = xr[m * S];
-#pragma unroll
-          for (int k = 1; k < S; k++)
-            if (k == i) v = xr[m * S + k];
-        } else {
-          v = ld_f4(rx, e * 4);
-        }
-        int ci, half, within;
-        chunk_pos(F, e, ci, half, within);
-        const uint32_t qv = quant4_fast(v, sc, inv);
-        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nchp + ci) * 16 + within) = qv;
-        const int gs = half_wave_sum(sum_i8x4(qv));
-        if ((threadIdx.x & 31) == 31) asl[m * Gp + (e >> 7)] = gs;
-      }
-    }
-  } else {
-    for (int m = 0; m < MB; m++) {
-      const Rsrc rq = make_rsrc(a.xq + (size_t)m * Kp, (uint32_t)Kp);
-      for (int e = threadIdx.x * 4; e < nchp * 32; e += T * 4) {
-        int ci, half, within;
-        chunk_pos(F, e, ci, half, within);
-        *reinterpret_cast<uint32_t *>(ql + ((size_t)(m * 2 + half) * nchp + ci) * 16 + within) = ld_u32(rq, e);
-      }
-      for (int gg = threadIdx.x; gg < Gp; gg += T) asl[m * Gp + gg] = gg < G ? a.asum[(size_t)m * G + gg] : 0;
-      if (threadIdx.x == 0) xsl[m] = a.xs[m];
-    }
-  }
-  __syncthreads();
-
-  // ---- 4. decode + accumulate R rows at a time; later batches load as the
-  //         previous one finishes
-  unsigned long long best = 0;  // argmax key of this wave's outputs
-  for (int rb = r0; rb < r1; rb += R) {
-    if (rb != r0) {
-      gemv_load<F, R, NIT>(a, g, rb, r1, lane, nch, G);
-      epi_load(rb);
-    }
-    const int nr = min(R, r1 - rb);
-    float acc[MB][R];
-#pragma unroll
-    for (int m = 0; m < MB; m++)
-#pragma unroll
-      for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
-    gemv_compute<F, MB, R, NIT>(g, acc, nr, lane, nchp, Gp, xl, ql, asl);
-    // ---- 5. one wave reduction per output (every lane gets it), the epilogue,
-    //         and lane m*R + r stores it
-#pragma unroll
-    for (int m = 0; m < MB; m++)
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        if (r >= nr) break;
-        float t = wave_sum(acc[m][r]);
-        const int n = rb + r;
-        const size_t o = (size_t)m * N + n;
-        {
-          // y is rounded before the bias and the residual are added, as separate
-          // float32 adds after the GEMM would round it (no fused multiply-add)
-#pragma clang fp contract(off)
-          if constexpr (kInt8) t *= xsl[m];
-          if (a.bias) t += bv[r];
-          if (a.res) t = rv[m][r] + t;
-        }
-        if (lane == m * R + r) a.y[o] = t;
-        if (a.amax_key) {
-          const unsigned long long k = argmax_key(t, n);
-          best = k > best ? k : best;
-        }
-      }
-  }
-  // spread over the slots so that no address takes more than a few atomics
-  if (a.amax_key && lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
-}
-
-// Register-held chunks per lane (NIT) from the row length; rows per wave (R)
-// from the share of rows each wave gets under the persistent grid.
-template <int F, int MB, int NIT, int PRO>
-static hipError_t launch_gemv_nit(const GemmArgs &a, int grid, int rpw, size_t lds, hipStream_t s) {
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kGemvThreads), lds, s, a);
-    return hipGetLastError();
-  };
-  // rows held at once: R * NIT chunks of weights must stay in registers next to the
-  // activations (larger shares are processed R rows at a time)
-  constexpr int RMAX = MB == 1 ? (NIT >= 8 ? 1 : NIT >= 4 ? 2 : 4) : MB == 2 ? (NIT >= 4 ? 1 : 2) : 1;
-  if constexpr (RMAX == 1) {
-    return go(gemv_kernel<F, MB, 1, NIT, PRO>);
-  } else if constexpr (RMAX == 2) {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
-    return go(gemv_kernel<F, MB, 2, NIT, PRO>);
-  } else {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
-    if (rpw <= 2) return go(gemv_kernel<F, MB, 2, NIT, PRO>);
-    if (rpw <= 3) return go(gemv_kernel<F, MB, 3, NIT, PRO>);
-    return go(gemv_kernel<F, MB, 4, NIT, PRO>);
-  }
-}
-
-template <int F, int MB, int PRO>
-static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
-  const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
-  const int cus = num_cus > 0 ? num_cus : 256;
-  // persistent grid: two workgroups per CU, fewer when there are few rows
-  int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
-  grid = grid < 2 * cus ? grid : 2 * cus;
-  const int waves = grid * kGemvWaves;
-  const int rpw = (a.N + waves - 1) / waves;
-  if (nit <= 1) return launch_gemv_nit<F, MB, 1, PRO>(a, grid, rpw, lds, s);
-  if (nit <= 2) return launch_gemv_nit<F, MB, 2, PRO>(a, grid, rpw, lds, s);
-  if (nit <= 4) return launch_gemv_nit<F, MB, 4, PRO>(a, grid, rpw, lds, s);
-  // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
-  if constexpr ((F == F_W4A16 || F == F_MXFP4) && MB >= 2) return hipErrorInvalidValue;
-  else return launch_gemv_nit<F, MB, 8, PRO>(a, grid, rpw, lds, s);
-}
-
-template <int F>
-static hipError_t launch_gemv_f(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
-  const int pro = gemv_prologue(a);
-  if (pro != 0) {
-    if (a.M != 1 || (a.norm_w && a.swiglu)) return hipErrorInvalidValue;
-    if constexpr (F == F_W4A8Q) return hipErrorInvalidValue;  // the prologues act on fp32 rows
-    else if (pro == 1) return launch_gemv_mb<F, 1, 1>(a, num_cus, lds, s);
-    else return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s);
-  }
-  switch (a.M) {
-    case 1: return launch_gemv_mb<F, 1, 0>(a, num_cus, lds, s);
-    case 2: return launch_gemv_mb<F, 2, 0>(a, num_cus, lds, s);
-    case 3: return launch_gemv_mb<F, 3, 0>(a, num_cus, lds, s);
-    case 4: return launch_gemv_mb<F, 4, 0>(a, num_cus, lds, s);
-  }
-  return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
@@ -647,6 +147,8 @@ hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
     case F_MXFP4: return launch_gemv_f<F_MXFP4>(a, num_cus, lds, s);
     case F_W4A8: return launch_gemv_f<F_W4A8>(a, num_cus, lds, s);
     case F_W4A8Q: return launch_gemv_f<F_W4A8Q>(a, num_cus, lds, s);
+    case F_W4A16G32:
+    case F_W4A8G32: return launch_gemv_g32(fmt, a, num_cus, lds, s);
   }
   return hipErrorInvalidValue;
 }

@@ -1,5 +1,5 @@
 // Weight quantizers on the device: fp32 [N, K] row-major in HBM -> the public packed
-// int4 g128 and MXFP4 formats, byte for byte what the host packers produce
+// int4 (groups of 128, or 32) and MXFP4 formats, byte for byte what the host packers produce
 // (src/lowbit/formats.py:90-142 and :182-212). A model's weights are uploaded once as
 // fp32 and packed where they will be read, instead of on the host.
 //
@@ -23,29 +23,34 @@ constexpr int kQT = 256;  // 4 waves per workgroup, one group (or 4 MX blocks) p
 __device__ __forceinline__ float xor_max(float v, int w) { return fmaxf(v, __shfl_xor(v, w)); }
 __device__ __forceinline__ float xor_min(float v, int w) { return fminf(v, __shfl_xor(v, w)); }
 
-// int4 g128: one wave per (row, group); lane l holds elements l and l + 64 of the
-// group, which are exactly the two nibbles of packed byte l.
+// int4, groups of GS = 128 or 32 elements: L = GS / 2 lanes per group, 64 / L groups
+// per wave; lane j of a group holds elements j and j + GS / 2, exactly the two
+// nibbles of packed byte j of the group (the "j / j+half" layout).
 //   absmax:     s = max|w| / 7,          q = clip(rint(w / s), -8, 7) + 8
 //   signed-max: s = m / -8 (m = the first element of largest magnitude, sign kept)
 //   asym:       s = (max(w, 0) - min(w, 0)) / 15, z = clip(rint(-min / s), 0, 15),
 //               q = clip(rint(w / s) + z, 0, 15)
 // A scale that is not > 0 (absmax, asym) or is 0 (signed-max) becomes 1.
-template <int MODE>  // 0 absmax, 1 signed-max, 2 asym
+template <int MODE, int GS>  // MODE 0 absmax, 1 signed-max, 2 asym
 __global__ __launch_bounds__(kQT) void quantize_int4_kernel(const float *__restrict__ w, int N, int K, int G,
                                                              uint8_t *__restrict__ qw, float *__restrict__ scales,
                                                              uint8_t *__restrict__ zeros) {
+  constexpr int L = GS / 2, GPW = kWave / L;
   const int lane = threadIdx.x & (kWave - 1);
+  const int GQ = (G + GPW - 1) / GPW;  // wave items per row
   const long long item = (long long)blockIdx.x * (kQT / kWave) + threadIdx.x / kWave;
-  if (item >= (long long)N * G) return;  // whole waves only: no barrier below
-  const int row = (int)(item / G), g = (int)(item % G);
-  const int k0 = g * 128 + lane, k1 = k0 + 64;
+  if (item >= (long long)N * GQ) return;  // whole waves only: no barrier below
+  const int row = (int)(item / GQ), g = (int)(item % GQ) * GPW + lane / L, j = lane % L;
+  const bool live = g < G;  // the last item of a row may hold groups past the row
+  const int k0 = g * GS + j, k1 = k0 + L;
   const float *wr = w + (size_t)row * K;
-  const bool in0 = k0 < K, in1 = k1 < K;
+  const bool in0 = live && k0 < K, in1 = live && k1 < K;
   const float x0 = in0 ? wr[k0] : 0.0f, x1 = in1 ? wr[k1] : 0.0f;
   float s, zf = 8.0f, lo_q = -8.0f, hi_q = 7.0f;
+  // xor offsets below L keep every reduction inside one group's lanes
   if (MODE == 2) {
     float hi = fmaxf(x0, x1), lo = fminf(x0, x1);
-    for (int o = 32; o > 0; o >>= 1) hi = xor_max(hi, o), lo = xor_min(lo, o);
+    for (int o = L / 2; o > 0; o >>= 1) hi = xor_max(hi, o), lo = xor_min(lo, o);
     hi = fmaxf(hi, 0.0f);
     lo = fminf(lo, 0.0f);
     s = (hi - lo) / 15.0f;
@@ -58,7 +63,7 @@ __global__ __launch_bounds__(kQT) void quantize_int4_kernel(const float *__restr
     float a = fabsf(x0), m = x0;
     int ix = k0;
     if (fabsf(x1) > a) a = fabsf(x1), m = x1, ix = k1;
-    for (int o = 32; o > 0; o >>= 1) {
+    for (int o = L / 2; o > 0; o >>= 1) {
       const float oa = __shfl_xor(a, o), om = __shfl_xor(m, o);
       const int oi = __shfl_xor(ix, o);
       if (oa > a || (oa == a && oi < ix)) a = oa, m = om, ix = oi;
@@ -67,7 +72,7 @@ __global__ __launch_bounds__(kQT) void quantize_int4_kernel(const float *__restr
     s = s != 0.0f ? s : 1.0f;
   } else {
     float a = fmaxf(fabsf(x0), fabsf(x1));
-    for (int o = 32; o > 0; o >>= 1) a = xor_max(a, o);
+    for (int o = L / 2; o > 0; o >>= 1) a = xor_max(a, o);
     s = a / 7.0f;
     s = s > 0.0f ? s : 1.0f;
   }
@@ -77,8 +82,9 @@ __global__ __launch_bounds__(kQT) void quantize_int4_kernel(const float *__restr
   const float c1 = fminf(fmaxf(__builtin_rintf(x1 / s) + add, lo_q), hi_q) + off;
   const uint32_t pad = (uint32_t)zf;  // padded elements decode to 0
   const uint32_t q0 = in0 ? (uint32_t)c0 : pad, q1 = in1 ? (uint32_t)c1 : pad;
-  qw[(size_t)row * (G * 64) + g * 64 + lane] = (uint8_t)(q0 | (q1 << 4));
-  if (lane == 0) {
+  if (!live) return;
+  qw[(size_t)row * ((size_t)G * L) + (size_t)g * L + j] = (uint8_t)(q0 | (q1 << 4));
+  if (j == 0) {
     scales[(size_t)row * G + g] = s;
     if (MODE == 2) zeros[(size_t)row * G + g] = (uint8_t)pad;
   }
@@ -133,16 +139,27 @@ __global__ __launch_bounds__(kQT) void quantize_mxfp4_kernel(const float *__rest
 
 static unsigned waves_grid(long long items) { return (unsigned)((items + kQT / kWave - 1) / (kQT / kWave)); }
 
-hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, uint8_t *qw, float *scales, uint8_t *zeros,
-                                hipStream_t s) {
-  const int G = (K + 127) / 128;
-  const dim3 grid(waves_grid((long long)N * G)), block(kQT);
+template <int GS>
+static void launch_quantize_int4_g(const float *w, int N, int K, int mode, uint8_t *qw, float *scales, uint8_t *zeros,
+                                   hipStream_t s) {
+  const int G = (K + GS - 1) / GS, GPW = kWave / (GS / 2);
+  const dim3 grid(waves_grid((long long)N * ((G + GPW - 1) / GPW))), block(kQT);
   if (mode == 2)
-    hipLaunchKernelGGL(quantize_int4_kernel<2>, grid, block, 0, s, w, N, K, G, qw, scales, zeros);
+    hipLaunchKernelGGL((quantize_int4_kernel<2, GS>), grid, block, 0, s, w, N, K, G, qw, scales, zeros);
   else if (mode == 1)
-    hipLaunchKernelGGL(quantize_int4_kernel<1>, grid, block, 0, s, w, N, K, G, qw, scales, zeros);
+    hipLaunchKernelGGL((quantize_int4_kernel<1, GS>), grid, block, 0, s, w, N, K, G, qw, scales, zeros);
   else
-    hipLaunchKernelGGL(quantize_int4_kernel<0>, grid, block, 0, s, w, N, K, G, qw, scales, zeros);
+    hipLaunchKernelGGL((quantize_int4_kernel<0, GS>), grid, block, 0, s, w, N, K, G, qw, scales, zeros);
+}
+
+hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, int group, uint8_t *qw, float *scales,
+                                uint8_t *zeros, hipStream_t s) {
+  if (group == 128)
+    launch_quantize_int4_g<128>(w, N, K, mode, qw, scales, zeros, s);
+  else if (group == 32)
+    launch_quantize_int4_g<32>(w, N, K, mode, qw, scales, zeros, s);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

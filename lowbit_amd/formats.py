@@ -13,6 +13,9 @@ Layouts (row n of W occupies Kp/2 contiguous bytes):
                    element 128g+j in its low nibble and element 128g+64+j in
                    its high nibble. value = (q - z) * s, q in 0..15, s fp32,
                    z uint8 (8 when ``zeros is None``).
+  int4, group 32   (an extension: the reference ships group 128 only) the same
+                   "j / j+half" rule per group of 32: group g is bytes
+                   [16g, 16g+16), byte j holds 32g+j and 32g+16+j.
   MXFP4, block 32  block b is bytes [16b, 16b+16); byte j holds element 32b+j
                    (low nibble) and 32b+16+j (high nibble). Codes are OCP E2M1
                    (sign | 2-bit exponent | 1-bit mantissa), value =
@@ -29,6 +32,7 @@ from dataclasses import dataclass
 import numpy as np
 
 GROUP = 128   # int4 group size (elements)
+GROUPS = (128, 32)  # supported int4 group sizes
 MXBLOCK = 32  # MXFP4 block size (elements)
 
 # OCP MX E2M1: code -> value. Bit 3 is the sign, bits 2..1 the exponent, bit 0
@@ -72,15 +76,16 @@ def unpack_nibbles(packed: np.ndarray, block: int) -> np.ndarray:
 
 @dataclass
 class Int4Weights:
-    """int4 weights, group 128, fp32 scale per group, optional uint8 zero-point.
+    """int4 weights, group 128 (or 32), fp32 scale per group, optional uint8 zero-point.
 
-    value[n, k] = (q[n, k] - z[n, k // 128]) * s[n, k // 128], z = 8 when symmetric
-    (src/lowbit/formats.py:56-87).
+    value[n, k] = (q[n, k] - z[n, k // group]) * s[n, k // group], z = 8 when
+    symmetric (src/lowbit/formats.py:56-87; `group` = 32 is this package's extension).
     """
     qw: np.ndarray            # uint8 [N, Kp/2] packed codes
     scales: np.ndarray        # float32 [N, G]
     zeros: np.ndarray | None  # uint8 [N, G], or None (symmetric, z = 8)
     k: int                    # logical K (before padding)
+    group: int = GROUP        # elements per group: 128 (the reference's) or 32
 
     @property
     def n(self) -> int:
@@ -97,12 +102,12 @@ class Int4Weights:
         return self.qw.nbytes + self.scales.nbytes + extra
 
     def codes(self) -> np.ndarray:
-        return unpack_nibbles(self.qw, GROUP)
+        return unpack_nibbles(self.qw, self.group)
 
     def dequantize(self) -> np.ndarray:
         """Dense float32 [N, K] (for baselines and checks only; the GEMMs never do this)."""
-        g = self.kp // GROUP
-        q = self.codes().astype(np.float32).reshape(self.n, g, GROUP)
+        g = self.kp // self.group
+        q = self.codes().astype(np.float32).reshape(self.n, g, self.group)
         if self.zeros is None:
             z = np.float32(8.0)
         else:
@@ -111,8 +116,9 @@ class Int4Weights:
         return dense.reshape(self.n, self.kp)[:, : self.k]
 
 
-def quantize_int4(w: np.ndarray, asym: bool = False, scale: str = "absmax") -> Int4Weights:
-    """Round-to-nearest int4 with group size 128 (src/lowbit/formats.py:90-142).
+def quantize_int4(w: np.ndarray, asym: bool = False, scale: str = "absmax", group: int = GROUP) -> Int4Weights:
+    """Round-to-nearest int4 with group size 128 (src/lowbit/formats.py:90-142), or 32
+    (`group=32`: the same rules per group of 32, packed "j / j+half" per group).
 
     absmax (symmetric):  s = absmax / 7,               q = clip(rint(w/s), -8, 7) + 8
     signed-max:          s = m / -8 (m = the element of largest magnitude, sign kept);
@@ -125,14 +131,16 @@ def quantize_int4(w: np.ndarray, asym: bool = False, scale: str = "absmax") -> I
         raise ValueError(f"scale must be 'absmax' or 'signed-max', not {scale!r}")
     if asym and scale != "absmax":
         raise ValueError("scale='signed-max' is a symmetric rule (asym=False)")
+    if group not in GROUPS:
+        raise ValueError(f"group must be one of {GROUPS}, not {group!r}")
     w = np.asarray(w, dtype=np.float32)
     n, k = w.shape
-    kp = pad_to(k, GROUP)
-    ng = kp // GROUP
+    kp = pad_to(k, group)
+    ng = kp // group
     padded = np.zeros((n, kp), np.float32)
     padded[:, :k] = w
-    grp = padded.reshape(n, ng, GROUP)
-    real = (np.arange(kp) < k).reshape(1, ng, GROUP)
+    grp = padded.reshape(n, ng, group)
+    real = (np.arange(kp) < k).reshape(1, ng, group)
     one = np.float32(1.0)
     if asym:
         # Padding is +0 and the range is clamped to include 0 anyway, so the zero
@@ -159,7 +167,7 @@ def quantize_int4(w: np.ndarray, asym: bool = False, scale: str = "absmax") -> I
         q = np.where(real, q, 8)
         zeros = None
     codes = q.astype(np.uint8).reshape(n, kp)
-    return Int4Weights(pack_nibbles(codes, GROUP), s.astype(np.float32), zeros, k)
+    return Int4Weights(pack_nibbles(codes, group), s.astype(np.float32), zeros, k, group)
 
 
 # ------------------------------------------------------------------ MXFP4

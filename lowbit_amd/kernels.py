@@ -24,7 +24,7 @@ from functools import lru_cache
 import numpy as np
 
 from ._build import lib_path
-from .formats import GROUP, MXBLOCK, Int4Weights, Int8Acts, MXFP4Weights, pad_acts, pad_to
+from .formats import GROUP, GROUPS, MXBLOCK, Int4Weights, Int8Acts, MXFP4Weights, pad_acts, pad_to
 
 ISA_GFX950 = 16
 ISA_GFX950_MFMA = 17
@@ -135,6 +135,9 @@ SIGNATURES = {
     "lbd_gemv_w4a8_fused": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
     "lbd_argmax_finalize": ([_vp, _vp, _vp, _int, _vp, _int, _vp], _int),
     "lbd_attention_decode": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _vp], _int),
+    "lbd_gemm_w4a16_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
+    "lbd_gemm_w4a8_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
+    "lbd_quantize_int4_g32": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),
 }
 
 
@@ -311,10 +314,13 @@ class DeviceInt4Weights:
     kp: int
     k: int
     nbytes: int
+    group: int = GROUP
     t16: tuple | None = None
 
     def tiles(self) -> tuple:
         """(qwt, st, zt or None) in the t16 layout, repacked on first use."""
+        if self.group != GROUP:
+            raise ValueError("the t16 matrix-core layout holds groups of 128 only")
         if self.t16 is None:
             L = lib()
             bq, bs, bz = _sz(0), _sz(0), _sz(0)
@@ -363,7 +369,7 @@ def to_device(w):
     if isinstance(w, Int4Weights):
         return DeviceInt4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.scales),
                                  None if w.zeros is None else DeviceBuffer.from_array(w.zeros),
-                                 w.n, w.kp, w.k, w.nbytes)
+                                 w.n, w.kp, w.k, w.nbytes, w.group)
     if isinstance(w, MXFP4Weights):
         return DeviceMXFP4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.e8m0),
                                   w.n, w.kp, w.k, w.nbytes)
@@ -388,26 +394,30 @@ def _device_fp32(w, shape):
 
 
 def quantize_int4_device(w, asym: bool = False, scale: str = "absmax", shape=None,
-                         stream=None) -> "DeviceInt4Weights":
-    """quantize_int4 run on the device (lbd_quantize_int4): the same packed bytes,
-    scales and zero points as the host packer (src/lowbit/formats.py:90-142) for
-    finite weights, left in HBM as a handle the GEMMs accept. `w` is a host array
-    [N, K] (uploaded as fp32) or a DeviceBuffer holding fp32 [N, K] with shape=(N, K)."""
+                         stream=None, group: int = GROUP) -> "DeviceInt4Weights":
+    """quantize_int4 run on the device (lbd_quantize_int4, or lbd_quantize_int4_g32 for
+    group=32): the same packed bytes, scales and zero points as the host packer
+    (src/lowbit/formats.py:90-142) for finite weights, left in HBM as a handle the
+    GEMMs accept. `w` is a host array [N, K] (uploaded as fp32) or a DeviceBuffer
+    holding fp32 [N, K] with shape=(N, K)."""
     if scale not in ("absmax", "signed-max"):
         raise ValueError(f"scale must be 'absmax' or 'signed-max', not {scale!r}")
     if asym and scale != "absmax":
         raise ValueError("scale='signed-max' is a symmetric rule (asym=False)")
+    if group not in GROUPS:
+        raise ValueError(f"group must be one of {GROUPS}, not {group!r}")
     src, n, k = _device_fp32(w, shape)
-    kp = pad_to(k, GROUP)
-    g = kp // GROUP
+    kp = pad_to(k, group)
+    g = kp // group
     qw, sc = DeviceBuffer(n * kp // 2), DeviceBuffer(n * g * 4)
     z = DeviceBuffer(n * g) if asym else None
-    _check(lib().lbd_quantize_int4(src.ptr, n, k, int(asym), int(scale == "signed-max"), qw.ptr, sc.ptr,
-                                   None if z is None else z.ptr, stream), "lbd_quantize_int4", False)
+    fn = lib().lbd_quantize_int4 if group == GROUP else lib().lbd_quantize_int4_g32
+    _check(fn(src.ptr, n, k, int(asym), int(scale == "signed-max"), qw.ptr, sc.ptr, None if z is None else z.ptr,
+              stream), "lbd_quantize_int4", False)
     if stream is not None:
         _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)  # src may be freed next
     nbytes = n * kp // 2 + n * g * 4 + (n * g if asym else 0)
-    return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes)
+    return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes, group)
 
 
 def quantize_mxfp4_device(w, shape=None, stream=None) -> "DeviceMXFP4Weights":
@@ -459,6 +469,24 @@ def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
     return pr.y
 
 
+def _g32_gemm(kind: str, pr: _Prepared, w) -> np.ndarray:
+    """Group-32 int4 GEMMs (lbd_gemm_w4a16_g32 / lbd_gemm_w4a8_g32): host containers
+    are uploaded for the call, device handles used in place."""
+    d = w if isinstance(w, DeviceInt4Weights) else to_device(w)
+    L = lib()
+    m = pr.x.shape[0]
+    dx, dy = DeviceBuffer.from_array(pr.x), DeviceBuffer(pr.y.nbytes)
+    fn = L.lbd_gemm_w4a16_g32 if kind == "w4a16" else L.lbd_gemm_w4a8_g32
+    _check(fn(dx.ptr, m, d.kp, d.qw.ptr, d.scales.ptr, None if d.zeros is None else d.zeros.ptr, d.n, dy.ptr, None),
+           f"lbd_gemm_{kind}_g32")
+    pr.y[...] = dy.to_array(pr.y.shape, np.float32)  # synchronous copy on the null stream
+    return pr.y
+
+
+def _int4_group(w) -> int:
+    return getattr(w, "group", GROUP)
+
+
 # ------------------------------------------------------------------ GEMMs
 
 def gemm_w4a16(x, w, params: Params | None = None, isa=None, threads: int | None = None,
@@ -466,6 +494,8 @@ def gemm_w4a16(x, w, params: Params | None = None, isa=None, threads: int | None
     """Y = X @ dequant(W)^T, fp32 activations and accumulation (src/lowbit/kernels.py:149-156)."""
     pr = _prep or _Prepared(x, w.kp, w.n)
     prm = _params(params, isa, threads, "w4a16", (pr.x.shape[0], w.n, w.k))
+    if _int4_group(w) != GROUP:
+        return _g32_gemm("w4a16", pr, w)
     if isinstance(w, DeviceInt4Weights):
         return _dev_gemm("w4a16", pr, w, prm)
     rc = lib().lb_gemm_w4a16(pr.x, pr.x.shape[0], w.kp, w.qw, w.scales, _zp(w.zeros), w.n, pr.y,
@@ -492,6 +522,8 @@ def gemm_w4a8(x, w, params: Params | None = None, isa=None, threads: int | None 
     (src/lowbit/kernels.py:169-177)."""
     pr = _prep or _Prepared(x, w.kp, w.n)
     prm = _params(params, isa, threads, "w4a8", (pr.x.shape[0], w.n, w.k))
+    if _int4_group(w) != GROUP:
+        return _g32_gemm("w4a8", pr, w)
     if isinstance(w, DeviceInt4Weights):
         return _dev_gemm("w4a8", pr, w, prm)
     rc = lib().lb_gemm_w4a8(pr.x, pr.x.shape[0], w.kp, w.qw, w.scales, _zp(w.zeros), w.n, pr.y,
@@ -503,6 +535,8 @@ def gemm_w4a8(x, w, params: Params | None = None, isa=None, threads: int | None 
 def gemm_w4a8_q(a: Int8Acts, w: Int4Weights, params: Params | None = None, isa=None,
                 threads: int | None = None) -> np.ndarray:
     """W4A8 on already-quantized activations (src/lowbit/kernels.py:180-187)."""
+    if _int4_group(w) != GROUP:
+        raise ValueError("gemm_w4a8_q takes the reference's group-128 weights and group sums")
     y = np.empty((a.xq.shape[0], w.n), np.float32)
     prm = _params(params, isa, threads, "w4a8", (a.xq.shape[0], w.n, w.k))
     rc = lib().lb_gemm_w4a8_q(np.ascontiguousarray(a.xq), np.ascontiguousarray(a.scale, np.float32),
@@ -528,6 +562,8 @@ def quant_act_int8(x: np.ndarray, kp: int) -> Int8Acts:
 def w4a8_group_acc(a: Int8Acts, w: Int4Weights, isa=None) -> np.ndarray:
     """Exact int32 group accumulators [M, N, G] from the device integer path named by
     `isa` ("gfx950" dot4 VALU, "gfx950-mfma" int8 MFMA) (src/lowbit/kernels.py:200-205)."""
+    if _int4_group(w) != GROUP:
+        raise ValueError("w4a8_group_acc takes the reference's group-128 weights")
     m = a.xq.shape[0]
     out = np.empty((m, w.n, w.kp // GROUP), np.int32)
     _check(lib().lb_w4a8_group_acc(np.ascontiguousarray(a.xq), np.ascontiguousarray(a.gsum, np.int32),

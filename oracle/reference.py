@@ -52,16 +52,17 @@ def e2m1_value(code: np.ndarray) -> np.ndarray:
     return np.where(code & 8, -mag, mag)
 
 
-def dequant_int4(qw, scales, zeros, k: int | None = None) -> np.ndarray:
-    """[N, K] float64 values of int4 g128 weights, (q - z) * s.
+def dequant_int4(qw, scales, zeros, k: int | None = None, group: int = GROUP) -> np.ndarray:
+    """[N, K] float64 values of int4 weights with groups of `group` (the reference's
+    128; 32 is the product's extension, the same formula), (q - z) * s.
 
     The product (q - z) * s is rounded to float32 first, as the reference's
     dequantize does (src/lowbit/formats.py:82-87), then widened.
     """
-    q = unpack_codes(qw, GROUP).astype(np.float32)
+    q = unpack_codes(qw, group).astype(np.float32)
     n, kp = q.shape
-    g = kp // GROUP
-    q = q.reshape(n, g, GROUP)
+    g = kp // group
+    q = q.reshape(n, g, group)
     z = np.float32(8.0) if zeros is None else np.asarray(zeros, np.float32)[:, :, None]
     w = ((q - z) * np.asarray(scales, np.float32)[:, :, None]).reshape(n, kp)
     return w[:, : (kp if k is None else k)].astype(np.float64)
@@ -83,9 +84,9 @@ def _xpad(x: np.ndarray, kp: int) -> np.ndarray:
     return x
 
 
-def gemm_w4a16_ref(x, qw, scales, zeros) -> np.ndarray:
+def gemm_w4a16_ref(x, qw, scales, zeros, group: int = GROUP) -> np.ndarray:
     """Y = X @ dequant(W)^T in float64 (src/lowbit/reference.py:9-11)."""
-    w = dequant_int4(qw, scales, zeros)
+    w = dequant_int4(qw, scales, zeros, group=group)
     return _xpad(x, w.shape[1]) @ w.T
 
 
@@ -118,40 +119,41 @@ def quant_act_int8(x: np.ndarray, kp: int | None = None):
     return xq, xs, asum
 
 
-def w4a8_group_acc_ref(xq, qw, zeros) -> np.ndarray:
+def w4a8_group_acc_ref(xq, qw, zeros, group: int = GROUP) -> np.ndarray:
     """Exact int64 acc[m, n, g] = sum_{k in g} (q[n,k] - z[n,g]) * xq[m,k]
-    (src/lowbit/reference.py:18-26)."""
+    (src/lowbit/reference.py:18-26; `group` 32 is the product's extension)."""
     xq = np.atleast_2d(np.asarray(xq, np.int64))
-    q = unpack_codes(qw, GROUP).astype(np.int64)
+    q = unpack_codes(qw, group).astype(np.int64)
     n, kp = q.shape
     m = xq.shape[0]
-    g = kp // GROUP
+    g = kp // group
     z = np.full((n, g), 8, np.int64) if zeros is None else np.asarray(zeros, np.int64)
-    qc = q.reshape(n, g, GROUP) - z[:, :, None]
-    xa = xq.reshape(m, g, GROUP)
+    qc = q.reshape(n, g, group) - z[:, :, None]
+    xa = xq.reshape(m, g, group)
     out = np.empty((m, n, g), np.int64)
     for gi in range(g):  # int64 matmul per group: exact, and fast enough for test sizes
         out[:, :, gi] = xa[:, gi, :] @ qc[:, gi, :].T
     return out
 
 
-def gemm_w4a8_ref(xq, xs, qw, scales, zeros) -> np.ndarray:
+def gemm_w4a8_ref(xq, xs, qw, scales, zeros, group: int = GROUP) -> np.ndarray:
     """Y[m,n] = xs[m] * sum_g s[n,g] * acc[m,n,g] in float64 (src/lowbit/reference.py:29-34)."""
-    acc = w4a8_group_acc_ref(xq, qw, zeros).astype(np.float64)
+    acc = w4a8_group_acc_ref(xq, qw, zeros, group).astype(np.float64)
     y = np.einsum("mng,ng->mn", acc, np.asarray(scales, np.float64))
     return y * np.asarray(xs, np.float64)[:, None]
 
 
-def w4a8_lane_bound(xq, xs, asum, qw, scales, zeros) -> np.ndarray:
+def w4a8_lane_bound(xq, xs, asum, qw, scales, zeros, group: int = GROUP) -> np.ndarray:
     """Magnitude the W4A8 fp32 rescale error is measured against: per group
-    sum_k q|a| + z|sum a|, times |s| and xs (tests/test_kernels.py:135-143)."""
+    sum_k q|a| + z|sum a|, times |s| and xs (tests/test_kernels.py:135-143).
+    `asum` holds the activation sums per group of `group`."""
     xq = np.atleast_2d(np.asarray(xq, np.float64))
-    q = unpack_codes(qw, GROUP).astype(np.float64)
+    q = unpack_codes(qw, group).astype(np.float64)
     n, kp = q.shape
-    g = kp // GROUP
+    g = kp // group
     z = np.full((n, g), 8.0) if zeros is None else np.asarray(zeros, np.float64)
-    aa = np.abs(xq).reshape(-1, g, GROUP)
-    qq = q.reshape(n, g, GROUP)
+    aa = np.abs(xq).reshape(-1, g, group)
+    qq = q.reshape(n, g, group)
     mag = np.einsum("mgk,ngk->mng", aa, qq) + z[None] * np.abs(np.asarray(asum, np.float64))[:, None, :]
     return np.einsum("mng,ng->mn", mag, np.abs(np.asarray(scales, np.float64))) * np.abs(
         np.asarray(xs, np.float64))[:, None]
