@@ -48,6 +48,7 @@ BATCH_SHAPES = [(16, 4096, 4096), (64, 4096, 4096), (16, 11008, 4096), (64, 1100
 PREFILL_SHAPES = [(512, 4096, 4096), (2048, 4096, 4096)]
 QUICK_SHAPES = [(1, 4096, 4096), (16, 4096, 4096)]
 FORMATS = ["w4a16", "w4a8", "mxfp4"]
+G32_FORMATS = ["w4a16", "w4a8"]  # int4 with groups of 32 (decode shapes only)
 HEADLINE_SHAPE = (1, 11008, 4096)
 
 # MI355X published peaks (dense)
@@ -155,7 +156,8 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
     L, s = timer.L, timer.stream
     m, n, _ = shape
     prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
-    mfma = _check(L.lbd_gemm_path(_KIND[fmt], m, W.kp, C.byref(prm)), "path") == K.ISA_GFX950_MFMA
+    g32 = getattr(W, "group", F.GROUP) == 32
+    mfma = not g32 and _check(L.lbd_gemm_path(_KIND[fmt], m, W.kp, C.byref(prm)), "path") == K.ISA_GFX950_MFMA
     copies = max(1, -(-COLD_POOL_BYTES // W.nbytes)) if cold else 1
     first = K.to_device(W)
     pool = [first] + [K.to_device(W) for _ in range(copies - 1)]
@@ -171,6 +173,10 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
 
     def launch(i):
         d = pool[i % len(pool)]
+        if g32:
+            fn = L.lbd_gemm_w4a16_g32 if fmt == "w4a16" else L.lbd_gemm_w4a8_g32
+            return _check(fn(dx.ptr, m, W.kp, d.qw.ptr, d.scales.ptr, None if d.zeros is None else d.zeros.ptr, n,
+                             dy.ptr, s), f"{fmt} g32 GEMM")
         if mfma:
             if fmt == "mxfp4":
                 qwt, et = d.tiles()
@@ -222,6 +228,7 @@ def run(shapes=None, cold: bool = True, seed: int = 0, n_launch: int = 50, reps:
         x = rng.standard_normal((m, k)).astype(np.float32)
         wq = {"w4a16": F.quantize_int4(w), "mxfp4": F.quantize_mxfp4(w)}
         wq["w4a8"] = wq["w4a16"]
+        w32 = w if m == 1 else None
         del w
         ref = {f: x.astype(np.float64) @ wq[f].dequantize().T.astype(np.float64) for f in ("w4a16", "mxfp4")}
         ref["w4a8"] = ref["w4a16"]
@@ -249,6 +256,30 @@ def run(shapes=None, cold: bool = True, seed: int = 0, n_launch: int = 50, reps:
                 rows.append(row)
                 log(f"  [{mode}] {row['method']:<18} {med * 1e6:9.2f} us  {row['gflops']:10.1f} GFLOP/s  "
                     f"{row['weight_gbps']:7.1f} GB/s  {100 * frac:5.1f}% of {roof}  rel err {row['max_rel_err']:.2g}")
+            if m > 1:
+                continue
+            # int4 with groups of 32 (this package's extension): decode shapes
+            for fmt in G32_FORMATS:
+                W = W32 = wq.setdefault("g32", F.quantize_int4(w32, group=32))
+                ref32 = ref.setdefault("g32", x.astype(np.float64) @ W32.dequantize().T.astype(np.float64))
+                launch, y, path, layout, copies, keep = _gemm_case(timer, fmt, (m, n, k), W, x, mode == "cold")
+                nl = max(n_launch, 2 * copies) if mode == "cold" else n_launch
+                ts = timer.samples(launch, nl, reps)
+                del keep
+                med, mn = statistics.median(ts), min(ts)
+                roof, frac = _roofline(fmt, layout, m, n, k, med, W.nbytes)
+                rows.append({
+                    "phase": phase, "M": m, "N": n, "K": k, "threads": None, "cache": mode,
+                    "method": f"{fmt}-g32 {path}", "format": f"{fmt}-g32", "isa": path, "params": None,
+                    "reps": len(ts), "t_median_s": med, "t_min_s": mn,
+                    "gflops": 2.0 * m * n * k / med / 1e9, "weight_bytes": int(W.nbytes),
+                    "weight_gbps": W.nbytes / med / 1e9, "speedup_vs_numpy_fp32": None,
+                    "max_rel_err": _rel_err(y, ref32), "device": info.get("arch"), "weight_layout": layout,
+                    "pool_copies": copies, "launches_per_rep": nl, "roofline": roof, "roofline_frac": frac,
+                })
+                r = rows[-1]
+                log(f"  [{mode}] {r['method']:<18} {med * 1e6:9.2f} us  {r['weight_gbps']:7.1f} GB/s  "
+                    f"{100 * frac:5.1f}% of {roof}  rel err {r['max_rel_err']:.2g}")
     meta = {
         "date": _dt.datetime.now(_dt.timezone.utc).isoformat(timespec="seconds"),
         "device": f"{info.get('arch')} ({info.get('compute_units')} CUs)",
@@ -325,6 +356,17 @@ def report(res: dict) -> str:
             refs.append(f"{ref[2]:.1f}" if ref else "—")
         out.append(f"| {sh[0]} | {sh[1]} | {sh[2]} | " + " | ".join(cells + refs) + " |")
     out.append("")
+    g32 = [r for r in rows if r["format"].endswith("-g32")]
+    if g32:
+        out += ["**int4 with groups of 32** (this package's extension; the reference ships group 128) — decode "
+                "shapes, the same weights as above with 4x the scales:\n",
+                "| M | N | K | cache | method | weight bytes | time | weight GB/s | % of HBM roofline | rel err |",
+                "|---|---|---|---|---|---|---|---|---|---|"]
+        for r in g32:
+            out.append(f"| {r['M']} | {r['N']} | {r['K']} | {r['cache']} | {r['method']} | "
+                       f"{r['weight_bytes'] / 2**20:.1f} MiB | {_t(r['t_median_s'])} | {r['weight_gbps']:.0f} | "
+                       f"{100 * r['roofline_frac']:.1f} % | {r['max_rel_err']:.2g} |")
+        out.append("")
     out.append(f"Measured {meta['date']} on {meta['device']}; {meta['timing']}. Maximum relative error against "
                f"float64 over every row: {max(r['max_rel_err'] for r in rows):.2g}. Reference rows: its "
                "results/bench.json (Xeon @ 2.10 GHz, 4 vCPU, AVX-512 VNNI + AMX).")

@@ -40,3 +40,12 @@ def test_reference_table_covers_the_published_shapes():
     for (m, n, k) in R.BATCH_SHAPES[:4]:
         for f in R.FORMATS:
             assert (m, n, k, f, "hot") in R.REFERENCE_4T
+
+
+def test_report_group32_table():
+    rows = [_row(1, 11008, 4096, f, "cold", 7.6e-6, "row-major") for f in R.FORMATS]
+    r = _row(1, 11008, 4096, "w4a8", "cold", 8.0e-6, "row-major")
+    r.update(format="w4a8-g32", method="w4a8-g32 gfx950")
+    rows.append(r)
+    md = R.report({"meta": {"date": "d", "device": "gfx950", "timing": "graph"}, "rows": rows})
+    assert "groups of 32" in md and "| 1 | 11008 | 4096 | cold | w4a8-g32 gfx950 |" in md
