@@ -227,12 +227,24 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
   }
 }
 
+// The persistent grid puts two 8-wave workgroups on every CU, i.e. four waves per
+// SIMD, which needs at most 128 VGPRs per lane; the int8 one-row kernels without a
+// prologue are asked to fit (their longest-row variants would otherwise use a few
+// more, and the second workgroup of every CU would wait for the first). The fp32
+// kernels of rows past 8192 elements, and the prologue variants, need far more and
+// are left unconstrained.
+template <int F, int MB, int PRO>
+struct GemvMinWaves {
+  static constexpr int value = (F == F_W4A8 || F == F_W4A8G32) && MB == 1 && PRO == 0 ? 4 : 1;
+};
+
 // PRO selects a fused prologue on the (single, register-held) activation row:
 // 0 none, 1 RMSNorm (x * (1 / sqrt(mean(x^2) + eps)) * norm_w, the mean over Kp),
 // 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
 // adds `bias` and `res` when given and max-combines argmax keys into `amax_key`.
 template <int F, int MB, int R, int NIT, int PRO>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(GemvMinWaves<F, MB, PRO>::value)))
+void gemv_kernel(GemmArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[2][kGemvWaves];
   constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q || F == F_W4A8G32);
