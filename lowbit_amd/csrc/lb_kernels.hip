@@ -452,7 +452,6 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_mfma_kernel(GemmArgs a, int32
 // phase of 32). fp32 rounding of the split terms stays within the reference's W4A8
 // bound, which is built from both magnitudes (sum q|a| and z|sum a|).
 
-constexpr int kW8PF = 2;  // weight subtiles in flight ahead of the one computed
 constexpr int kW8GB = 1;  // groups whose MFMAs are issued together
 
 // Weight operands of one subtile when all four of the wave's groups exist and G % 4
@@ -515,7 +514,7 @@ __device__ __forceinline__ void w8_tile(const W8Stage &cur, const v4i (&xlo)[kW8
 // WT: weights in the t16 tile layout, so each 16-byte weight load of a wave is one
 // contiguous 1 KiB tile instead of 64 bytes from each of 16 rows (the row-major
 // pattern runs at about half the cache bandwidth). Groups past G hold zeros there.
-template <int TM, int NS, bool VEC, bool FULL, bool TILED, bool WT>
+template <int TM, int NS, int PF, bool VEC, bool FULL, bool TILED, bool WT>
 __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
   static_assert(!FULL || VEC, "the full path needs G % 4 == 0");
   static_assert(!WT || VEC, "the t16 layout pads groups to a multiple of 4");
@@ -563,14 +562,20 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
 
   v4i xlo[kW8GW][TM], xhi[kW8GW][TM];
   float asf[TM];
+  // partial tiles: in registers across the phases of a chunk for the tall tiles
+  // (TM = 4: their activations fill half the register file), otherwise written
+  // to the LDS reduction buffer as each subtile completes, which frees the
+  // registers for more weight subtiles in flight
+  constexpr bool kRegAcc = TM >= 4;
   for (int cb = sb; cb < se; cb += NS) {
     const int ce = min(cb + NS, se);
-    v4f facc[NS][TM];
+    v4f racc[kRegAcc ? NS : 1][TM];
+    if constexpr (kRegAcc) {
 #pragma unroll
-    for (int j = 0; j < NS; j++)
+      for (int j = 0; j < NS; j++)
 #pragma unroll
-      for (int i = 0; i < TM; i++) facc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
-
+        for (int i = 0; i < TM; i++) racc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
     for (int ph = 0; ph < nph; ph++) {
       const int gb = ph * kW8Phase + wave * kW8GW;     // this wave's first group
       const int gcnt = max(0, min(kW8GW, G - gb));
@@ -594,10 +599,11 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
           w8_load<VEC>(st, rw, rs, rz, in ? 16 * sj + c : N, N, gb, gcnt, G, rowbytes, q);
         }
       };
-      // weights of the first PF + 1 subtiles go out before the activations
-      W8Stage st[kW8PF + 1];
-#pragma unroll
-      for (int j = 0; j <= kW8PF; j++) load(st[j], j);
+      // issue order = retirement order: the first subtile's weights, then the
+      // activations, then the other PF subtiles of the chunk, so the first
+      // MFMAs wait for the first subtile and the activations alone
+      W8Stage st[PF + 1];
+      load(st[0], 0);
       if (nph > 1 || cb == sb) {
         // activation operands of this wave's groups (groups past G read 0, so the
         // weights of those slots never matter) and the group sums of the
@@ -629,9 +635,12 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
         }
       }
 #pragma unroll
+      for (int j = 1; j <= PF; j++)
+        if (cb + j < ce) load(st[j], j);  // workgroup-uniform: stages past the chunk stay unused
+#pragma unroll
       for (int j = 0; j < NS; j++) {
         if (cb + j >= ce) break;  // workgroup-uniform
-        W8Stage &cur = st[j % (kW8PF + 1)];
+        W8Stage &cur = st[j % (PF + 1)];
         const int n = 16 * (cb + j) + c;
         if constexpr (!FULL) {
           // groups past G: zero scales (their activations are zero too)
@@ -654,17 +663,36 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
           zq = q == 3 ? z3 : zq;
         }
         const float bz = -sq * (float)(zq + zadd);
-        w8_tile<TM>(cur, xlo, xhi, asf, bz, facc[j]);
+        if constexpr (kRegAcc) {
+          w8_tile<TM>(cur, xlo, xhi, asf, bz, racc[j]);
+        } else {
+          // each thread owns its LDS slots, so no barrier is needed until the
+          // reduction; later phases add onto the earlier ones
+          v4f *slot = reinterpret_cast<v4f *>(&red[((j * TM * kW8Waves + wave) * kWave + lane) * 4]);
+          v4f facc[TM];
+#pragma unroll
+          for (int i = 0; i < TM; i++) facc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+          w8_tile<TM>(cur, xlo, xhi, asf, bz, facc);
+          if (ph == 0) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) slot[i * kW8Waves * kWave] = facc[i];
+          } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++) slot[i * kW8Waves * kWave] += facc[i];
+          }
+        }
         // refill this stage with subtile j + PF + 1 (zero-length past the chunk)
-        if (j + kW8PF + 1 < NS) load(cur, j + kW8PF + 1);
+        if (j + PF + 1 < NS) load(cur, j + PF + 1);
       }
     }
     // ---- reduce the waves' partial tiles of the chunk, scale by xs, store
+    if constexpr (kRegAcc) {
 #pragma unroll
-    for (int j = 0; j < NS; j++)
+      for (int j = 0; j < NS; j++)
 #pragma unroll
-      for (int i = 0; i < TM; i++)
-        *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) = facc[j][i];
+        for (int i = 0; i < TM; i++)
+          *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) = racc[j][i];
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < (ce - cb) * TM * kWave; e += kW8Threads) {
       const int j = e / (kWave * TM);  // e % 64 == rlane, (e / 64) % TM == rblk
@@ -685,24 +713,34 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
   }
 }
 
-// Largest NS (subtiles held per chunk) each TM affords in registers.
-template <int TM> struct W8NS { static constexpr int value = TM >= 4 ? 1 : TM == 2 ? 3 : 6; };
+// Subtiles per chunk (NS: their partial tiles share the LDS reduction buffer) and
+// weight subtiles in flight ahead of the one computed (PF: PF + 1 stages of
+// registers next to the 2 * TM * kW8GW activation operands; PF for t16 weights,
+// PFR for row-major ones and PFS for the per-group weight loads of G % 4 != 0,
+// whose addressing needs more registers). The largest values that compile
+// without spills.
+template <int TM> struct W8Cfg {
+  static constexpr int NS = TM >= 4 ? 1 : 6;
+  static constexpr int PF = TM >= 4 ? 0 : 5;
+  static constexpr int PFR = TM >= 4 ? 0 : 4;
+  static constexpr int PFS = TM >= 4 ? 0 : TM == 2 ? 2 : 3;
+};
 
 template <int TM, bool TILED>
 static void launch_w4a8_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
-  constexpr int NS = W8NS<TM>::value;
+  constexpr int NS = W8Cfg<TM>::NS, PF = W8Cfg<TM>::PF, PFR = W8Cfg<TM>::PFR, PFS = W8Cfg<TM>::PFS;
   const int G = a.Kp / kGroup;
   if (a.wt16) {
     if (G % kW8Phase == 0)
-      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, true, true, true>), grid, dim3(kW8Threads), 0, s, a);
+      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PF, true, true, true, true>), grid, dim3(kW8Threads), 0, s, a);
     else
-      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, false, true, true>), grid, dim3(kW8Threads), 0, s, a);
+      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PF, true, false, true, true>), grid, dim3(kW8Threads), 0, s, a);
   } else if (G % kW8Phase == 0) {
-    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, true, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PFR, true, true, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
   } else if (G % 4 == 0) {
-    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, true, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PFR, true, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, false, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PFS, false, false, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
   }
 }
 
@@ -859,15 +897,17 @@ __device__ __forceinline__ void w4_bf16x4(uint32_t nib, float zf, uint32_t &d0, 
   d1 = pack_bf16(__float_as_uint(f2), __float_as_uint(f3));
 }
 
-constexpr int kB3PF = 3;  // weight subtiles in flight ahead of the one computed
-
 // Waves split the K groups (wave w takes group 8 ph + w of phase ph) and keep
 // their activation operands (4 x 3 x TM x 1 KiB) in registers across the
 // workgroup's subtiles; per subtile and row block, 12 MFMAs accumulate the group
 // (W4A16) or the four blocks (MXFP4) and one FMA per output applies the fp32
-// factor. Partial tiles are reduced across waves in LDS once per chunk of NS
-// subtiles, in a fixed order.
-template <int F, int TM, int NS>
+// factor. A chunk holds up to NS subtiles (normally all of the workgroup's), so
+// each phase's activations are loaded once per workgroup; each subtile's partial
+// tile is kept in the LDS reduction buffer (each thread owns its slots, later
+// phases accumulate onto them), which leaves the registers for PF weight
+// subtiles in flight. Partial tiles are reduced across waves in LDS once per
+// chunk, in a fixed order.
+template <int F, int TM, int NS, int PF>
 __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
   const int lane = threadIdx.x & (kWave - 1);
@@ -892,12 +932,14 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   v4u xa[4][3][TM];
   for (int cb = sb; cb < se; cb += NS) {
     const int ce = min(cb + NS, se);
-    v4f facc[NS][TM];
+    if (wave >= G) {
+      // no group in any phase (Kp < 1024): this wave's partial tiles are zero
+      for (int j = 0; j < ce - cb; j++)
 #pragma unroll
-    for (int j = 0; j < NS; j++)
-#pragma unroll
-      for (int i = 0; i < TM; i++) facc[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
-
+        for (int i = 0; i < TM; i++)
+          *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) =
+              v4f{0.f, 0.f, 0.f, 0.f};
+    }
     for (int ph = 0; ph < nph; ph++) {
       const int g = ph * kW8Waves + wave;
       if (g >= G) continue;  // wave-uniform: this wave has no group in the last phase
@@ -915,9 +957,10 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
           st.z = ld_u8(rs, in ? tile * kWave + lane : 0xFFFFFFF0u);
         }
       };
-      B3Stage st[kB3PF + 1];
-#pragma unroll
-      for (int j = 0; j <= kB3PF; j++) load(st[j], j);
+      // issue order = retirement order: the first subtile's weights, then the
+      // activations, then the other PF subtiles of the chunk
+      B3Stage st[PF + 1];
+      load(st[0], 0);
       if (nph > 1 || cb == sb) {
 #pragma unroll
         for (int u = 0; u < 4; u++)
@@ -932,11 +975,18 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
             }
       }
 #pragma unroll
+      for (int j = 1; j <= PF; j++)
+        if (cb + j < ce) load(st[j], j);  // workgroup-uniform: stages past the chunk stay unused
+#pragma unroll
       for (int j = 0; j < NS; j++) {
         // workgroup-uniform guard instead of a break: a constant trip count lets the
-        // loop unroll fully, so facc[j] stays in registers
+        // loop unroll fully
         if (cb + j >= ce) continue;
-        B3Stage &cur = st[j % (kB3PF + 1)];
+        B3Stage &cur = st[j % (PF + 1)];
+        v4f *slot = reinterpret_cast<v4f *>(&red[((j * TM * kW8Waves + wave) * kWave + lane) * 4]);
+        v4f prev[TM];  // the earlier phases' sum of this subtile (read ahead of the MFMAs)
+#pragma unroll
+        for (int i = 0; i < TM; i++) prev[i] = ph == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : slot[i * kW8Waves * kWave];
         v4u b[4];
         float fs;
         if constexpr (F == F_W4A16) {
@@ -983,18 +1033,15 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
             for (int p = 0; p < 3; p++)
               dacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[u][p][i]),
                                                              __builtin_bit_cast(v8bf, b[u]), dacc, 0, 0, 0);
+          v4f f;
 #pragma unroll
-          for (int r = 0; r < 4; r++) facc[j][i][r] = __builtin_fmaf(fs, dacc[r], facc[j][i][r]);
+          for (int r = 0; r < 4; r++) f[r] = __builtin_fmaf(fs, dacc[r], prev[i][r]);
+          slot[i * kW8Waves * kWave] = f;
         }
-        if (j + kB3PF + 1 < NS) load(cur, j + kB3PF + 1);
+        if (j + PF + 1 < NS) load(cur, j + PF + 1);
       }
     }
     // ---- reduce the waves' partial tiles of the chunk and store
-#pragma unroll
-    for (int j = 0; j < NS; j++)
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-        *reinterpret_cast<v4f *>(&red[(((j * TM + i) * kW8Waves + wave) * kWave + lane) * 4]) = facc[j][i];
     __syncthreads();
     for (int e = threadIdx.x; e < (ce - cb) * TM * kWave; e += kW8Threads) {
       const int l = e % kWave, i = (e / kWave) % TM, j = e / (kWave * TM);
@@ -1015,14 +1062,31 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   }
 }
 
-template <int TM> struct B3NS { static constexpr int value = TM >= 2 ? 4 : 8; };
+// Subtiles per chunk (their partial tiles fill NS * TM * 8 KiB of LDS) and weight
+// subtiles in flight (PF + 1 stages of 6 registers).
+#ifndef XB3NS1
+#define XB3NS1 8
+#endif
+#ifndef XB3NS2
+#define XB3NS2 6
+#endif
+#ifndef XB3PF1
+#define XB3PF1 7
+#endif
+#ifndef XB3PF2
+#define XB3PF2 5
+#endif
+template <int TM> struct B3Cfg {
+  static constexpr int NS = TM >= 2 ? XB3NS2 : XB3NS1;
+  static constexpr int PF = TM >= 2 ? XB3PF2 : XB3PF1;
+};
 
 template <int F, int TM>
 static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
-  constexpr int NS = B3NS<TM>::value;
+  constexpr int NS = B3Cfg<TM>::NS, PF = B3Cfg<TM>::PF;
   const int gy = (a.M + 16 * TM - 1) / (16 * TM), S = (a.N + 15) / 16;
   const int gx = std::max(1, std::min(S, cus / gy));
-  hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, NS>), dim3(gx, gy), dim3(kW8Threads), 0, s, a);
+  hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, NS, PF>), dim3(gx, gy), dim3(kW8Threads), 0, s, a);
 }
 
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {

@@ -10,6 +10,7 @@
 #include <math.h>
 
 #include "lb_device.h"
+#include "lb_attn.h"
 #include "lb_internal.h"
 
 namespace lbk {
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(kWave) void attention_kernel(const float *__restric
 //   1. rotate the query head and the key ("rotate_half", src/lowbit/model.py:
 //      201-210) into LDS; the group's first workgroup writes the rotated key and
 //      the value to the caches at p (when p < cap);
-//   2. over chunks of kAttChunk keys (online softmax, src/lowbit/model.py:353-378):
+//   2. over chunks of kAttThreads keys (online softmax, src/lowbit/model.py:353-378):
 //      thread t scores key c0 + t, the chunk maximum updates the running maximum,
 //      and wave w accumulates p * v over its 64 keys, lane l owning output
 //      elements l, l + 64, ...;
@@ -176,47 +177,25 @@ __global__ __launch_bounds__(kWave) void attention_kernel(const float *__restric
 // one (from LDS, never read back from the cache), otherwise all S come from the
 // cache, as lbd_qkv_rope + lbd_attention behave. Output out [H D].
 constexpr int kAttThreads = 256;
-constexpr int kAttWaves = kAttThreads / kWave;
-constexpr int kAttChunk = kAttThreads;
-constexpr int kAttVB = 16;  // values in flight per lane in the p * v loop past the first chunk
 
 template <int D>
 __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
     const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
     const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc, float *__restrict__ vc, int cap,
     float *__restrict__ out) {
-  constexpr int half = D / 2, DPL = (D + kWave - 1) / kWave, NK4 = D / 4;
-  constexpr bool kPre = D <= 64;
+  constexpr int half = D / 2;
   __shared__ __align__(16) float qs[D];
   __shared__ __align__(16) float kn[D];
   __shared__ float vn[D];
-  __shared__ float pb[kAttChunk];
-  __shared__ float red[kAttWaves];
-  __shared__ float part[kAttWaves][D];
-  __shared__ float lsw[kAttWaves];
+  __shared__ AttnShared<D, kAttThreads> sh;
   const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int tid = threadIdx.x;
   const float *kb = kc + (size_t)g * cap * D;
   const float *vb = vc + (size_t)g * cap * D;
-  const bool own = D >= kWave || lane < D;  // D = 32: lanes 32..63 hold no output
-  const int l = own ? lane : 0;
 
-  // ---- 0. prefetch of the first chunk's keys and values (rows clamped below cap)
-  float4 kpre[kPre ? NK4 : 1];
-  float vpre[kPre ? kWave * DPL : 1];
-  if constexpr (kPre) {
-    const int t = tid < cap ? tid : cap - 1;
-    const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)t * D);
-#pragma unroll
-    for (int e = 0; e < NK4; e++) kpre[e] = kr[e];
-#pragma unroll
-    for (int u = 0; u < kWave; u++) {
-      const int row = wave * kWave + u < cap ? wave * kWave + u : cap - 1;
-#pragma unroll
-      for (int q = 0; q < DPL; q++) vpre[u * DPL + q] = vb[(size_t)row * D + l + kWave * q];
-    }
-  }
+  // ---- 0. prefetch of the first chunk's keys and values
+  AttnPre<D> pre;
+  attn_prefetch<D, kAttThreads>(pre, kb, vb, cap);
 
   const int p = *pos;
   const int pc = p < 0 ? 0 : (p < max_pos ? p : max_pos - 1);  // positions past the tables reuse the last angle
@@ -230,7 +209,8 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
     const int hd = which == 0 ? h : H + g;
     const float x1 = qkv[(size_t)hd * D + i], x2 = qkv[(size_t)hd * D + i + half];
     const float c = cosT[(size_t)pc * half + i], sn = sinT[(size_t)pc * half + i];
-    const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+    float y1, y2;
+    rope_pair(x1, x2, c, sn, y1, y2);
     if (which == 0) {
       qs[i] = y1;
       qs[i + half] = y2;
@@ -250,114 +230,8 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   }
   __syncthreads();
 
-  const float scale = 1.0f / sqrtf((float)D);
-  float acc[DPL], lsum = 0.0f, mrun = -INFINITY;
-#pragma unroll
-  for (int q = 0; q < DPL; q++) acc[q] = 0.0f;
-
-  for (int c0 = 0; c0 < S; c0 += kAttChunk) {
-    const bool pre = kPre && c0 == 0;
-    // ---- 2a. score of key c0 + tid
-    const int s = c0 + tid;
-    float d = 0.0f;
-    if (s < S) {
-      float4 kv[NK4];
-      if (s >= Sc) {
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = reinterpret_cast<const float4 *>(kn)[e];
-      } else if (pre) {
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = kpre[e < (kPre ? NK4 : 1) ? e : 0];
-      } else {
-        const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)s * D);
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = kr[e];
-      }
-#pragma unroll
-      for (int e = 0; e < NK4; e++) {
-        const float4 qv = reinterpret_cast<const float4 *>(qs)[e];
-        d = __builtin_fmaf(qv.x, kv[e].x, d);
-        d = __builtin_fmaf(qv.y, kv[e].y, d);
-        d = __builtin_fmaf(qv.z, kv[e].z, d);
-        d = __builtin_fmaf(qv.w, kv[e].w, d);
-      }
-    }
-    d = s < S ? d * scale : -INFINITY;
-    const float mw = wave_max(d);
-    if (lane == 0) red[wave] = mw;
-    __syncthreads();
-    // ---- 2b. running maximum, probabilities of this chunk, rescaled accumulators
-    float cm = red[0];
-#pragma unroll
-    for (int w = 1; w < kAttWaves; w++) cm = fmaxf(cm, red[w]);
-    const float mnew = fmaxf(mrun, cm);
-    const float alpha = expf(mrun - mnew);  // 0 on the first chunk
-    mrun = mnew;
-    lsum *= alpha;
-#pragma unroll
-    for (int q = 0; q < DPL; q++) acc[q] *= alpha;
-    pb[tid] = s < S ? expf(d - mnew) : 0.0f;
-    __syncthreads();
-    // ---- 2c. wave w: p * v over keys c0 + 64 w .. c0 + 64 w + 63; the new key's
-    //          value from LDS
-    const int sb = c0 + wave * kWave;
-    const int se = sb + kWave < S ? sb + kWave : S;
-    const int sce = se < Sc ? se : Sc;
-    if (pre) {
-#pragma unroll
-      for (int u = 0; u < kWave; u++) {
-        if (sb + u < sce) {
-          const float pr = pb[sb + u - c0];
-          lsum += pr;
-#pragma unroll
-          for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, vpre[(u * DPL + q) % (kPre ? kWave * DPL : 1)], acc[q]);
-        }
-      }
-    } else {
-      for (int k0 = sb; k0 < sce; k0 += kAttVB) {
-        float v[kAttVB][DPL];
-#pragma unroll
-        for (int u = 0; u < kAttVB; u++) {
-          const int k = k0 + u < sce ? k0 + u : sce - 1;  // in-range row; its weight is dropped below
-#pragma unroll
-          for (int q = 0; q < DPL; q++) v[u][q] = vb[(size_t)k * D + l + kWave * q];
-        }
-#pragma unroll
-        for (int u = 0; u < kAttVB; u++) {
-          if (k0 + u < sce) {
-            const float pr = pb[k0 + u - c0];
-            lsum += pr;
-#pragma unroll
-            for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, v[u][q], acc[q]);
-          }
-        }
-      }
-    }
-    if (newk && Sc >= sb && Sc < se) {
-      const float pr = pb[Sc - c0];
-      lsum += pr;
-#pragma unroll
-      for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, vn[l + kWave * q], acc[q]);
-    }
-    __syncthreads();  // pb is rewritten by the next chunk
-  }
-
-  // ---- 3. add the waves' partial sums
-  if (own) {
-#pragma unroll
-    for (int q = 0; q < DPL; q++) part[wave][l + kWave * q] = acc[q];
-  }
-  if (lane == 0) lsw[wave] = lsum;
-  __syncthreads();
-  for (int e = tid; e < D; e += kAttThreads) {
-    float num = 0.0f, den = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kAttWaves; w++) {
-      num += part[w][e];
-      den += lsw[w];
-    }
-    out[(size_t)h * D + e] = num / den;
-  }
+  // ---- 2, 3. online softmax over chunks of kAttThreads keys; the waves' sums
+  attn_run<D, kAttThreads>(pre, qs, kn, vn, kb, vb, S, Sc, newk, sh, out + (size_t)h * D);
 }
 
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
