@@ -27,6 +27,8 @@
 // matrix cores without an LDS transpose.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "lb_device.h"
 #include "lb_gemv.h"
 #include "lb_internal.h"
@@ -601,10 +603,13 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
       };
       // issue order = retirement order: the first subtile's weights, then the
       // activations, then the other PF subtiles of the chunk, so the first
-      // MFMAs wait for the first subtile and the activations alone
+      // MFMAs wait for the first subtile and the activations alone. Every load
+      // is unconditional (stages past the chunk read zero-length ranges, and the
+      // activations are reloaded per chunk from the cache) so that the compiler
+      // can count the loads in flight and wait for exactly the ones needed
       W8Stage st[PF + 1];
       load(st[0], 0);
-      if (nph > 1 || cb == sb) {
+      {
         // activation operands of this wave's groups (groups past G read 0, so the
         // weights of those slots never matter) and the group sums of the
         // zero-point MFMA (lane (q, c): row c of the block, group gb + q)
@@ -634,9 +639,14 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
           asf[i] = (float)(int32_t)ld_u32(ra, q < gcnt ? off : 0xFFFFFFF0u);
         }
       }
+      // the scheduler would otherwise group the loads by type, moving each
+      // subtile's scales behind every later weight load
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 1; j <= PF; j++)
-        if (cb + j < ce) load(st[j], j);  // workgroup-uniform: stages past the chunk stay unused
+      for (int j = 1; j <= PF; j++) {
+        load(st[j], j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int j = 0; j < NS; j++) {
         if (cb + j >= ce) break;  // workgroup-uniform
@@ -726,15 +736,35 @@ template <int TM> struct W8Cfg {
   static constexpr int PFS = TM >= 4 ? 0 : TM == 2 ? 2 : 3;
 };
 
+// Calls go(std::integral_constant<int, P>) with the stages in flight a workgroup
+// of spw subtiles needs: every load is issued, so stages past the workgroup's
+// subtiles would only cost issue slots (0 for one subtile, 1 for two, 3 for up
+// to four, else PFMAX).
+template <int PFMAX, typename Go>
+static void with_prefetch(int spw, Go &&go) {
+  if constexpr (PFMAX == 0) {
+    go(std::integral_constant<int, 0>{});
+  } else {
+    if (spw <= 1) go(std::integral_constant<int, 0>{});
+    else if (spw <= 2) go(std::integral_constant<int, 1>{});
+    else if (spw <= 4 || PFMAX <= 3) go(std::integral_constant<int, (PFMAX < 3 ? PFMAX : 3)>{});
+    else go(std::integral_constant<int, PFMAX>{});
+  }
+}
+
 template <int TM, bool TILED>
 static void launch_w4a8_gemm_t(const GemmArgs &a, dim3 grid, hipStream_t s) {
   constexpr int NS = W8Cfg<TM>::NS, PF = W8Cfg<TM>::PF, PFR = W8Cfg<TM>::PFR, PFS = W8Cfg<TM>::PFS;
   const int G = a.Kp / kGroup;
+  const int spw = ((a.N + 15) / 16 + (int)grid.x - 1) / (int)grid.x;  // subtiles per workgroup
   if (a.wt16) {
-    if (G % kW8Phase == 0)
-      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PF, true, true, true, true>), grid, dim3(kW8Threads), 0, s, a);
-    else
-      hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PF, true, false, true, true>), grid, dim3(kW8Threads), 0, s, a);
+    with_prefetch<PF>(spw, [&](auto pf) {
+      constexpr int P = decltype(pf)::value;
+      if (G % kW8Phase == 0)
+        hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, P, true, true, true, true>), grid, dim3(kW8Threads), 0, s, a);
+      else
+        hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, P, true, false, true, true>), grid, dim3(kW8Threads), 0, s, a);
+    });
   } else if (G % kW8Phase == 0) {
     hipLaunchKernelGGL((w4a8_gemm_kernel<TM, NS, PFR, true, true, TILED, false>), grid, dim3(kW8Threads), 0, s, a);
   } else if (G % 4 == 0) {
@@ -958,10 +988,11 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
         }
       };
       // issue order = retirement order: the first subtile's weights, then the
-      // activations, then the other PF subtiles of the chunk
+      // activations, then the other PF subtiles of the chunk (all unconditional:
+      // stages past the chunk read zero-length ranges, so the waits are exact)
       B3Stage st[PF + 1];
       load(st[0], 0);
-      if (nph > 1 || cb == sb) {
+      {
 #pragma unroll
         for (int u = 0; u < 4; u++)
 #pragma unroll
@@ -974,19 +1005,30 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
               xa[u][p][i] = v4u{v.x, v.y, v.z, v.w};
             }
       }
+      // the scheduler would otherwise group the loads by type, moving each
+      // subtile's scales behind every later weight load
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 1; j <= PF; j++)
-        if (cb + j < ce) load(st[j], j);  // workgroup-uniform: stages past the chunk stay unused
+      for (int j = 1; j <= PF; j++) {
+        load(st[j], j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int j = 0; j < NS; j++) {
-        // workgroup-uniform guard instead of a break: a constant trip count lets the
-        // loop unroll fully
-        if (cb + j >= ce) continue;
+        // only the last slot is guarded (workgroups get floor or ceil of the
+        // average share): earlier subtiles past the chunk (a short last chunk)
+        // read zero-length ranges and fill LDS slots the reduction never reads,
+        // so most of the unrolled loop is one basic block and the scheduler can
+        // decode the next subtile under this one's MFMAs
+        if (j == NS - 1 && cb + j >= ce) continue;
         B3Stage &cur = st[j % (PF + 1)];
         v4f *slot = reinterpret_cast<v4f *>(&red[((j * TM * kW8Waves + wave) * kWave + lane) * 4]);
         v4f prev[TM];  // the earlier phases' sum of this subtile (read ahead of the MFMAs)
 #pragma unroll
-        for (int i = 0; i < TM; i++) prev[i] = ph == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : slot[i * kW8Waves * kWave];
+        for (int i = 0; i < TM; i++) {
+          const v4f t = slot[i * kW8Waves * kWave];  // unconditional: a select, not a branch
+          prev[i] = ph == 0 ? v4f{0.f, 0.f, 0.f, 0.f} : t;
+        }
         v4u b[4];
         float fs;
         if constexpr (F == F_W4A16) {
@@ -1086,7 +1128,22 @@ static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
   constexpr int NS = B3Cfg<TM>::NS, PF = B3Cfg<TM>::PF;
   const int gy = (a.M + 16 * TM - 1) / (16 * TM), S = (a.N + 15) / 16;
   const int gx = std::max(1, std::min(S, cus / gy));
-  hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, NS, PF>), dim3(gx, gy), dim3(kW8Threads), 0, s, a);
+  // every subtile slot of a chunk but the last is computed, so the chunk length
+  // is the workgroup's share (up to NS; its loads all in flight)
+  const int spw = (S + gx - 1) / gx;
+  auto go = [&](auto ns) {
+    constexpr int C = decltype(ns)::value < NS ? decltype(ns)::value : NS;
+    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF)>), dim3(gx, gy), dim3(kW8Threads), 0, s,
+                       a);
+  };
+  switch (spw) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 5: go(std::integral_constant<int, 5>{}); break;
+    default: go(std::integral_constant<int, NS>{}); break;
+  }
 }
 
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
