@@ -313,7 +313,7 @@ int lbd_gemv_w4a8_fused(const float *x, int M, int Kp, const uint8_t *qw, const 
 int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc,
                         int32_t *hist, int hist_len, void *stream);
 /* One token at position *pos: lbd_qkv_rope (without the bias, which the qkv GEMV's
- * epilogue adds) and lbd_attention with T = 1 in one launch, one workgroup per KV
+ * epilogue adds) and lbd_attention with T = 1 in one launch, one workgroup per query
  * head (model.py:353-378). qkv [(H + 2 KV) D] is read only; k and v are written to
  * the caches; out [H D]. H / KV <= 16, D in {32, 64, 128}, cap <= 16000. */
 int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table,

@@ -192,8 +192,11 @@ __device__ __forceinline__ void attn_run(const AttnPre<D> &pre, const float *qs,
 }
 
 // Rotate the pair (x1, x2) of element i of a head at the table row pc
-// ("rotate_half", src/lowbit/model.py:201-210).
+// ("rotate_half", src/lowbit/model.py:201-210): each product rounded, then the
+// sum, as numpy's float32 evaluates it (no fused multiply-add, so every kernel
+// that inlines this gives the same bits).
 __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, float &y1, float &y2) {
+#pragma clang fp contract(off)
   y1 = x1 * c - x2 * s;
   y2 = x2 * c + x1 * s;
 }

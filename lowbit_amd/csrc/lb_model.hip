@@ -76,7 +76,8 @@ __global__ void qkv_rope_kernel(float *__restrict__ qkv, const float *__restrict
   if (hd < H + KV) {  // q or k: rotate
     const int pp = p < max_pos ? p : max_pos - 1;  // positions past the tables reuse the last angle
     const float c = cosT[(size_t)pp * half + i], s = sinT[(size_t)pp * half + i];
-    const float y1 = x1 * c - x2 * s, y2 = x2 * c + x1 * s;
+    float y1, y2;
+    rope_pair(x1, x2, c, s, y1, y2);
     x1 = y1;
     x2 = y2;
   }
