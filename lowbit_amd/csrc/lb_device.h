@@ -110,6 +110,20 @@ __device__ __forceinline__ uint32_t ld_u32(Rsrc r, uint32_t off) {
 __device__ __forceinline__ uint32_t ld_u8(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }
+// With a workgroup-uniform part `soff` in the instruction's scalar offset, so that
+// loads at several uniform distances share one vector offset register. The
+// hardware range check covers the vector offset only: soff must keep the access
+// inside the buffer.
+__device__ __forceinline__ uint4 ld_b128(Rsrc r, uint32_t voff, uint32_t soff) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float ld_f32(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint32_t ld_u32(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
 
 // Hides a value from the optimizer (no instruction is emitted), so that a mask
 // is not folded into later byte extractions: (m >> 8k) & 0xFF of an opaque m

@@ -444,9 +444,13 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_mfma_kernel(GemmArgs a, int32
 //     the second sum over a wave's four groups is one v_mfma_f32_16x16x4_f32 per
 //     row block (A = asum of the 16 rows x 4 groups, B = -s z of the 16 weight rows
 //     x 4 groups), accumulated into the same fp32 tile.
-//   * latency: weights of the next PF subtiles are in flight while one is computed,
-//     and the waves' partial tiles of a whole chunk of NS subtiles are reduced in
-//     LDS once, with one barrier, instead of once per subtile.
+//   * latency: a workgroup's subtiles form one chunk (up to NS), whose weight loads
+//     are all in flight (PF stages ahead of the one computed): each subtile's
+//     partial tile goes to the LDS reduction buffer as it completes, so registers
+//     hold weights rather than accumulators, and the waves' tiles are reduced once
+//     per chunk with one barrier. Loads are issued in need order (first subtile,
+//     activations, later subtiles) behind scheduling barriers, and every load is
+//     unconditional, so each subtile waits for its own stage alone.
 //   * L1/L2 bandwidth: every workgroup reads its 16*TM activation rows once per
 //     K phase into registers; TM is chosen per shape to minimise the bytes each CU
 //     must read (activations + its share of the weights).
@@ -604,12 +608,14 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
       // issue order = retirement order: the first subtile's weights, then the
       // activations, then the other PF subtiles of the chunk, so the first
       // MFMAs wait for the first subtile and the activations alone. Every load
-      // is unconditional (stages past the chunk read zero-length ranges, and the
-      // activations are reloaded per chunk from the cache) so that the compiler
-      // can count the loads in flight and wait for exactly the ones needed
+      // is unconditional (stages past the chunk read zero-length ranges, and a
+      // later chunk reloads the activations from the cache) so that the compiler
+      // can count the loads in flight and wait for exactly the ones needed. The
+      // tall tiles take one subtile per chunk, many chunks per workgroup: they
+      // load the activations once per phase (their waits are for whole chunks)
       W8Stage st[PF + 1];
       load(st[0], 0);
-      {
+      if (!kRegAcc || nph > 1 || cb == sb) {
         // activation operands of this wave's groups (groups past G read 0, so the
         // weights of those slots never matter) and the group sums of the
         // zero-point MFMA (lane (q, c): row c of the block, group gb + q)
@@ -911,7 +917,10 @@ hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipS
 }
 
 // Weight stage of one subtile: the lane's 16 bytes of the group's tile and, for
-// W4A16, its row's scale and zero-point; for MXFP4, the E8M0 byte of its block.
+// W4A16, its row's scale and the dword of zero-points holding its group's; for
+// MXFP4, the dword of E8M0 bytes holding its block's. Bytes are extracted where
+// they are used (a byte load's zero extension next to the load would make each
+// stage wait for its own load).
 struct B3Stage {
   uint4 w;
   float s;
@@ -973,23 +982,28 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
     for (int ph = 0; ph < nph; ph++) {
       const int g = ph * kW8Waves + wave;
       if (g >= G) continue;  // wave-uniform: this wave has no group in the last phase
+      // Each stage's address is one lane offset (shared by all stages) plus a
+      // workgroup-uniform scalar offset: per-stage vector addresses would be
+      // allocated to the registers of earlier stages' pending loads, which makes
+      // every stage wait for the previous one. Stages past the chunk reload its
+      // last subtile (in bounds; they fill LDS slots the reduction never reads).
       auto load = [&](B3Stage &st, int j) {
-        const int sj = cb + j;
-        const bool in = j < NS && sj < ce;  // past the chunk: zero-length reads
-        const uint32_t tile = (uint32_t)sj * G4 + g;
-        st.w = ld_b128(rw, in ? (tile * kWave + lane) * 16u : 0xFFFFFFF0u);
+        const uint32_t sj = (uint32_t)min(cb + j, ce - 1);
+        st.w = ld_b128(rw, (uint32_t)lane * 16u, (sj * G4 + g) * (kWave * 16u));
         if constexpr (F == F_W4A16) {
-          const uint32_t ge = (((uint32_t)sj * (G4 / 4) + g / 4) * 16 + c) * 4 + (g & 3);
-          st.s = ld_f32(rs, in ? ge * 4u : 0xFFFFFFF0u);
-          st.z = ld_u8(rz, in ? ge : 0xFFFFFFF0u) + zadd;
+          // entry ((sj G4/4 + g/4) 16 + c) 4 + g % 4 of the group data
+          const uint32_t gu = (sj * (G4 / 4) + g / 4) * 64u;
+          st.s = ld_f32(rs, (uint32_t)c * 16u, (gu + (g & 3)) * 4u);
+          st.z = ld_u32(rz, (uint32_t)c * 4u, gu);  // symmetric: a zero-length range reads 0
         } else {
           st.s = 0.0f;
-          st.z = ld_u8(rs, in ? tile * kWave + lane : 0xFFFFFFF0u);
+          st.z = ld_u32(rs, (uint32_t)(lane & ~3), (sj * G4 + g) * kWave);
         }
       };
       // issue order = retirement order: the first subtile's weights, then the
       // activations, then the other PF subtiles of the chunk (all unconditional:
-      // stages past the chunk read zero-length ranges, so the waits are exact)
+      // stages past the chunk read zero-length ranges, and a later chunk reloads
+      // the activations from the cache, so the waits are exact)
       B3Stage st[PF + 1];
       load(st[0], 0);
       {
@@ -1032,7 +1046,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
         v4u b[4];
         float fs;
         if constexpr (F == F_W4A16) {
-          const float zf = (float)(int)cur.z;
+          const float zf = (float)(int)(((cur.z >> (8 * (g & 3))) & 0xFFu) + (uint32_t)zadd);
           const uint32_t wd[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
 #pragma unroll
           for (int h = 0; h < 2; h++)  // u = h: low nibbles of bytes 8h .. 8h+7; u = 2 + h: high nibbles
@@ -1051,7 +1065,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
           // the MFMA sums the four blocks of group g of row c (lanes c, c+16, c+32,
           // c+48): each block's codes carry 2^(e - emax), exact in bf16 down to
           // 2^-126; the fp32 factor 2^(emax - 127) (NaN for 255) follows the MFMA
-          const int e = (int)cur.z;
+          const int e = (int)((cur.z >> (8 * (lane & 3))) & 0xFFu);
           int emax = max(e, __shfl_xor(e, 16));
           emax = max(emax, __shfl_xor(emax, 32));
           const int dexp = e - emax;
@@ -1104,23 +1118,11 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   }
 }
 
-// Subtiles per chunk (their partial tiles fill NS * TM * 8 KiB of LDS) and weight
-// subtiles in flight (PF + 1 stages of 6 registers).
-#ifndef XB3NS1
-#define XB3NS1 8
-#endif
-#ifndef XB3NS2
-#define XB3NS2 6
-#endif
-#ifndef XB3PF1
-#define XB3PF1 7
-#endif
-#ifndef XB3PF2
-#define XB3PF2 5
-#endif
+// Largest chunk (its partial tiles fill NS * TM * 8 KiB of LDS) and weight subtiles
+// in flight (PF + 1 stages of 6 registers) that compile without spills.
 template <int TM> struct B3Cfg {
-  static constexpr int NS = TM >= 2 ? XB3NS2 : XB3NS1;
-  static constexpr int PF = TM >= 2 ? XB3PF2 : XB3PF1;
+  static constexpr int NS = TM >= 2 ? 6 : 8;
+  static constexpr int PF = NS - 1;
 };
 
 template <int F, int TM>
