@@ -1,16 +1,18 @@
-// One decode token's attention for one query head, as device functions shared by
-// the one-token attention kernel (lb_model.hip) and the fused q/k/v GEMV +
-// attention kernel (lb_gemv.h): src/lowbit/model.py:353-378 for a single query at
-// absolute position p against the KV-cache keys 0 .. S-1, S = min(p + 1, cap),
-// where (when p < cap) key p is the new one, held in LDS and never read back from
-// the cache.
+// One decode token's attention for one query head, as device functions of the
+// one-token attention kernel (lb_model.hip): src/lowbit/model.py:353-378 for a
+// single query at absolute position p against the KV-cache keys 0 .. S-1,
+// S = min(p + 1, cap), where (when p < cap) key p is the new one, held in LDS and
+// never read back from the cache.
 //
-// NT threads (NT / 64 waves) per workgroup; keys are scored NT per chunk (one per
-// thread) with an online softmax across chunks; wave w accumulates p * v over keys
-// c0 + 64 w .. c0 + 64 w + 63 of a chunk, lane l owning output elements l, l + 64,
-// ...; the waves' partial sums are added in LDS at the end. The kernel memory
-// chain is short when the first chunk's key and value rows are prefetched into
-// registers before anything else (attn_prefetch, D <= 64).
+// Memory layout of the work: D / 4 lanes share a key (or value) row, each lane
+// holding one float4 of it, so a wave load covers RPL = 256 / D consecutive rows
+// (1 KiB contiguous). A wave takes KB = 16 RPL keys per round (16 key loads and 16
+// value loads per lane, all in flight together, within the 63 loads a wave can
+// have outstanding): the score of each key is a sum over its row's lanes, and
+// the lanes that hold a value row already hold that key's probability. Every
+// wave keeps its own online softmax (running max, sum and p * v) over rounds
+// of NW * KB keys; the waves are merged once at the end, in LDS. The first
+// round's rows are requested before the position is known (rows below cap).
 #pragma once
 
 #include <math.h>
@@ -21,171 +23,165 @@ namespace lbk {
 
 template <int D>
 struct AttnCfg {
-  static constexpr int kDPL = (D + kWave - 1) / kWave;  // output elements per lane
-  static constexpr bool kPre = D <= 64;                  // first chunk prefetched into registers
-  static constexpr int kVB = 16;                         // values in flight per lane past the first chunk
+  static constexpr int kLPR = D / 4;          // lanes per key row
+  static constexpr int kRPL = kWave / kLPR;   // key rows per wave load
+  static constexpr int kU = 16;               // key (and value) loads per lane and round
+  static constexpr int kKB = kU * kRPL;       // keys per wave and round
 };
 
-// Registers holding the first chunk's key row (one per thread) and value rows (64
-// per wave) of the workgroup's KV head.
+// Registers holding one round of a wave's key and value rows.
 template <int D>
-struct AttnPre {
-  float4 k[AttnCfg<D>::kPre ? D / 4 : 1];
-  float v[AttnCfg<D>::kPre ? kWave * AttnCfg<D>::kDPL : 1];
+struct AttnRound {
+  float4 k[AttnCfg<D>::kU];
+  float4 v[AttnCfg<D>::kU];
 };
 
-// LDS of attn_run for NT threads.
+// LDS of the final merge for NT threads.
 template <int D, int NT>
 struct AttnShared {
-  float pb[NT];                   // probabilities of the chunk's keys
-  float red[NT / kWave];          // per-wave chunk maxima
-  float part[NT / kWave][D];      // per-wave partial outputs
-  float lsw[NT / kWave];          // per-wave softmax sums
+  float part[NT / kWave][D];  // per-wave p * v sums
+  float mw[NT / kWave];       // per-wave running maxima
+  float lw[NT / kWave];       // per-wave softmax sums
 };
 
-// Issue the prefetch (rows clamped below cap, so every address is in the cache;
-// rows past the keys in use are loaded but never used). kb / vb: the KV head's
-// cache rows [cap][D].
-template <int D, int NT>
-__device__ __forceinline__ void attn_prefetch(AttnPre<D> &pre, const float *__restrict__ kb,
-                                              const float *__restrict__ vb, int cap) {
-  if constexpr (AttnCfg<D>::kPre) {
-    constexpr int DPL = AttnCfg<D>::kDPL;
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int l = (D >= kWave || lane < D) ? lane : 0;
-    const int t = tid < cap ? tid : cap - 1;
-    const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)t * D);
+// Sum over each group of LPR consecutive lanes (8, 16 or 32); every lane of the
+// group gets it.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_f<kDppQuad1032>(v, 0.0f);
+  v += dpp_f<kDppQuad2301>(v, 0.0f);
+  v += dpp_f<kDppRowHalfMirror>(v, 0.0f);  // 8-lane sums
+  if constexpr (LPR >= 16) v += dpp_f<kDppRowMirror>(v, 0.0f);
+  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+  return v;
+}
+
+// Sum over the lanes l, l + LPR, l + 2 LPR, ... (the same element of every row a
+// wave load covers); every lane gets its column's sum.
+template <int LPR>
+__device__ __forceinline__ float column_sum(float v) {
 #pragma unroll
-    for (int e = 0; e < D / 4; e++) pre.k[e] = kr[e];
+  for (int off = LPR; off < kWave; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Key and value rows of one round of this wave, starting at key k0; rows clamped
+// below cap, so every address is inside the cache (rows past the keys in use are
+// masked out of the softmax). kb / vb: the KV head's cache rows [cap][D].
+template <int D>
+__device__ __forceinline__ void attn_load_round(AttnRound<D> &rd, const float *__restrict__ kb,
+                                                const float *__restrict__ vb, int k0, int cap) {
+  constexpr int LPR = AttnCfg<D>::kLPR, RPL = AttnCfg<D>::kRPL, U = AttnCfg<D>::kU;
+  const int lane = threadIdx.x & (kWave - 1), r = lane / LPR, e4 = lane % LPR;
 #pragma unroll
-    for (int u = 0; u < kWave; u++) {
-      const int row = wave * kWave + u < cap ? wave * kWave + u : cap - 1;
+  for (int u = 0; u < U; u++) {
+    int row = k0 + RPL * u + r;
+    row = row < cap ? row : cap - 1;
+    rd.k[u] = reinterpret_cast<const float4 *>(kb + (size_t)row * D)[e4];
+  }
 #pragma unroll
-      for (int q = 0; q < DPL; q++) pre.v[u * DPL + q] = vb[(size_t)row * D + l + kWave * q];
-    }
+  for (int u = 0; u < U; u++) {
+    int row = k0 + RPL * u + r;
+    row = row < cap ? row : cap - 1;
+    rd.v[u] = reinterpret_cast<const float4 *>(vb + (size_t)row * D)[e4];
   }
 }
 
-// Attention of the rotated query qs[D] (LDS) over keys 0 .. S-1: keys below Sc from
-// the cache rows kb / vb, key Sc (when newk) from kn / vn (LDS). Writes out[0 .. D).
-// Every thread of the workgroup calls it (it has barriers); the LDS in qs, kn, vn
-// must be visible to all threads on entry.
+// The first round of this wave (keys KB * wave ...), issued by the caller before
+// anything else.
 template <int D, int NT>
-__device__ __forceinline__ void attn_run(const AttnPre<D> &pre, const float *qs, const float *kn, const float *vn,
-                                         const float *__restrict__ kb, const float *__restrict__ vb, int S,
-                                         int Sc, bool newk, AttnShared<D, NT> &sh, float *__restrict__ out) {
-  constexpr int DPL = AttnCfg<D>::kDPL, NK4 = D / 4, NW = NT / kWave, VB = AttnCfg<D>::kVB;
-  constexpr bool kPre = AttnCfg<D>::kPre;
-  static_assert(NT % kWave == 0 && NT >= kWave, "whole waves");
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+__device__ __forceinline__ void attn_prefetch(AttnRound<D> &rd, const float *__restrict__ kb,
+                                              const float *__restrict__ vb, int cap) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  attn_load_round<D>(rd, kb, vb, AttnCfg<D>::kKB * wave, cap);
+}
+
+// Attention of the rotated query qs[D] (LDS) over keys 0 .. S-1: keys other than
+// Sc from the cache rows kb / vb, key Sc (when newk) from kn / vn (LDS). `first`
+// holds the wave's first round (attn_prefetch). Writes out[0 .. D). Every thread
+// of the workgroup calls it (one barrier, at the merge); qs, kn, vn must be
+// visible to all threads on entry.
+template <int D, int NT>
+__device__ __forceinline__ void attn_run(const AttnRound<D> &first, const float *qs, const float *kn,
+                                         const float *vn, const float *__restrict__ kb,
+                                         const float *__restrict__ vb, int S, int Sc, bool newk, int cap,
+                                         AttnShared<D, NT> &sh, float *__restrict__ out) {
+  constexpr int LPR = AttnCfg<D>::kLPR, RPL = AttnCfg<D>::kRPL, U = AttnCfg<D>::kU, KB = AttnCfg<D>::kKB;
+  constexpr int NW = NT / kWave;
+  static_assert(NT % kWave == 0, "whole waves");
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), r = lane / LPR, e4 = lane % LPR;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const bool own = D >= kWave || lane < D;  // D = 32: lanes 32..63 hold no output
-  const int l = own ? lane : 0;
   const float scale = 1.0f / sqrtf((float)D);
-  float acc[DPL], lsum = 0.0f, mrun = -INFINITY;
+  const float4 q4 = reinterpret_cast<const float4 *>(qs)[e4];
+  const float4 kn4 = reinterpret_cast<const float4 *>(kn)[e4];
+  const float4 vn4 = reinterpret_cast<const float4 *>(vn)[e4];
+  float m = -INFINITY, l = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  AttnRound<D> rd = first;
+  for (int c0 = 0; c0 < S; c0 += NW * KB) {
+    const int k0 = c0 + KB * wave;
+    if (c0 > 0) attn_load_round<D>(rd, kb, vb, k0, cap);
+    if (k0 >= S) continue;  // wave-uniform: no key of this round for this wave
+    // ---- scores of the round's keys (each in all lanes of its row)
+    float sc[U];
+    float mx = -INFINITY;
 #pragma unroll
-  for (int q = 0; q < DPL; q++) acc[q] = 0.0f;
-
-  for (int c0 = 0; c0 < S; c0 += NT) {
-    const bool pre_chunk = kPre && c0 == 0;
-    // ---- score of key c0 + tid
-    const int s = c0 + tid;
-    float d = 0.0f;
-    if (s < S) {
-      float4 kv[NK4];
-      if (s >= Sc) {
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = reinterpret_cast<const float4 *>(kn)[e];
-      } else if (pre_chunk) {
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = pre.k[kPre ? e : 0];
-      } else {
-        const float4 *kr = reinterpret_cast<const float4 *>(kb + (size_t)s * D);
-#pragma unroll
-        for (int e = 0; e < NK4; e++) kv[e] = kr[e];
-      }
-#pragma unroll
-      for (int e = 0; e < NK4; e++) {
-        const float4 qv = reinterpret_cast<const float4 *>(qs)[e];
-        d = __builtin_fmaf(qv.x, kv[e].x, d);
-        d = __builtin_fmaf(qv.y, kv[e].y, d);
-        d = __builtin_fmaf(qv.z, kv[e].z, d);
-        d = __builtin_fmaf(qv.w, kv[e].w, d);
-      }
+    for (int u = 0; u < U; u++) {
+      const int row = k0 + RPL * u + r;
+      const float4 kk = (newk && row == Sc) ? kn4 : rd.k[u];
+      float d = q4.x * kk.x;
+      d = __builtin_fmaf(q4.y, kk.y, d);
+      d = __builtin_fmaf(q4.z, kk.z, d);
+      d = __builtin_fmaf(q4.w, kk.w, d);
+      d = group_sum<LPR>(d) * scale;
+      sc[u] = row < S ? d : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
     }
-    d = s < S ? d * scale : -INFINITY;
-    const float mw = wave_max(d);
-    if (lane == 0) sh.red[wave] = mw;
-    __syncthreads();
-    // ---- running maximum, probabilities of this chunk, rescaled accumulators
-    float cm = sh.red[0];
+    // ---- running maximum (the round has a key below S: row k0), rescale, p * v
+    const float mnew = fmaxf(m, wave_max(mx));
+    const float alpha = expf(m - mnew);  // 0 on the wave's first round
+    m = mnew;
+    l *= alpha;
+    acc.x *= alpha;
+    acc.y *= alpha;
+    acc.z *= alpha;
+    acc.w *= alpha;
 #pragma unroll
-    for (int w = 1; w < NW; w++) cm = fmaxf(cm, sh.red[w]);
-    const float mnew = fmaxf(mrun, cm);
-    const float alpha = expf(mrun - mnew);  // 0 on the first chunk
-    mrun = mnew;
-    lsum *= alpha;
-#pragma unroll
-    for (int q = 0; q < DPL; q++) acc[q] *= alpha;
-    sh.pb[tid] = s < S ? expf(d - mnew) : 0.0f;
-    __syncthreads();
-    // ---- wave w: p * v over keys c0 + 64 w .. c0 + 64 w + 63; the new key's
-    //      value from LDS
-    const int sb = c0 + wave * kWave;
-    const int se = sb + kWave < S ? sb + kWave : S;
-    const int sce = se < Sc ? se : Sc;
-    if (pre_chunk) {
-#pragma unroll
-      for (int u = 0; u < kWave; u++) {
-        if (sb + u < sce) {
-          const float pr = sh.pb[sb + u - c0];
-          lsum += pr;
-#pragma unroll
-          for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, pre.v[kPre ? u * DPL + q : 0], acc[q]);
-        }
-      }
-    } else {
-      for (int k0 = sb; k0 < sce; k0 += VB) {
-        float v[VB][DPL];
-#pragma unroll
-        for (int u = 0; u < VB; u++) {
-          const int k = k0 + u < sce ? k0 + u : sce - 1;  // in-range row; its weight is dropped below
-#pragma unroll
-          for (int q = 0; q < DPL; q++) v[u][q] = vb[(size_t)k * D + l + kWave * q];
-        }
-#pragma unroll
-        for (int u = 0; u < VB; u++) {
-          if (k0 + u < sce) {
-            const float pr = sh.pb[k0 + u - c0];
-            lsum += pr;
-#pragma unroll
-            for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, v[u][q], acc[q]);
-          }
-        }
-      }
+    for (int u = 0; u < U; u++) {
+      const int row = k0 + RPL * u + r;
+      const float pr = expf(sc[u] - m);  // 0 for masked keys
+      // masked rows (past the keys in use) may hold anything, NaN included: 0 * NaN
+      // would poison the sum, so their values are replaced, not just weighted by 0
+      const float4 vv = row < S ? ((newk && row == Sc) ? vn4 : rd.v[u]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      l += pr;
+      acc.x = __builtin_fmaf(pr, vv.x, acc.x);
+      acc.y = __builtin_fmaf(pr, vv.y, acc.y);
+      acc.z = __builtin_fmaf(pr, vv.z, acc.z);
+      acc.w = __builtin_fmaf(pr, vv.w, acc.w);
     }
-    if (newk && Sc >= sb && Sc < se) {
-      const float pr = sh.pb[Sc - c0];
-      lsum += pr;
-#pragma unroll
-      for (int q = 0; q < DPL; q++) acc[q] = __builtin_fmaf(pr, vn[l + kWave * q], acc[q]);
-    }
-    __syncthreads();  // pb is rewritten by the next chunk
   }
-
-  // ---- add the waves' partial sums
-  if (own) {
-#pragma unroll
-    for (int q = 0; q < DPL; q++) sh.part[wave][l + kWave * q] = acc[q];
+  // ---- the wave's sums over its rows, then the waves merged in LDS
+  acc.x = column_sum<LPR>(acc.x);
+  acc.y = column_sum<LPR>(acc.y);
+  acc.z = column_sum<LPR>(acc.z);
+  acc.w = column_sum<LPR>(acc.w);
+  l = column_sum<LPR>(l);  // each row's sum is held by all its lanes
+  if (lane < LPR) *reinterpret_cast<float4 *>(&sh.part[wave][4 * lane]) = acc;
+  if (lane == 0) {
+    sh.mw[wave] = m;
+    sh.lw[wave] = l;
   }
-  if (lane == 0) sh.lsw[wave] = lsum;
   __syncthreads();
+  float M = sh.mw[0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) M = fmaxf(M, sh.mw[w]);
   for (int e = tid; e < D; e += NT) {
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-      num += sh.part[w][e];
-      den += sh.lsw[w];
+      const float f = expf(sh.mw[w] - M);  // 0 for a wave that saw no key
+      num = __builtin_fmaf(sh.part[w][e], f, num);
+      den = __builtin_fmaf(sh.lw[w], f, den);
     }
     out[e] = num / den;
   }

@@ -163,17 +163,15 @@ __global__ __launch_bounds__(kWave) void attention_kernel(const float *__restric
 // epilogue) sits in qkv [(H + 2 KV) D] at absolute position p = *pos. One workgroup
 // per query head h (grid KV x H/KV; KV head g = h / (H/KV)). The step is a chain
 // of memory round trips, so the kernel is laid out to need as few as possible:
-//   0. before anything else (and before *pos arrives) thread t loads key row t and
-//      wave w the value rows 64 w .. 64 w + 63 of the first chunk into registers
-//      (rows below cap; D <= 64);
+//   0. before anything else (and before *pos arrives) each wave requests its first
+//      round of key and value rows (coalesced float4 rows, lb_attn.h; rows below
+//      cap);
 //   1. rotate the query head and the key ("rotate_half", src/lowbit/model.py:
 //      201-210) into LDS; the group's first workgroup writes the rotated key and
 //      the value to the caches at p (when p < cap);
-//   2. over chunks of kAttThreads keys (online softmax, src/lowbit/model.py:353-378):
-//      thread t scores key c0 + t, the chunk maximum updates the running maximum,
-//      and wave w accumulates p * v over its 64 keys, lane l owning output
-//      elements l, l + 64, ...;
-//   3. the waves' partial sums are added in LDS and divided by the softmax sum.
+//   2. every wave runs an online softmax over its keys of each round
+//      (src/lowbit/model.py:353-378), with no barrier;
+//   3. the waves' (max, sum, p * v) are merged in LDS and divided by the sum.
 // Keys 0 .. S-1 with S = min(p + 1, cap) take part; when p < cap key p is the new
 // one (from LDS, never read back from the cache), otherwise all S come from the
 // cache, as lbd_qkv_rope + lbd_attention behave. Output out [H D].
@@ -187,15 +185,15 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   constexpr int half = D / 2;
   __shared__ __align__(16) float qs[D];
   __shared__ __align__(16) float kn[D];
-  __shared__ float vn[D];
+  __shared__ __align__(16) float vn[D];
   __shared__ AttnShared<D, kAttThreads> sh;
   const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
   const int tid = threadIdx.x;
   const float *kb = kc + (size_t)g * cap * D;
   const float *vb = vc + (size_t)g * cap * D;
 
-  // ---- 0. prefetch of the first chunk's keys and values
-  AttnPre<D> pre;
+  // ---- 0. the first round of keys and values, requested before anything else
+  AttnRound<D> pre;
   attn_prefetch<D, kAttThreads>(pre, kb, vb, cap);
 
   const int p = *pos;
@@ -231,8 +229,8 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   }
   __syncthreads();
 
-  // ---- 2, 3. online softmax over chunks of kAttThreads keys; the waves' sums
-  attn_run<D, kAttThreads>(pre, qs, kn, vn, kb, vb, S, Sc, newk, sh, out + (size_t)h * D);
+  // ---- 2, 3. per-wave online softmax over rounds of keys; the waves merged
+  attn_run<D, kAttThreads>(pre, qs, kn, vn, kb, vb, S, Sc, newk, cap, sh, out + (size_t)h * D);
 }
 
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
