@@ -1121,7 +1121,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
 // Largest chunk (its partial tiles fill NS * TM * 8 KiB of LDS) and weight subtiles
 // in flight (PF + 1 stages of 6 registers) that compile without spills.
 template <int TM> struct B3Cfg {
-  static constexpr int NS = TM >= 2 ? 6 : 8;
+  static constexpr int NS = TM >= 2 ? 6 : 12;
   static constexpr int PF = NS - 1;
 };
 
@@ -1144,6 +1144,9 @@ static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
     case 3: go(std::integral_constant<int, 3>{}); break;
     case 4: go(std::integral_constant<int, 4>{}); break;
     case 5: go(std::integral_constant<int, 5>{}); break;
+    case 6: go(std::integral_constant<int, 6>{}); break;
+    case 7:
+    case 8: go(std::integral_constant<int, 8>{}); break;
     default: go(std::integral_constant<int, NS>{}); break;
   }
 }
@@ -1151,11 +1154,23 @@ static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
   const int cus = num_cus > 0 ? num_cus : 256;
   if (!a.x3 || !a.wt16) return hipErrorInvalidValue;
-  // 32-row blocks halve the weight decode per output once there are two row blocks
-  // (the kernel is bound by the decode and MFMA issue, not by reloading the
-  // activations per chunk: 16-row blocks with one chunk per workgroup, which read
-  // 40 % fewer bytes, ran slower)
-  const bool tall = a.M > 16;
+  // W4A16: 32-row blocks halve the weight decode per output once there are two
+  // row blocks (its decode VALU, not bytes, bounds it). MXFP4 decodes with a few
+  // conversion instructions, and each CU's bytes matter more: the activation terms
+  // (6 B per element of its 16 TM rows) plus its share of the weights, the
+  // smaller of TM = 1 and 2 once it saves a quarter (16-row blocks, which decode
+  // each weight twice as often, win at N = 4096 and K = 11008, saving ~38 %, and
+  // lose slightly at M = 64 x 11008 x 4096, saving 21 %).
+  bool tall = a.M > 16;
+  if (fmt == F_MXFP4 && tall) {
+    auto cu_bytes = [&](int tm) {
+      const int gy = (a.M + 16 * tm - 1) / (16 * tm), S = (a.N + 15) / 16;
+      const int gx = std::max(1, std::min(S, cus / gy));
+      const double spw = (double)((S + gx - 1) / gx);
+      return (double)tm * 16 * a.Kp * 6 + spw * 16 * (a.Kp / 2 + a.Kp / 32);
+    };
+    tall = cu_bytes(1) > 0.75 * cu_bytes(2);
+  }
   if (fmt == F_W4A16) {
     if (tall) launch_bf3_t<F_W4A16, 2>(a, cus, s);
     else launch_bf3_t<F_W4A16, 1>(a, cus, s);
