@@ -241,3 +241,46 @@ def test_prefill_m_within_bound(rng, m, n, k):
     bound = cref.c_gemm_mxfp4(xp, Wm.qw, Wm.e8m0, absval=True)
     for y in (K.gemm_mxfp4(x, lb.to_device(Wm)), K.gemm_mxfp4(x, Wm)):
         O.assert_fp_close(y, ref, bound, 1e-5)
+
+
+# ---------------------------------------------------------------- launch variants
+
+# Subtiles (16 weight rows) per workgroup pick the compiled chunk length and the
+# number of weight stages in flight (1, 2, 3, 4, 5, 6, 8, the largest, and more
+# than one chunk per workgroup, whose last chunk is short). With 256 compute units
+# a 16-row activation block spreads S = N / 16 subtiles over 256 workgroups, a
+# 64-row block over 128 (32-row tiles) or 64 (16-row tiles).
+SHARES = [1, 2, 3, 4, 5, 6, 8, 12, 14]
+
+
+@pytest.mark.parametrize("share", SHARES)
+@pytest.mark.parametrize("fmt", ["w4a8", "w4a16", "mxfp4"])
+@pytest.mark.parametrize("m", [16, 64])
+def test_batch_kernels_every_share_of_subtiles(rng, fmt, m, share):
+    """Each compiled variant of the batch kernels (chunk length, stages in flight,
+    multi-chunk workgroups) against the float64 oracle within the reference's
+    bound (the counts assume 256 compute units; on another part the same shapes
+    still check correctness)."""
+    n = 16 * (256 if m == 16 else 128) * share  # M = 64: 2 row blocks x 128 workgroups
+    kp = 1152 if share == 5 else 256  # one share with two K phases of the bf16x3 kernel
+    x = rng.standard_normal((m, kp)).astype(np.float32)
+    if fmt == "mxfp4":
+        W = lb.quantize_mxfp4(_lognormal_rows(rng, n, kp))
+        D = lb.to_device(W)
+        y = K.gemm_mxfp4(x, D, isa="gfx950-mfma")
+        ref = cref.c_gemm_mxfp4(x, W.qw, W.e8m0)
+        bound = cref.c_gemm_mxfp4(x, W.qw, W.e8m0, absval=True)
+    elif fmt == "w4a16":
+        W = lb.quantize_int4(_lognormal_rows(rng, n, kp), asym=True)
+        D = lb.to_device(W)
+        y = K.gemm_w4a16(x, D, isa="gfx950-mfma")
+        ref = cref.c_gemm_w4a16(x, W.qw, W.scales, W.zeros)
+        bound = cref.c_gemm_w4a16(x, W.qw, W.scales, W.zeros, absval=True)
+    else:
+        W = _random_int4(rng, n, kp, True)
+        D = lb.to_device(W)
+        y = K.gemm_w4a8(x, D, isa="gfx950-mfma")
+        a = lb.quantize_act_int8(x)
+        ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+    assert K.last_path() == "gfx950-mfma" and D.t16 is not None
+    O.assert_fp_close(y, ref, bound, 1e-5)
