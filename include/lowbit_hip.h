@@ -265,6 +265,9 @@ int lbd_attention(const float *q, int qstride, const float *k_cache,
                   int cap, float *out, void *stream);
 /* out [T, I] = silu(gu[:, :I]) * gu[:, I:] (model.py:213, 416-417) */
 int lbd_swiglu(const float *gu, int T, int I, float *out, void *stream);
+/* out [T, I] = silu(gu[:, 2i]) * gu[:, 2i + 1]: the same operation on gate/up rows
+ * stored in pairs (the layout the glu epilogue of the fused GEMVs consumes) */
+int lbd_swiglu_pairs(const float *gu, int T, int I, float *out, void *stream);
 /* x += y over n floats (the residual adds) */
 int lbd_add(float *x, const float *y, size_t n, void *stream);
 /* tok[0] = numpy's argmax of v[0..n) (the first NaN if any, else the first maximum);
@@ -299,6 +302,12 @@ typedef struct {
    * else first maximum); the slots must be 0 before the call (lbd_argmax_finalize
    * reads the index and clears them). 8-byte aligned device memory. */
   unsigned long long *argmax_key;
+  /* glu != 0: the weight rows come in pairs (row 2p the gate, row 2p + 1 the up
+   * projection of output p; N even) and y [M, N/2] receives y[m, p] = silu(g) * u of
+   * the pair's outputs g, u (bias added; model.py:213), computed once per output in
+   * the epilogue instead of once per workgroup in the next GEMV's SwiGLU prologue.
+   * Excludes residual and argmax_key. */
+  int glu;
 } lbd_fusion;
 #define LBD_ARGMAX_SLOTS 1024
 int lbd_gemv_w4a16_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,

@@ -657,6 +657,13 @@ int lbd_swiglu(const float *gu, int T, int I, float *out, void *stream) {
   LB_LAUNCH(lbk::launch_swiglu(gu, T, I, out, static_cast<hipStream_t>(stream)), "swiglu launch");
 }
 
+int lbd_swiglu_pairs(const float *gu, int T, int I, float *out, void *stream) {
+  if (T <= 0 || I <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!gu || !out) return fail(LB_ERR_ARG, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(gu) & 7) != 0) return fail(LB_ERR_ARG, "gu must be 8-byte aligned");
+  LB_LAUNCH(lbk::launch_swiglu_pairs(gu, T, I, out, static_cast<hipStream_t>(stream)), "swiglu launch");
+}
+
 int lbd_add(float *x, const float *y, size_t n, void *stream) {
   if (!x || !y) return fail(LB_ERR_ARG, "null pointer");
   if (n == 0) return ok(0);
@@ -689,12 +696,16 @@ int fused_args(int fmt, const lbd_fusion *f, lbk::GemmArgs &a) {
   if (f->norm_w && !aligned16(f->norm_w)) return fail(LB_ERR_ARG, "norm_w must be 16-byte aligned");
   if (f->argmax_key && (reinterpret_cast<uintptr_t>(f->argmax_key) & 7) != 0)
     return fail(LB_ERR_ARG, "argmax_key must be 8-byte aligned");
+  if (f->glu && (f->residual || f->argmax_key))
+    return fail(LB_ERR_ARG, "the glu epilogue excludes the residual and the argmax key");
+  if (f->glu && (a.N & 1)) return fail(LB_ERR_SHAPE, "the glu epilogue takes an even N (gate/up row pairs)");
   a.norm_w = f->norm_w;
   a.norm_eps = f->norm_eps;
   a.swiglu = f->swiglu != 0;
   a.bias = f->bias;
   a.res = f->residual;
   a.amax_key = f->argmax_key;
+  a.glu = f->glu != 0;
   return 0;
 }
 

@@ -241,7 +241,8 @@ struct GemvMinWaves {
 // PRO selects a fused prologue on the (single, register-held) activation row:
 // 0 none, 1 RMSNorm (x * (1 / sqrt(mean(x^2) + eps)) * norm_w, the mean over Kp),
 // 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
-// adds `bias` and `res` when given and max-combines argmax keys into `amax_key`.
+// adds `bias` and `res` when given and max-combines argmax keys into `amax_key`;
+// under `glu` it writes silu(gate) * up of each (gate, up) row pair instead.
 template <int F, int MB, int R, int NIT, int PRO>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(GemvMinWaves<F, MB, PRO>::value)))
 void gemv_kernel(GemmArgs a) {
@@ -258,9 +259,11 @@ void gemv_kernel(GemmArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int gw = blockIdx.x * kGemvWaves + wave, W = gridDim.x * kGemvWaves;
-  // wave gw takes rows [r0, r1): N / W each, one more for the first N % W waves
-  const int rbase = (int)((unsigned)N / (unsigned)W), rrem = N - rbase * W;
-  const int r0 = gw * rbase + min(gw, rrem), r1 = r0 + rbase + (gw < rrem ? 1 : 0);
+  // wave gw takes rows [r0, r1): NU / W units of u rows each (u = 2 under the glu
+  // epilogue, whose gate/up pairs must share a wave), one more for the first NU % W waves
+  const int u = a.glu ? 2 : 1, NU = a.glu ? N >> 1 : N;
+  const int ubase = (int)((unsigned)NU / (unsigned)W), urem = NU - ubase * W;
+  const int r0 = u * (gw * ubase + min(gw, urem)), r1 = r0 + u * (ubase + (gw < urem ? 1 : 0));
 
   float *xl = reinterpret_cast<float *>(lds);                           // fp32 planes [MB][8][nchp][4]
   uint8_t *ql = lds;                                                      // int8 planes [MB][2][nchp][16]
@@ -437,6 +440,9 @@ void gemv_kernel(GemmArgs a) {
   // ---- 4. decode + accumulate R rows at a time; later batches load as the
   //         previous one finishes
   unsigned long long best = 0;  // argmax key of this wave's outputs
+  float tg[MB];                 // glu: the gate output of the pair in progress (rows in order)
+#pragma unroll
+  for (int m = 0; m < MB; m++) tg[m] = 0.0f;
   for (int rb = r0; rb < r1; rb += R) {
     if (rb != r0) {
       gemv_load<F, R, NIT>(a, g, rb, r1, lane, nch, G);
@@ -458,7 +464,7 @@ void gemv_kernel(GemmArgs a) {
         if (r >= nr) break;
         float t = wave_sum(acc[m][r]);
         const int n = rb + r;
-        const size_t o = (size_t)m * N + n;
+        size_t o = (size_t)m * N + n;
         {
           // y is rounded before the bias and the residual are added, as separate
           // float32 adds after the GEMM would round it (no fused multiply-add)
@@ -466,6 +472,15 @@ void gemv_kernel(GemmArgs a) {
           if constexpr (kInt8) t *= xsl[m];
           if (a.bias) t += bv[r];
           if (a.res) t = rv[m][r] + t;
+        }
+        if (a.glu) {
+          // wave-uniform: r0 is even, so even rows are gates and the next row is their up
+          if ((n & 1) == 0) {
+            tg[m] = t;
+            continue;
+          }
+          t = tg[m] / (1.0f + expf(-tg[m])) * t;  // the SwiGLU kernel's expression
+          o = (size_t)m * (N >> 1) + (n >> 1);
         }
         if (lane == m * R + r) a.y[o] = t;
         if (a.amax_key) {
@@ -510,7 +525,7 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
   int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
   grid = grid < 2 * cus ? grid : 2 * cus;
   const int waves = grid * kGemvWaves;
-  const int rpw = (a.N + waves - 1) / waves;
+  const int rpw = a.glu ? 2 * ((a.N / 2 + waves - 1) / waves) : (a.N + waves - 1) / waves;
   if (nit <= 1) return launch_gemv_nit<F, MB, 1, PRO>(a, grid, rpw, lds, s);
   if (nit <= 2) return launch_gemv_nit<F, MB, 2, PRO>(a, grid, rpw, lds, s);
   if (nit <= 4) return launch_gemv_nit<F, MB, 4, PRO>(a, grid, rpw, lds, s);

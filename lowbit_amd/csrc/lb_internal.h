@@ -39,6 +39,7 @@ struct GemmArgs {
   const float *bias = nullptr;    // [N]
   const float *res = nullptr;     // [M, N]
   unsigned long long *amax_key = nullptr;  // M == 1: kArgmaxSlots argmax keys of the y row, max-combined
+  bool glu = false;               // rows in (gate, up) pairs; y [M, N/2] = silu(gate) * up of each pair
 };
 
 // Argmax keys are max-combined into this many slots (global wave index modulo the
@@ -115,6 +116,7 @@ hipError_t launch_qkv_rope(float *qkv, const float *bias, int T, int H, int KV, 
 hipError_t launch_attention(const float *q, int qstride, const float *kc, const float *vc, int T, int H, int KV, int D,
                             const int32_t *pos, int cap, float *out, hipStream_t s);
 hipError_t launch_swiglu(const float *gu, int T, int I, float *out, hipStream_t s);
+hipError_t launch_swiglu_pairs(const float *gu, int T, int I, float *out, hipStream_t s);
 hipError_t launch_add(float *x, const float *y, size_t n, hipStream_t s);
 hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int inc, int32_t *hist, int hist_len,
                          hipStream_t s);

@@ -281,6 +281,15 @@ __global__ __launch_bounds__(kMT) void swiglu_kernel(const float *__restrict__ g
   }
 }
 
+// out[t, i] = silu(gu[t, 2i]) * gu[t, 2i + 1]: gate and up interleaved by output.
+__global__ __launch_bounds__(kMT) void swiglu_pairs_kernel(const float *__restrict__ gu, size_t n,
+                                                            float *__restrict__ out) {
+  for (size_t e = (size_t)blockIdx.x * kMT + threadIdx.x; e < n; e += (size_t)gridDim.x * kMT) {
+    const float2 p = reinterpret_cast<const float2 *>(gu)[e];
+    out[e] = p.x / (1.0f + expf(-p.x)) * p.y;
+  }
+}
+
 __global__ __launch_bounds__(kMT) void add_kernel(float *__restrict__ x, const float *__restrict__ y, size_t n) {
   for (size_t e = (size_t)blockIdx.x * kMT + threadIdx.x; e < n; e += (size_t)gridDim.x * kMT) x[e] += y[e];
 }
@@ -375,6 +384,12 @@ hipError_t launch_attention(const float *q, int qstride, const float *kc, const 
 
 hipError_t launch_swiglu(const float *gu, int T, int I, float *out, hipStream_t s) {
   hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((size_t)T * I)), dim3(kMT), 0, s, gu, T, I, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_pairs(const float *gu, int T, int I, float *out, hipStream_t s) {
+  const size_t n = (size_t)T * I;
+  hipLaunchKernelGGL(swiglu_pairs_kernel, dim3(grid_for(n)), dim3(kMT), 0, s, gu, n, out);
   return hipGetLastError();
 }
 

@@ -128,6 +128,7 @@ SIGNATURES = {
     "lbd_qkv_rope": ([_vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp], _int),
     "lbd_attention": ([_vp, _int, _vp, _vp, _int, _int, _int, _int, _vp, _int, _vp, _vp], _int),
     "lbd_swiglu": ([_vp, _int, _int, _vp, _vp], _int),
+    "lbd_swiglu_pairs": ([_vp, _int, _int, _vp, _vp], _int),
     "lbd_add": ([_vp, _vp, _sz, _vp], _int),
     "lbd_argmax": ([_vp, _int, _vp, _vp, _int, _vp, _int, _vp], _int),
     "lbd_gemv_w4a16_fused": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
@@ -145,7 +146,8 @@ class LbdFusion(C.Structure):
     """lbd_fusion of include/lowbit_hip.h: the prologue / epilogue of a fused GEMV
     (pass C.byref(f) as the `f` argument)."""
     _fields_ = [("norm_w", C.c_void_p), ("norm_eps", C.c_float), ("swiglu", C.c_int),
-                ("bias", C.c_void_p), ("residual", C.c_void_p), ("argmax_key", C.c_void_p)]
+                ("bias", C.c_void_p), ("residual", C.c_void_p), ("argmax_key", C.c_void_p),
+                ("glu", C.c_int)]
 
 
 @lru_cache(maxsize=1)

@@ -15,16 +15,18 @@ of launches: `generate` records it once as a HIP graph and replays it per token.
 
 A one-token step (fused=True, the default) runs five launches per layer: each
 linear layer is one fused GEMV (`lbd_gemv_*_fused`) whose prologue applies the
-RMSNorm (q/k/v, gate/up, LM head) or the SwiGLU (down) to its activation row and
-whose epilogue adds the q/k/v bias or the residual in place; the rotary embedding
+RMSNorm (q/k/v, gate/up, LM head) to its activation row and whose epilogue adds
+the q/k/v bias or the residual in place, or (gate/up) writes the SwiGLU of each
+gate/up output pair, so the down projection reads its activations ready-made;
+the rotary embedding
 and the KV-cache write run inside the one-token attention
 (`lbd_attention_decode`); the LM head's epilogue folds the greedy argmax into a
 64-bit key that `lbd_argmax_finalize` turns into the next token. Prompts (T > 1)
 run the unfused sequence on the matrix-core GEMMs.
 
 Same architecture and arithmetic as the reference model: RMSNorm in fp32, q/k/v
-and gate/up projections concatenated along N (quantization is per output row,
-so no quantized value changes), rotary embedding in the "rotate_half"
+projections concatenated along N and gate/up rows interleaved in (gate i, up i)
+pairs (quantization is per output row, so no quantized value changes), rotary embedding in the "rotate_half"
 convention from float32 cos/sin tables built in float64, grouped-query causal
 attention with a KV cache, SwiGLU MLP, tied or untied LM head (quantized like
 the other linears). Norm weights, biases, the embedding table and the KV cache
@@ -203,7 +205,9 @@ class Model:
             wqkv = np.concatenate([g(a + "q_proj.weight"), g(a + "k_proj.weight"), g(a + "v_proj.weight")], 0)
             bqkv = (np.concatenate([g(a + "q_proj.bias"), g(a + "k_proj.bias"), g(a + "v_proj.bias")])
                     if cfg.qkv_bias else None)
-            wgu = np.concatenate([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
+            # row 2i: gate i, row 2i + 1: up i (the pairs of the glu epilogue)
+            wgu = np.stack([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 1).reshape(
+                2 * cfg.intermediate_size, -1)
             self.layers.append(_Layer(up(g(p + "input_layernorm.weight")), lin(wqkv),
                                       None if bqkv is None else up(bqkv), lin(g(a + "o_proj.weight")),
                                       up(g(p + "post_attention_layernorm.weight")), lin(wgu),
@@ -283,11 +287,12 @@ class Model:
                                      ws.nbytes, s)
         _check(rc, f"{self.backend} linear")
 
-    def _fused_linear(self, w, x: int, y: int, norm: int | None = None, swiglu: bool = False,
+    def _fused_linear(self, w, x: int, y: int, norm: int | None = None, glu: bool = False,
                       bias: int | None = None, res: int | None = None, key: int | None = None):
         """y[0, n] = res[n] + (act(x) . w^T)[n] + bias[n] for one token, one launch;
-        act is the RMSNorm with weights `norm` or the SwiGLU of x = [gate | up]."""
-        f = K.LbdFusion(norm, self.cfg.rms_norm_eps if norm else 0.0, int(swiglu), bias, res, key)
+        act is the RMSNorm with weights `norm` (or the identity). With glu the rows
+        of w are (gate, up) pairs and y[0, p] = silu(gate) * up of pair p."""
+        f = K.LbdFusion(norm, self.cfg.rms_norm_eps if norm else 0.0, 0, bias, res, key, int(glu))
         L, s = self.L, self.stream
         if self.backend == "mxfp4":
             rc = L.lbd_gemv_mxfp4_fused(x, 1, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, y, C.byref(f), s)
@@ -311,8 +316,8 @@ class Model:
                                           cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
                                           self.att.ptr, s), "attention decode")
             self._fused_linear(ly.o, self.att.ptr, x, res=x)
-            self._fused_linear(ly.gate_up, x, self.gu.ptr, norm=ly.ln2.ptr)
-            self._fused_linear(ly.down, self.gu.ptr, x, swiglu=True, res=x)
+            self._fused_linear(ly.gate_up, x, self.m.ptr, norm=ly.ln2.ptr, glu=True)
+            self._fused_linear(ly.down, self.m.ptr, x, res=x)
         if logits == "none":
             _check(L.lbd_rmsnorm(x, self.norm.ptr, 1, h, cfg.rms_norm_eps, self.h.ptr, s), "rmsnorm")
         elif logits == "last":
@@ -346,7 +351,7 @@ class Model:
             _check(L.lbd_add(self.x.ptr, self.o.ptr, T * h, s), "add")
             _check(L.lbd_rmsnorm(self.x.ptr, ly.ln2.ptr, T, h, cfg.rms_norm_eps, self.h.ptr, s), "rmsnorm")
             self._linear(ly.gate_up, self.h.ptr, T, self.gu.ptr)
-            _check(L.lbd_swiglu(self.gu.ptr, T, I, self.m.ptr, s), "swiglu")
+            _check(L.lbd_swiglu_pairs(self.gu.ptr, T, I, self.m.ptr, s), "swiglu")
             self._linear(ly.down, self.m.ptr, T, self.o.ptr)
             _check(L.lbd_add(self.x.ptr, self.o.ptr, T * h, s), "add")
         _check(L.lbd_rmsnorm(self.x.ptr, self.norm.ptr, T, h, cfg.rms_norm_eps, self.h.ptr, s), "rmsnorm")

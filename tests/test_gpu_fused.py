@@ -70,9 +70,10 @@ def plain(fmt, dw, x_dev, y_dev, m=1):
     assert rc == K.ISA_GFX950, K.lib().lb_last_error().decode()
 
 
-def fused(fmt, dw, x_dev, y_dev, m=1, norm=None, eps=0.0, swiglu=False, bias=None, res=None, key=None):
+def fused(fmt, dw, x_dev, y_dev, m=1, norm=None, eps=0.0, swiglu=False, bias=None, res=None, key=None,
+          glu=False):
     L = K.lib()
-    f = K.LbdFusion(norm, eps, int(swiglu), bias, res, key)
+    f = K.LbdFusion(norm, eps, int(swiglu), bias, res, key, int(glu))
     if fmt == "mxfp4":
         return L.lbd_gemv_mxfp4_fused(x_dev, m, dw.kp, dw.qw.ptr, dw.e8m0.ptr, dw.n, y_dev, C.byref(f), None)
     zp = None if dw.zeros is None else dw.zeros.ptr
@@ -159,6 +160,47 @@ def test_bias_and_residual_in_place(rng, fmt, m):
     np.testing.assert_array_equal(dy.to_array((m, n), np.float32), r + y0)
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("m,n,k", [(1, 9728, 896), (1, 600, 4864), (2, 600, 4864), (1, 154, 11008),
+                                   (4, 2000, 128), (1, 2, 256), (3, 9728, 896)])
+def test_glu_epilogue(rng, fmt, m, n, k):
+    """(gate, up) row pairs: the glu epilogue equals the plain fused GEMV followed by
+    lbd_swiglu_pairs bit for bit (same rows, same sums, the SwiGLU kernel's
+    expression), with the RMSNorm prologue and a bias too; shapes cover one, two
+    and four rows per batch (one row: the gate is carried across batches) and the
+    2-8 pair shares of the persistent grid. W4A16 / MXFP4 also held to the float64
+    oracle's bound on silu(g) * u."""
+    hw, dw = weights(rng, fmt, n, k, asym=(fmt == "w4a8"))
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    dx, db = up(x), up(b)
+    L = K.lib()
+    yp, ref, yg = K.DeviceBuffer(4 * m * n), K.DeviceBuffer(4 * m * n // 2), K.DeviceBuffer(4 * m * n // 2)
+    _LIVE.extend([yp, ref, yg])
+    cases = [dict(), dict(bias=db.ptr)]
+    if m == 1:
+        nw = up((1 + 0.05 * rng.standard_normal(k)).astype(np.float32))
+        cases.append(dict(norm=nw.ptr, eps=1e-6, bias=db.ptr))
+    for kw in cases:
+        ok(fused(fmt, dw, dx.ptr, yp.ptr, m, **kw))
+        ok(L.lbd_swiglu_pairs(yp.ptr, m, n // 2, ref.ptr, None))
+        ok(fused(fmt, dw, dx.ptr, yg.ptr, m, glu=True, **kw))
+        np.testing.assert_array_equal(yg.to_array((m, n // 2), np.float32), ref.to_array((m, n // 2), np.float32))
+    if fmt != "w4a8":
+        ok(fused(fmt, dw, dx.ptr, yg.ptr, m, glu=True))
+        t = x.astype(np.float64) @ dense(hw).T
+        g, u = t[:, 0::2], t[:, 1::2]
+        with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: s = 0
+            s = 1 / (1 + np.exp(-g))
+        # |d(silu(g) u)| <= |u| (|s| + |g| s (1 - s)) |dg| + |silu(g)| |du|, dg and du
+        # within the GEMM bound of their rows; plus the float32 rounding of the product
+        bnd = 1e-5 * O.fp_bound(x.astype(np.float64), dense(hw))
+        tol = np.abs(u) * (s + np.abs(g) * s * (1 - s)) * bnd[:, 0::2] + np.abs(g * s) * bnd[:, 1::2]
+        want = g * s * u
+        got = yg.to_array((m, n // 2), np.float32).astype(np.float64)
+        assert np.all(np.abs(got - want) <= tol + 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-30)
+
+
 def test_fused_argument_checks(rng):
     hw, dw = weights(rng, "w4a16", 64, 256)
     x, y, nw = up(np.zeros(512, np.float32)), K.DeviceBuffer(4 * 64 * 4), up(np.ones(256, np.float32))
@@ -167,6 +209,11 @@ def test_fused_argument_checks(rng):
     key = up(np.zeros(1024, np.uint64))
     assert fused("w4a16", dw, x.ptr, y.ptr, m=2, key=key.ptr) == -6           # argmax needs M == 1
     assert fused("w4a16", dw, x.ptr, y.ptr, m=5) == -1                        # small-M kernels only
+    assert fused("w4a16", dw, x.ptr, y.ptr, glu=True, res=y.ptr) == -6         # glu excludes the residual
+    assert fused("w4a16", dw, x.ptr, y.ptr, glu=True, key=key.ptr) == -6       # ... and the argmax key
+    hw3, dw3 = weights(rng, "w4a16", 63, 256)
+    assert fused("w4a16", dw3, x.ptr, y.ptr, glu=True) == -1                   # glu takes row pairs
+    assert fused("w4a16", dw, x.ptr, y.ptr, m=2, glu=True) == K.ISA_GFX950
     assert fused("w4a16", dw, x.ptr, y.ptr, m=1) == K.ISA_GFX950
 
 

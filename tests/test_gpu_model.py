@@ -159,6 +159,11 @@ def test_swiglu_and_add(rng):
     g, u = gu[:, :I].astype(np.float64), gu[:, I:].astype(np.float64)
     ref = g / (1 + np.exp(-g)) * u
     np.testing.assert_allclose(out.to_array((T, I), np.float32), ref, rtol=2e-6, atol=1e-30)
+    # the pair layout: the same operation, bit for bit
+    pairs = np.stack([gu[:, :I], gu[:, I:]], 2).reshape(T, 2 * I)
+    out2 = K.DeviceBuffer(T * I * 4)
+    ok(L.lbd_swiglu_pairs(up(pairs).ptr, T, I, out2.ptr, None))
+    np.testing.assert_array_equal(out2.to_array((T, I), np.float32), out.to_array((T, I), np.float32))
     x, y = rng.standard_normal(1001).astype(np.float32), rng.standard_normal(1001).astype(np.float32)
     dx = up(x)
     ok(L.lbd_add(dx.ptr, up(y).ptr, 1001, None))
