@@ -324,7 +324,8 @@ int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int
 /* One token at position *pos: lbd_qkv_rope (without the bias, which the qkv GEMV's
  * epilogue adds) and lbd_attention with T = 1 in one launch, one workgroup per query
  * head (model.py:353-378). qkv [(H + 2 KV) D] is read only; k and v are written to
- * the caches; out [H D]. H / KV <= 16, D in {32, 64, 128}, cap <= 16000. */
+ * the caches; out [H D]. H / KV <= 16, D in {32, 64, 128}, cap <= 16000; qkv, the
+ * tables and the caches 16-byte aligned. */
 int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table,
                          const float *sin_table, const int32_t *pos, int max_pos,
                          float *k_cache, float *v_cache, int cap, float *out, void *stream);

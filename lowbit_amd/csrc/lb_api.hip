@@ -834,7 +834,9 @@ int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *co
     return fail(LB_ERR_SHAPE, "bad shape");
   if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out)
     return fail(LB_ERR_ARG, "null pointer");
-  if ((reinterpret_cast<uintptr_t>(k_cache) & 15) != 0) return fail(LB_ERR_ARG, "k_cache must be 16-byte aligned");
+  if (!aligned16(qkv) || !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(k_cache) ||
+      !aligned16(v_cache))
+    return fail(LB_ERR_ARG, "qkv, the tables and the caches must be 16-byte aligned");
   LB_LAUNCH(lbk::launch_attention_decode(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap,
                                          out, static_cast<hipStream_t>(stream)),
             "attention decode launch");

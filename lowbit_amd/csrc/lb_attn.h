@@ -1,8 +1,8 @@
 // One decode token's attention for one query head, as device functions of the
 // one-token attention kernel (lb_model.hip): src/lowbit/model.py:353-378 for a
 // single query at absolute position p against the KV-cache keys 0 .. S-1,
-// S = min(p + 1, cap), where (when p < cap) key p is the new one, held in LDS and
-// never read back from the cache.
+// S = min(p + 1, cap), where (when p < cap) key p is the new one, held in
+// registers and never read back from the cache.
 //
 // Memory layout of the work: D / 4 lanes share a key (or value) row, each lane
 // holding one float4 of it, so a wave load covers RPL = 256 / D consecutive rows
@@ -96,25 +96,22 @@ __device__ __forceinline__ void attn_prefetch(AttnRound<D> &rd, const float *__r
   attn_load_round<D>(rd, kb, vb, AttnCfg<D>::kKB * wave, cap);
 }
 
-// Attention of the rotated query qs[D] (LDS) over keys 0 .. S-1: keys other than
-// Sc from the cache rows kb / vb, key Sc (when newk) from kn / vn (LDS). `first`
-// holds the wave's first round (attn_prefetch). Writes out[0 .. D). Every thread
-// of the workgroup calls it (one barrier, at the merge); qs, kn, vn must be
-// visible to all threads on entry.
+// Attention of the rotated query over keys 0 .. S-1: keys other than Sc from the
+// cache rows kb / vb, key Sc (when newk) the new one. Each lane passes its float4
+// (elements 4 (lane % (D/4)) ..) of the rotated query q4, the new key kn4 and its
+// value vn4. `first` holds the wave's first round (attn_prefetch). Writes
+// out[0 .. D). Every thread of the workgroup calls it (one barrier, at the merge).
 template <int D, int NT>
-__device__ __forceinline__ void attn_run(const AttnRound<D> &first, const float *qs, const float *kn,
-                                         const float *vn, const float *__restrict__ kb,
-                                         const float *__restrict__ vb, int S, int Sc, bool newk, int cap,
-                                         AttnShared<D, NT> &sh, float *__restrict__ out) {
+__device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, float4 kn4, float4 vn4,
+                                         const float *__restrict__ kb, const float *__restrict__ vb, int S,
+                                         int Sc, bool newk, int cap, AttnShared<D, NT> &sh,
+                                         float *__restrict__ out) {
   constexpr int LPR = AttnCfg<D>::kLPR, RPL = AttnCfg<D>::kRPL, U = AttnCfg<D>::kU, KB = AttnCfg<D>::kKB;
   constexpr int NW = NT / kWave;
   static_assert(NT % kWave == 0, "whole waves");
   const int tid = threadIdx.x, lane = tid & (kWave - 1), r = lane / LPR, e4 = lane % LPR;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const float scale = 1.0f / sqrtf((float)D);
-  const float4 q4 = reinterpret_cast<const float4 *>(qs)[e4];
-  const float4 kn4 = reinterpret_cast<const float4 *>(kn)[e4];
-  const float4 vn4 = reinterpret_cast<const float4 *>(vn)[e4];
   float m = -INFINITY, l = 0.0f;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   AttnRound<D> rd = first;
@@ -195,6 +192,33 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s, 
 #pragma clang fp contract(off)
   y1 = x1 * c - x2 * s;
   y2 = x2 * c + x1 * s;
+}
+
+// The rotated value of one element of a head: `own` is the element, `partner`
+// the one it is paired with (i + D/2 for i < D/2, i - D/2 otherwise; `hi` for the
+// second half), c / s the angle of the pair.
+__device__ __forceinline__ float rope_elem(bool hi, float own, float partner, float c, float s) {
+  float y1, y2;
+  rope_pair(hi ? partner : own, hi ? own : partner, c, s, y1, y2);
+  return hi ? y2 : y1;
+}
+
+// Elements 4 e4 .. 4 e4 + 3 of the head row x [D] rotated at table row pc (cos/sin
+// tables [.., D/2]); x, the tables and their rows 16-byte aligned.
+template <int D>
+__device__ __forceinline__ float4 rope4(const float *x, const float *__restrict__ cosT,
+                                        const float *__restrict__ sinT, int pc, int e4) {
+  constexpr int half = D / 2;
+  static_assert(half % 4 == 0, "a float4 never straddles the two halves");
+  const int e = 4 * e4;
+  const bool hi = e >= half;
+  const int i = hi ? e - half : e;
+  const float4 a = *reinterpret_cast<const float4 *>(x + e);
+  const float4 b = *reinterpret_cast<const float4 *>(x + (hi ? i : e + half));
+  const float4 c = *reinterpret_cast<const float4 *>(cosT + (size_t)pc * half + i);
+  const float4 s = *reinterpret_cast<const float4 *>(sinT + (size_t)pc * half + i);
+  return make_float4(rope_elem(hi, a.x, b.x, c.x, s.x), rope_elem(hi, a.y, b.y, c.y, s.y),
+                     rope_elem(hi, a.z, b.z, c.z, s.z), rope_elem(hi, a.w, b.w, c.w, s.w));
 }
 
 }  // namespace lbk

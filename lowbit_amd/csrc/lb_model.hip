@@ -166,14 +166,15 @@ __global__ __launch_bounds__(kWave) void attention_kernel(const float *__restric
 //   0. before anything else (and before *pos arrives) each wave requests its first
 //      round of key and value rows (coalesced float4 rows, lb_attn.h; rows below
 //      cap);
-//   1. rotate the query head and the key ("rotate_half", src/lowbit/model.py:
-//      201-210) into LDS; the group's first workgroup writes the rotated key and
-//      the value to the caches at p (when p < cap);
+//   1. every lane rotates its float4 of the query head and of the key
+//      ("rotate_half", src/lowbit/model.py:201-210) in registers, with no LDS and
+//      no barrier; the group's first workgroup writes the rotated key and the
+//      value to the caches at p (when p < cap);
 //   2. every wave runs an online softmax over its keys of each round
 //      (src/lowbit/model.py:353-378), with no barrier;
 //   3. the waves' (max, sum, p * v) are merged in LDS and divided by the sum.
 // Keys 0 .. S-1 with S = min(p + 1, cap) take part; when p < cap key p is the new
-// one (from LDS, never read back from the cache), otherwise all S come from the
+// one (from registers, never read back from the cache), otherwise all S come from the
 // cache, as lbd_qkv_rope + lbd_attention behave. Output out [H D].
 constexpr int kAttThreads = 256;
 
@@ -182,13 +183,9 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
     const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
     const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc, float *__restrict__ vc, int cap,
     float *__restrict__ out) {
-  constexpr int half = D / 2;
-  __shared__ __align__(16) float qs[D];
-  __shared__ __align__(16) float kn[D];
-  __shared__ __align__(16) float vn[D];
   __shared__ AttnShared<D, kAttThreads> sh;
   const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, e4 = tid % (D / 4);
   const float *kb = kc + (size_t)g * cap * D;
   const float *vb = vc + (size_t)g * cap * D;
 
@@ -202,35 +199,18 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
   const int Sc = newk ? S - 1 : S;  // keys read from the cache; key Sc is the new one when newk
 
-  // ---- 1. rotary embedding of the query head and of the key; the value
-  for (int e = tid; e < 2 * half; e += kAttThreads) {
-    const int which = e / half, i = e - which * half;  // 0: query head h, 1: key head g
-    const int hd = which == 0 ? h : H + g;
-    const float x1 = qkv[(size_t)hd * D + i], x2 = qkv[(size_t)hd * D + i + half];
-    const float c = cosT[(size_t)pc * half + i], sn = sinT[(size_t)pc * half + i];
-    float y1, y2;
-    rope_pair(x1, x2, c, sn, y1, y2);
-    if (which == 0) {
-      qs[i] = y1;
-      qs[i + half] = y2;
-    } else {
-      kn[i] = y1;
-      kn[i + half] = y2;
-      if (newk && j == 0) {
-        kc[((size_t)g * cap + p) * D + i] = y1;
-        kc[((size_t)g * cap + p) * D + i + half] = y2;
-      }
-    }
+  // ---- 1. every lane rotates its float4 of the query head and of the key; the
+  //         group's first workgroup writes the key and the value to the caches
+  const float4 q4 = rope4<D>(qkv + (size_t)h * D, cosT, sinT, pc, e4);
+  const float4 kn4 = rope4<D>(qkv + (size_t)(H + g) * D, cosT, sinT, pc, e4);
+  const float4 vn4 = *reinterpret_cast<const float4 *>(qkv + (size_t)(H + KV + g) * D + 4 * e4);
+  if (newk && j == 0 && tid < D / 4) {
+    *reinterpret_cast<float4 *>(kc + ((size_t)g * cap + p) * D + 4 * e4) = kn4;
+    *reinterpret_cast<float4 *>(vc + ((size_t)g * cap + p) * D + 4 * e4) = vn4;
   }
-  for (int e = tid; e < D; e += kAttThreads) {
-    const float v = qkv[(size_t)(H + KV + g) * D + e];
-    vn[e] = v;
-    if (newk && j == 0) vc[((size_t)g * cap + p) * D + e] = v;
-  }
-  __syncthreads();
 
   // ---- 2, 3. per-wave online softmax over rounds of keys; the waves merged
-  attn_run<D, kAttThreads>(pre, qs, kn, vn, kb, vb, S, Sc, newk, cap, sh, out + (size_t)h * D);
+  attn_run<D, kAttThreads>(pre, q4, kn4, vn4, kb, vb, S, Sc, newk, cap, sh, out + (size_t)h * D);
 }
 
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused

@@ -293,7 +293,8 @@ def attention_one(qkv, kc, vc, p, H, KV, D, cos, sin):
 
 @pytest.mark.parametrize("D,H,KV,p,cap", [(64, 14, 2, 0, 8), (64, 14, 2, 191, 192), (64, 14, 2, 255, 300),
                                           (64, 14, 2, 256, 300), (32, 8, 1, 37, 64), (128, 4, 4, 700, 1000),
-                                          (64, 16, 1, 5, 16), (64, 2, 2, 20, 20), (64, 14, 2, 15999, 16000)])
+                                          (64, 16, 1, 5, 16), (64, 2, 2, 20, 20), (64, 14, 2, 15999, 16000),
+                                          (64, 14, 2, 70, 16000), (32, 8, 2, 300, 301), (128, 8, 8, 4000, 4000)])
 def test_attention_decode(rng, D, H, KV, p, cap):
     L = K.lib()
     width = (H + 2 * KV) * D
@@ -324,6 +325,29 @@ def test_attention_decode(rng, D, H, KV, p, cap):
         others[p] = False
     np.testing.assert_array_equal(kc[:, others], kc0[:, others])
     np.testing.assert_array_equal(vc[:, others], vc0[:, others])
+
+
+def test_attention_decode_consecutive_positions(rng):
+    """A run of decode positions on one cache (as the decoder's graph replays it):
+    every step matches the float64 attention, and each step's cache row is there
+    for the next."""
+    L = K.lib()
+    D, H, KV, cap = 64, 14, 2, 600
+    max_pos = 1024
+    cos, sin = DM.rope_tables(D, max_pos, 10000.0)
+    kc = rng.standard_normal((KV, cap, D)).astype(np.float32)
+    vc = rng.standard_normal((KV, cap, D)).astype(np.float32)
+    dk, dv, out = up(kc), up(vc), K.DeviceBuffer(4 * H * D)
+    _LIVE.append(out)
+    dcos, dsin = up(cos), up(sin)
+    for p in (0, 1, 63, 64, 65, 255, 256, 300, 599):
+        qkv = rng.standard_normal((H + 2 * KV) * D).astype(np.float32)
+        ok(L.lbd_attention_decode(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, up(np.array([p], np.int32)).ptr,
+                                  max_pos, dk.ptr, dv.ptr, cap, out.ptr, None))
+        ref, k, v = attention_one(qkv, kc, vc, p, H, KV, D, cos, sin)
+        got = out.to_array((H * D,), np.float32)
+        assert np.abs(got - ref).max() <= 2e-5 * max(np.abs(vc).max(), np.abs(v).max()), p
+        kc, vc = dk.to_array(kc.shape, np.float32), dv.to_array(vc.shape, np.float32)
 
 
 def test_attention_decode_argument_checks():
