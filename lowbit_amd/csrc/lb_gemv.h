@@ -18,7 +18,8 @@ namespace lbk {
 //     for every workgroup, so it should run as few times as possible;
 //   * the VALU issue rate, not HBM, is the next limit, so tails and bounds must
 //     cost no instructions.
-// The grid is persistent: two 512-thread workgroups per CU. Each workgroup
+// The grid is persistent: two 512-thread workgroups per CU where two fit at once
+// (one elsewhere, see launch_gemv_mb). Each workgroup
 // stages (or quantizes) the activations once, and its 8 waves take an even
 // share of the weight rows (rows [gw*N/W, (gw+1)*N/W) for global wave gw of W).
 // A wave first loads its activation slice into registers, then issues all the
@@ -493,45 +494,68 @@ void gemv_kernel(GemmArgs a) {
   if (a.amax_key && lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
 }
 
-// Register-held chunks per lane (NIT) from the row length; rows per wave (R)
-// from the share of rows each wave gets under the persistent grid.
+using GemvFn = void (*)(GemmArgs);
+
+// Rows held at once (R) from the share of rows each wave gets under the
+// persistent grid, for NIT register-held chunks per lane.
 template <int F, int MB, int NIT, int PRO>
-static hipError_t launch_gemv_nit(const GemmArgs &a, int grid, int rpw, size_t lds, hipStream_t s) {
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(kGemvThreads), lds, s, a);
-    return hipGetLastError();
-  };
+static GemvFn pick_gemv_nit(int rpw) {
   // rows held at once: R * NIT chunks of weights must stay in registers next to the
   // activations (larger shares are processed R rows at a time)
   constexpr int RMAX = MB == 1 ? (NIT >= 8 ? 1 : NIT >= 4 ? 2 : 4) : MB == 2 ? (NIT >= 4 ? 1 : 2) : 1;
   if constexpr (RMAX == 1) {
-    return go(gemv_kernel<F, MB, 1, NIT, PRO>);
+    return gemv_kernel<F, MB, 1, NIT, PRO>;
   } else if constexpr (RMAX == 2) {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
-    return go(gemv_kernel<F, MB, 2, NIT, PRO>);
+    return rpw <= 1 ? gemv_kernel<F, MB, 1, NIT, PRO> : gemv_kernel<F, MB, 2, NIT, PRO>;
   } else {
-    if (rpw <= 1) return go(gemv_kernel<F, MB, 1, NIT, PRO>);
-    if (rpw <= 2) return go(gemv_kernel<F, MB, 2, NIT, PRO>);
-    if (rpw <= 3) return go(gemv_kernel<F, MB, 3, NIT, PRO>);
-    return go(gemv_kernel<F, MB, 4, NIT, PRO>);
+    if (rpw <= 1) return gemv_kernel<F, MB, 1, NIT, PRO>;
+    if (rpw <= 2) return gemv_kernel<F, MB, 2, NIT, PRO>;
+    if (rpw <= 3) return gemv_kernel<F, MB, 3, NIT, PRO>;
+    return gemv_kernel<F, MB, 4, NIT, PRO>;
   }
 }
 
+// The kernel for rows of nit register-held chunks per lane; null where the
+// activations exceed the LDS budget.
+template <int F, int MB, int PRO>
+static GemvFn pick_gemv(int nit, int rpw) {
+  if (nit <= 1) return pick_gemv_nit<F, MB, 1, PRO>(rpw);
+  if (nit <= 2) return pick_gemv_nit<F, MB, 2, PRO>(rpw);
+  if (nit <= 4) return pick_gemv_nit<F, MB, 4, PRO>(rpw);
+  // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
+  if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return nullptr;
+  else return pick_gemv_nit<F, MB, 8, PRO>(rpw);
+}
+
+// Persistent grid of at most two workgroups per CU, fewer when there are few rows.
+// Two only when two fit on a CU at once (at most 128 VGPRs per lane, and the LDS of
+// both): otherwise the second waits for the first to finish, and one workgroup per
+// CU with twice the rows is faster (long rows: 9-16 % at 1 x 4096 x 11008 cold).
+// W4A8 quantizes the activation row in every workgroup, so below two rows per wave
+// it takes one workgroup per CU as well (3-9 % at N = 3072 .. 6144).
 template <int F, int MB, int PRO>
 static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
+  constexpr bool kQuant = (F == F_W4A8 || F == F_W4A8G32);
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
   const int cus = num_cus > 0 ? num_cus : 256;
-  // persistent grid: two workgroups per CU, fewer when there are few rows
-  int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
-  grid = grid < 2 * cus ? grid : 2 * cus;
-  const int waves = grid * kGemvWaves;
-  const int rpw = a.glu ? 2 * ((a.N / 2 + waves - 1) / waves) : (a.N + waves - 1) / waves;
-  if (nit <= 1) return launch_gemv_nit<F, MB, 1, PRO>(a, grid, rpw, lds, s);
-  if (nit <= 2) return launch_gemv_nit<F, MB, 2, PRO>(a, grid, rpw, lds, s);
-  if (nit <= 4) return launch_gemv_nit<F, MB, 4, PRO>(a, grid, rpw, lds, s);
-  // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
-  if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return hipErrorInvalidValue;
-  else return launch_gemv_nit<F, MB, 8, PRO>(a, grid, rpw, lds, s);
+  int per_cu = (kQuant && a.N < 2 * 2 * cus * kGemvWaves) ? 1 : 2;
+  for (;;) {
+    int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
+    grid = grid < per_cu * cus ? grid : per_cu * cus;
+    const int waves = grid * kGemvWaves;
+    const int rpw = a.glu ? 2 * ((a.N / 2 + waves - 1) / waves) : (a.N + waves - 1) / waves;
+    const GemvFn k = pick_gemv<F, MB, PRO>(nit, rpw);
+    if (!k) return hipErrorInvalidValue;
+    if (per_cu == 2 && grid > cus && gemv_wg_per_cu(reinterpret_cast<const void *>(k), lds) < 2) {
+      per_cu = 1;
+      continue;
+    }
+    GemmArgs arg = a;
+    void *args[] = {&arg};
+    const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(kGemvThreads), args,
+                                         lds, s);
+    return e != hipSuccess ? e : hipGetLastError();
+  }
 }
 
 template <int F>

@@ -87,6 +87,9 @@ size_t gemv_lds_bytes(int fmt, int M, int Kp);
 bool gemv_eligible(int fmt, int M, int Kp);
 
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
+// Workgroups of a small-M kernel (512 threads, `lds` bytes of dynamic LDS) that fit
+// on one CU at once; asked of the runtime once per kernel and size.
+int gemv_wg_per_cu(const void *kern, size_t lds);
 // the group-32 instantiations of the small-M kernels (lb_gemv_g32.hip)
 hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s);
 // Per-token int8 quantizer: xq, xs, asum as lb_quant_act_int8, or (tiled) xq and asum

@@ -26,6 +26,9 @@
 // the matching activations in the same slots, so weights go from HBM to the
 // matrix cores without an LDS transpose.
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include <type_traits>
 
@@ -139,6 +142,19 @@ size_t gemv_lds_bytes(int fmt, int M, int Kp) {
 bool gemv_eligible(int fmt, int M, int Kp) {
   return M >= 1 && M <= kGemvMaxM && Kp <= kGemvMaxNit * kWave * 32 &&
          gemv_lds_bytes(fmt, M, Kp) <= kGemvLdsLimit;
+}
+
+int gemv_wg_per_cu(const void *kern, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, size_t>, int> known;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kern, lds);
+  const auto it = known.find(key);
+  if (it != known.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kGemvThreads, lds) != hipSuccess || n < 1) n = 1;
+  known[key] = n;
+  return n;
 }
 
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
