@@ -72,6 +72,16 @@ __device__ __forceinline__ int half_wave_sum(int v) {
   return v;
 }
 
+// Float sum over each 32-lane half of the wave; the totals land in lanes 31 and 63.
+__device__ __forceinline__ float half_wave_sum_f(float v) {
+  v += dpp_f<kDppQuad1032>(v, 0.0f);
+  v += dpp_f<kDppQuad2301>(v, 0.0f);
+  v += dpp_f<kDppRowHalfMirror>(v, 0.0f);
+  v += dpp_f<kDppRowMirror>(v, 0.0f);
+  v += dpp_f<kDppRowBcast15, 0xA>(v, 0.0f);
+  return v;
+}
+
 // Sum over each group of eight lanes; every lane of the group gets it (quad sums,
 // then the mirrored quad of the same half-row).
 __device__ __forceinline__ int eighth_wave_sum(int v) {

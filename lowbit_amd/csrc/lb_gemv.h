@@ -74,51 +74,60 @@ struct GemvRegs {
 };
 
 // Rows rb .. rb+R-1; rows at or past `rend` get zero-length descriptors (read 0).
-template <int F, int R, int NIT>
+// HW (rows of at most 32 chunks): slot r holds two rows, rb + 2r in lanes 0..31 and
+// rb + 2r + 1 in lanes 32..63, under one descriptor over both (adjacent in memory);
+// lanes past a row's chunks read past the descriptor, i.e. zeros.
+template <int F, int R, int NIT, bool HW>
 __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT> &g, int rb, int rend, int lane,
                                           int nch, int G) {
+  static_assert(!HW || NIT == 1, "two rows per wave load: one chunk per lane");
   const uint32_t rowbytes = (uint32_t)(a.Kp >> 1);
   const int zadd = a.zeros ? 0 : 8;  // symmetric weights: z = 8
   constexpr bool kG32 = fmt_g32(F);
+  const uint32_t half = HW ? (uint32_t)lane >> 5 : 0u;
+  const uint32_t cl = HW ? (uint32_t)lane & 31u : (uint32_t)lane;
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const int row = rb + r;
-    const bool ok = row < rend;
-    const size_t rr = ok ? (size_t)row : 0;
-    const Rsrc rw = make_rsrc(a.qw + rr * rowbytes, ok ? rowbytes : 0);
+    const int row = rb + (HW ? 2 * r : r);
+    const uint32_t nrows = row < rend ? ((HW && row + 1 < rend) ? 2u : 1u) : 0u;
+    const size_t rr = nrows ? (size_t)row : 0;
+    const Rsrc rw = make_rsrc(a.qw + rr * rowbytes, nrows * rowbytes);
     if constexpr (F == F_MXFP4) {
-      const Rsrc re = make_rsrc(a.e8m0 + rr * nch, ok ? (uint32_t)nch : 0);
+      const Rsrc re = make_rsrc(a.e8m0 + rr * nch, nrows * (uint32_t)nch);
 #pragma unroll
       for (int it = 0; it < NIT; it++) {
-        const uint32_t ci = lane + kWave * it;
-        g.w[r][it] = ld_b128(rw, ci * 16);
-        g.sc[r][it] = e8m0_to_f32(ld_u8(re, ci));
+        const uint32_t ci = cl + kWave * it;
+        const bool live = !HW || ci < (uint32_t)nch;
+        g.w[r][it] = ld_b128(rw, live ? half * rowbytes + ci * 16 : 2 * rowbytes);
+        g.sc[r][it] = e8m0_to_f32(ld_u8(re, live ? half * (uint32_t)nch + ci : 2 * (uint32_t)nch));
         g.zi[r][it] = 0;
       }
     } else {
-      const Rsrc rs = make_rsrc(a.scales + rr * G, ok ? (uint32_t)G * 4 : 0);
-      const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (ok && a.zeros) ? (uint32_t)G : 0);
+      const Rsrc rs = make_rsrc(a.scales + rr * G, nrows * (uint32_t)G * 4);
+      const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, a.zeros ? nrows * (uint32_t)G : 0);
 #pragma unroll
       for (int it = 0; it < NIT; it++) {
-        const uint32_t ci = lane + kWave * it;
-        g.w[r][it] = ld_b128(rw, ci * 16);
+        const uint32_t ci = cl + kWave * it;
+        const bool live = !HW || ci < (uint32_t)nch;
+        g.w[r][it] = ld_b128(rw, live ? half * rowbytes + ci * 16 : 2 * rowbytes);
         const uint32_t gi = kG32 ? ci : ci >> 2;  // the chunk's group
-        g.sc[r][it] = ld_f32(rs, gi * 4);
-        g.zi[r][it] = (int)ld_u8(rz, gi) + zadd;
+        g.sc[r][it] = ld_f32(rs, live ? (half * (uint32_t)G + gi) * 4 : 2 * (uint32_t)G * 4);
+        g.zi[r][it] = (int)ld_u8(rz, live ? half * (uint32_t)G + gi : 2 * (uint32_t)G) + zadd;
       }
     }
   }
 }
 
-// acc[m][r] += this lane's share of row r (r < nr) against activation row m.
-// Chunks past the row end hold zero weights, zero scales and zero activations.
-template <int F, int MB, int R, int NIT>
+// acc[m][r] += this lane's share of slot r (r < nr) against activation row m (HW:
+// each half-wave its own row of the slot). Chunks past the row end hold zero
+// weights, zero scales and zero activations.
+template <int F, int MB, int R, int NIT, bool HW>
 __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float (&acc)[MB][R], int nr, int lane,
                                              int nchp, int Gp, const float *xl, const uint8_t *ql,
                                              const int32_t *asl) {
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int ci = lane + kWave * it;
+    const int ci = (HW ? lane & 31 : lane) + kWave * it;
     if (it * kWave >= nchp) break;  // uniform: this row length needs fewer chunks
     if constexpr (F == F_W4A16 || F == F_W4A16G32) {
 #pragma unroll
@@ -244,9 +253,13 @@ struct GemvMinWaves {
 // 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
 // adds `bias` and `res` when given and max-combines argmax keys into `amax_key`;
 // under `glu` it writes silu(gate) * up of each (gate, up) row pair instead.
-template <int F, int MB, int R, int NIT, int PRO>
+// HW (rows of at most 1024 elements, one activation row): every wave load covers
+// two weight rows, one per half-wave, so no lane idles past a short row's end.
+template <int F, int MB, int R, int NIT, int PRO, bool HW = false>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(GemvMinWaves<F, MB, PRO>::value)))
 void gemv_kernel(GemmArgs a) {
+  static_assert(!HW || (MB == 1 && NIT == 1), "two rows per wave load: one activation row, one chunk per lane");
+  constexpr int RR = HW ? 2 * R : R;  // weight rows per batch (R slots)
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[2][kGemvWaves];
   constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q || F == F_W4A8G32);
@@ -296,17 +309,17 @@ void gemv_kernel(GemmArgs a) {
   // ---- 2. the weight stream of this wave's first R rows, then their epilogue
   //         operands (bias, residual), so that the epilogue waits for no load
   GemvRegs<F, R, NIT> g;
-  float bv[R], rv[MB][R];
+  float bv[RR], rv[MB][RR];
   auto epi_load = [&](int rb) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
+    for (int r = 0; r < RR; r++) {
       const int n = rb + r < N ? rb + r : N - 1;  // rows past the share are never stored
       bv[r] = a.bias ? a.bias[n] : 0.0f;
 #pragma unroll
       for (int m = 0; m < MB; m++) rv[m][r] = a.res ? a.res[(size_t)m * N + n] : 0.0f;
     }
   };
-  gemv_load<F, R, NIT>(a, g, r0, r1, lane, nch, G);
+  gemv_load<F, R, NIT, HW>(a, g, r0, r1, lane, nch, G);
   epi_load(r0);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -444,26 +457,39 @@ void gemv_kernel(GemmArgs a) {
   float tg[MB];                 // glu: the gate output of the pair in progress (rows in order)
 #pragma unroll
   for (int m = 0; m < MB; m++) tg[m] = 0.0f;
-  for (int rb = r0; rb < r1; rb += R) {
+  for (int rb = r0; rb < r1; rb += RR) {
     if (rb != r0) {
-      gemv_load<F, R, NIT>(a, g, rb, r1, lane, nch, G);
+      gemv_load<F, R, NIT, HW>(a, g, rb, r1, lane, nch, G);
       epi_load(rb);
     }
-    const int nr = min(R, r1 - rb);
+    const int nr = min(RR, r1 - rb);          // rows of this batch
+    const int ns = HW ? (nr + 1) >> 1 : nr;   // slots holding them
     float acc[MB][R];
 #pragma unroll
     for (int m = 0; m < MB; m++)
 #pragma unroll
       for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
-    gemv_compute<F, MB, R, NIT>(g, acc, nr, lane, nchp, Gp, xl, ql, asl);
-    // ---- 5. one wave reduction per output (every lane gets it), the epilogue,
-    //         and lane m*R + r stores it
+    gemv_compute<F, MB, R, NIT, HW>(g, acc, ns, lane, nchp, Gp, xl, ql, asl);
+    // ---- 5. one wave (HW: half-wave) reduction per output (every lane gets it),
+    //         the epilogue, and lane m*RR + r stores it
 #pragma unroll
-    for (int m = 0; m < MB; m++)
+    for (int m = 0; m < MB; m++) {
+      float tt[RR];
 #pragma unroll
       for (int r = 0; r < R; r++) {
+        if (r >= ns) break;
+        if constexpr (HW) {
+          const float v = half_wave_sum_f(acc[m][r]);
+          tt[2 * r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+          tt[2 * r + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+        } else {
+          tt[r] = wave_sum(acc[m][r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RR; r++) {
         if (r >= nr) break;
-        float t = wave_sum(acc[m][r]);
+        float t = tt[r];
         const int n = rb + r;
         size_t o = (size_t)m * N + n;
         {
@@ -483,12 +509,13 @@ void gemv_kernel(GemmArgs a) {
           t = tg[m] / (1.0f + expf(-tg[m])) * t;  // the SwiGLU kernel's expression
           o = (size_t)m * (N >> 1) + (n >> 1);
         }
-        if (lane == m * R + r) a.y[o] = t;
+        if (lane == m * RR + r) a.y[o] = t;
         if (a.amax_key) {
           const unsigned long long k = argmax_key(t, n);
           best = k > best ? k : best;
         }
       }
+    }
   }
   // spread over the slots so that no address takes more than a few atomics
   if (a.amax_key && lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
@@ -515,10 +542,23 @@ static GemvFn pick_gemv_nit(int rpw) {
   }
 }
 
-// The kernel for rows of nit register-held chunks per lane; null where the
-// activations exceed the LDS budget.
+// Two rows per wave load (HW) for rows of at most 32 chunks: R slots of two rows.
+template <int F, int PRO>
+static GemvFn pick_gemv_hw(int rpw) {
+  const int slots = (rpw + 1) / 2;
+  if (slots <= 1) return gemv_kernel<F, 1, 1, 1, PRO, true>;
+  if (slots <= 2) return gemv_kernel<F, 1, 2, 1, PRO, true>;
+  if (slots <= 3) return gemv_kernel<F, 1, 3, 1, PRO, true>;
+  return gemv_kernel<F, 1, 4, 1, PRO, true>;
+}
+
+// The kernel for rows of nit register-held chunks per lane (nch chunks); null where
+// the activations exceed the LDS budget.
 template <int F, int MB, int PRO>
-static GemvFn pick_gemv(int nit, int rpw) {
+static GemvFn pick_gemv(int nit, int nch, int rpw) {
+  if constexpr (MB == 1 && !fmt_g32(F)) {
+    if (nch <= kWave / 2 && rpw >= 2) return pick_gemv_hw<F, PRO>(rpw);
+  }
   if (nit <= 1) return pick_gemv_nit<F, MB, 1, PRO>(rpw);
   if (nit <= 2) return pick_gemv_nit<F, MB, 2, PRO>(rpw);
   if (nit <= 4) return pick_gemv_nit<F, MB, 4, PRO>(rpw);
@@ -544,7 +584,7 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
     grid = grid < per_cu * cus ? grid : per_cu * cus;
     const int waves = grid * kGemvWaves;
     const int rpw = a.glu ? 2 * ((a.N / 2 + waves - 1) / waves) : (a.N + waves - 1) / waves;
-    const GemvFn k = pick_gemv<F, MB, PRO>(nit, rpw);
+    const GemvFn k = pick_gemv<F, MB, PRO>(nit, a.Kp >> 5, rpw);
     if (!k) return hipErrorInvalidValue;
     if (per_cu == 2 && grid > cus && gemv_wg_per_cu(reinterpret_cast<const void *>(k), lds) < 2) {
       per_cu = 1;

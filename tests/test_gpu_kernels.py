@@ -238,6 +238,36 @@ def test_one_dimensional_x_and_params_auto(rng):
     np.testing.assert_array_equal(y1, y2)
 
 
+# Rows of at most 1024 elements at one activation row take two weight rows per
+# wave load (one per half-wave; the last slot of an odd share holds one). The
+# same rows through the two-activation-row kernel, which loads one weight row per
+# wave load, must give the same bits (both reduce each row over the same lanes in
+# the same order), and both stay within the oracle's bound.
+@pytest.mark.parametrize("fmt", ["w4a16", "w4a8", "mxfp4"])
+@pytest.mark.parametrize("n,k", [(8191, 896), (12345, 1024), (151936, 128), (5000, 640), (9001, 256), (4097, 96)])
+def test_two_rows_per_wave_load_match_one(rng, fmt, n, k):
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    W = lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=(fmt == "w4a8"))
+    D = lb.to_device(W)
+    fn = {"w4a16": K.gemm_w4a16, "w4a8": K.gemm_w4a8, "mxfp4": K.gemm_mxfp4}[fmt]
+    y1 = fn(x, D, isa="gfx950")
+    y2 = fn(np.concatenate([x, x]), D, isa="gfx950")
+    assert K.last_path() == "gfx950"
+    np.testing.assert_array_equal(y1[0], y2[0])
+    np.testing.assert_array_equal(y1[0], y2[1])
+    xp = lb.formats.pad_acts(x, W.kp)
+    if fmt == "w4a16":
+        O.assert_fp_close(y1, O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros), _int4_bound(xp, W), RTOL)
+    elif fmt == "mxfp4":
+        O.assert_fp_close(y1, O.gemm_mxfp4_ref(xp, W.qw, W.e8m0),
+                          cref.c_gemm_mxfp4(xp, W.qw, W.e8m0, absval=True), RTOL)
+    else:
+        a = lb.quantize_act_int8(x)
+        ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+        O.assert_fp_close(y1, ref, bound, RTOL)
+
+
 def test_device_resident_weights_match_host_path(rng):
     x, w = _problem(rng, 3, 130, 700)
     for Wq in (lb.quantize_int4(w, asym=True), lb.quantize_int4(w)):
