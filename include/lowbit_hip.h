@@ -329,6 +329,18 @@ int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int
 int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table,
                          const float *sin_table, const int32_t *pos, int max_pos,
                          float *k_cache, float *v_cache, int cap, float *out, void *stream);
+/* The same with a workspace for long caches: with work != NULL and cap >= 1024, each
+ * query head's keys are cut into slices of 4096 / D keys on one-wave workgroups (at
+ * most 32 per head) and a second launch merges their partial sums from `work`, so a
+ * head's keys stream through many compute units; shorter caches (or work == NULL)
+ * take lbd_attention_decode's one-workgroup-per-head kernel. work: device memory of
+ * lbd_attention_decode_work_bytes(H, D, cap) bytes, 16-byte aligned (out too); calls
+ * sharing it must be ordered (one stream). */
+size_t lbd_attention_decode_work_bytes(int H, int D, int cap);
+int lbd_attention_decode_ws(const float *qkv, int H, int KV, int D, const float *cos_table,
+                            const float *sin_table, const int32_t *pos, int max_pos,
+                            float *k_cache, float *v_cache, int cap, float *out, void *work,
+                            size_t work_bytes, void *stream);
 
 /* ---- device plumbing for the ctypes layer and benchmarks ---- */
 int lb_dev_malloc(void **ptr, size_t bytes);

@@ -826,9 +826,9 @@ int lbd_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int
             "argmax finalize launch");
 }
 
-int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
-                         const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *out,
-                         void *stream) {
+static int attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
+                     const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *out, void *work,
+                     size_t work_bytes, void *stream) {
   if (H <= 0 || KV <= 0 || H % KV || H / KV > lbk::kAttnMaxGroup || (D != 32 && D != 64 && D != 128) ||
       max_pos <= 0 || cap <= 0 || cap > 16000)
     return fail(LB_ERR_SHAPE, "bad shape");
@@ -837,9 +837,32 @@ int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *co
   if (!aligned16(qkv) || !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(k_cache) ||
       !aligned16(v_cache))
     return fail(LB_ERR_ARG, "qkv, the tables and the caches must be 16-byte aligned");
+  if (work && (!aligned16(work) || !aligned16(out)))
+    return fail(LB_ERR_ARG, "work and out must be 16-byte aligned");
+  if (work && work_bytes < lbk::attn_work_bytes(H, D, cap))
+    return fail(LB_ERR_ARG, "work smaller than lbd_attention_decode_work_bytes");
   LB_LAUNCH(lbk::launch_attention_decode(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap,
-                                         out, static_cast<hipStream_t>(stream)),
+                                         out, static_cast<float *>(work), static_cast<hipStream_t>(stream)),
             "attention decode launch");
+}
+
+int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
+                         const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *out,
+                         void *stream) {
+  return attention_decode(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap, out, nullptr, 0,
+                          stream);
+}
+
+size_t lbd_attention_decode_work_bytes(int H, int D, int cap) {
+  if (H <= 0 || (D != 32 && D != 64 && D != 128) || cap <= 0) return 0;
+  return lbk::attn_work_bytes(H, D, cap);
+}
+
+int lbd_attention_decode_ws(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
+                            const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *out,
+                            void *work, size_t work_bytes, void *stream) {
+  return attention_decode(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap, out, work,
+                          work_bytes, stream);
 }
 
 // ---------------------------------------------------------------- host-pointer GEMMs

@@ -126,9 +126,23 @@ hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int 
 hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist,
                                   int hist_len, hipStream_t s);
 // One-token attention with the rotary embedding and the KV-cache write folded in.
-constexpr int kAttnMaxGroup = 16;  // query heads per KV head
+// With a workspace and a cache of at least kAttnSliceMinCap positions, each query
+// head's keys are cut into slices of one wave round (4096 / D keys), at most
+// kAttnMaxSplit per head, whose partials [H][slices][D + 4] floats a second kernel
+// merges; otherwise one workgroup per query head (work may be null).
+constexpr int kAttnMaxGroup = 16;     // query heads per KV head
+constexpr int kAttnMaxSplit = 32;     // key slices per head
+constexpr int kAttnSliceMinCap = 1024;
+inline int attn_slices(int D, int cap) {
+  const int kb = 64 * 64 / D;
+  const int n = (cap + kb - 1) / kb;
+  return n < kAttnMaxSplit ? n : kAttnMaxSplit;
+}
+inline size_t attn_work_bytes(int H, int D, int cap) {
+  return (size_t)H * attn_slices(D, cap) * (D + 4) * sizeof(float);
+}
 hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
                                    const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
-                                   hipStream_t s);
+                                   float *work, hipStream_t s);
 
 }  // namespace lbk

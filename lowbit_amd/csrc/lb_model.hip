@@ -9,6 +9,8 @@
 // from `pos`, and the argmax writes the next token and advances `pos`.
 #include <math.h>
 
+#include <type_traits>
+
 #include "lb_device.h"
 #include "lb_attn.h"
 #include "lb_internal.h"
@@ -213,6 +215,140 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   attn_run<D, kAttThreads>(pre, q4, kn4, vn4, kb, vb, S, Sc, newk, cap, sh, out + (size_t)h * D);
 }
 
+// Long caches (cap >= kAttnSliceMinCap, with a workspace): the same one-token
+// attention with each query head's keys cut into slices of one wave round (KB keys,
+// lb_attn.h) on one-wave workgroups, grid KV x H/KV x NS, so that a head's keys
+// stream through NS compute units instead of one. Workgroup (g, j, sl) takes the
+// rounds sl, sl + NS, ... below S and stores its (p * v, max, sum) partial;
+// attention_merge_kernel combines them after the kernel boundary (no fence, no
+// counter: an in-kernel merge through an agent-scope fence and an atomic cost more
+// than the split saved). Slices past the keys in use return after reading *pos,
+// before loading anything. Rotation and the cache write are those of
+// attention_decode_kernel.
+template <int D>
+__global__ __launch_bounds__(kWave) void attention_slice_kernel(
+    const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
+    const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc, float *__restrict__ vc, int cap,
+    float *__restrict__ part) {
+  using Cfg = AttnCfg<D>;
+  constexpr int LPR = Cfg::kLPR, RPL = Cfg::kRPL, U = Cfg::kU, KB = Cfg::kKB, PS = D + 4;
+  const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
+  const int sl = blockIdx.z, NS = gridDim.z;
+  const int lane = threadIdx.x, r = lane / LPR, e4 = lane % LPR;
+  const float *kb = kc + (size_t)g * cap * D;
+  const float *vb = vc + (size_t)g * cap * D;
+  const int p = *pos;
+  const int pc = p < 0 ? 0 : (p < max_pos ? p : max_pos - 1);
+  const bool newk = p >= 0 && p < cap;
+  const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
+  const int Sc = newk ? S - 1 : S;
+  int nact = (S + KB - 1) / KB;
+  nact = nact < 1 ? 1 : (nact < NS ? nact : NS);
+  if (sl >= nact) return;
+  AttnRound<D> rd;
+  attn_load_round<D>(rd, kb, vb, KB * sl, cap);
+  const float4 q4 = rope4<D>(qkv + (size_t)h * D, cosT, sinT, pc, e4);
+  const float4 kn4 = rope4<D>(qkv + (size_t)(H + g) * D, cosT, sinT, pc, e4);
+  const float4 vn4 = *reinterpret_cast<const float4 *>(qkv + (size_t)(H + KV + g) * D + 4 * e4);
+  if (newk && j == 0 && sl == 0 && r == 0) {
+    *reinterpret_cast<float4 *>(kc + ((size_t)g * cap + p) * D + 4 * e4) = kn4;
+    *reinterpret_cast<float4 *>(vc + ((size_t)g * cap + p) * D + 4 * e4) = vn4;
+  }
+  const float scale = 1.0f / sqrtf((float)D);
+  float m = -INFINITY, l = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int c = sl; KB * c < S; c += NS) {
+    const int k0 = KB * c;
+    if (c != sl) attn_load_round<D>(rd, kb, vb, k0, cap);
+    float sc[U];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int row = k0 + RPL * u + r;
+      const float4 kk = (newk && row == Sc) ? kn4 : rd.k[u];
+      float d = q4.x * kk.x;
+      d = __builtin_fmaf(q4.y, kk.y, d);
+      d = __builtin_fmaf(q4.z, kk.z, d);
+      d = __builtin_fmaf(q4.w, kk.w, d);
+      d = group_sum<LPR>(d) * scale;
+      sc[u] = row < S ? d : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
+    }
+    const float mnew = fmaxf(m, wave_max(mx));  // the round has a key below S: row k0
+    const float alpha = expf(m - mnew);         // 0 on the first round
+    m = mnew;
+    l *= alpha;
+    acc.x *= alpha;
+    acc.y *= alpha;
+    acc.z *= alpha;
+    acc.w *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int row = k0 + RPL * u + r;
+      const float pr = expf(sc[u] - m);
+      // masked rows may hold anything, NaN included: their values are replaced
+      const float4 vv = row < S ? ((newk && row == Sc) ? vn4 : rd.v[u]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      l += pr;
+      acc.x = __builtin_fmaf(pr, vv.x, acc.x);
+      acc.y = __builtin_fmaf(pr, vv.y, acc.y);
+      acc.z = __builtin_fmaf(pr, vv.z, acc.z);
+      acc.w = __builtin_fmaf(pr, vv.w, acc.w);
+    }
+  }
+  acc.x = column_sum<LPR>(acc.x);
+  acc.y = column_sum<LPR>(acc.y);
+  acc.z = column_sum<LPR>(acc.z);
+  acc.w = column_sum<LPR>(acc.w);
+  l = column_sum<LPR>(l);
+  float *pp = part + ((size_t)h * NS + sl) * PS;
+  if (r == 0) *reinterpret_cast<float4 *>(pp + 4 * e4) = acc;
+  if (lane == 0) {
+    pp[D] = m;
+    pp[D + 1] = l;
+  }
+}
+
+// out[h] = the slices' partials of head h combined:
+// sum_s acc_s exp(m_s - M) / sum_s l_s exp(m_s - M), M = max_s m_s. One wave per
+// head; every load is issued before the first wait (lane s holds slice s's max and
+// sum, and the partial vectors are read for all kAttnMaxSplit slots, slots past the
+// active slices re-reading the last one with weight 0), so the merge costs one
+// round trip, not one per slice.
+template <int D>
+__global__ __launch_bounds__(kWave) void attention_merge_kernel(const int32_t *__restrict__ pos, int cap, int NS,
+                                                                const float *__restrict__ part,
+                                                                float *__restrict__ out) {
+  static_assert(kAttnMaxSplit <= kWave, "one lane per slice");
+  constexpr int KB = AttnCfg<D>::kKB, PS = D + 4, LPR = D / 4;
+  const int h = blockIdx.x, lane = threadIdx.x, e4 = lane % LPR;
+  const int p = *pos;
+  const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
+  int nact = (S + KB - 1) / KB;
+  nact = nact < 1 ? 1 : (nact < NS ? nact : NS);
+  const float *ph = part + (size_t)h * NS * PS;
+  const int sl = lane < nact ? lane : nact - 1;
+  float4 a[kAttnMaxSplit];
+#pragma unroll
+  for (int s = 0; s < kAttnMaxSplit; s++)
+    a[s] = *reinterpret_cast<const float4 *>(ph + (size_t)(s < nact ? s : nact - 1) * PS + 4 * e4);
+  const float ms = ph[(size_t)sl * PS + D], ls = ph[(size_t)sl * PS + D + 1];
+  const float M = wave_max(lane < nact ? ms : -INFINITY);
+  const float f = lane < nact ? expf(ms - M) : 0.0f;
+  const float den = wave_sum(ls * f);
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int s = 0; s < kAttnMaxSplit; s++) {
+    const float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s));  // 0 past the active slices
+    num.x = __builtin_fmaf(a[s].x, fs, num.x);
+    num.y = __builtin_fmaf(a[s].y, fs, num.y);
+    num.z = __builtin_fmaf(a[s].z, fs, num.z);
+    num.w = __builtin_fmaf(a[s].w, fs, num.w);
+  }
+  if (lane < LPR)
+    *reinterpret_cast<float4 *>(out + (size_t)h * D + 4 * e4) =
+        make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+}
+
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
 // max-combined (the one argmax_kernel would pick from the logits); advances *pos
 // and records hist[*pos] like argmax_kernel, and clears every slot for the next
@@ -386,21 +522,27 @@ hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int 
 
 hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
                                    const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
-                                   hipStream_t s) {
+                                   float *work, hipStream_t s) {
   if (KV <= 0 || H % KV || H / KV > kAttnMaxGroup || cap <= 0) return hipErrorInvalidValue;
-  const dim3 grid(KV, H / KV);
-  if (D == 32)
-    hipLaunchKernelGGL(attention_decode_kernel<32>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
-                       max_pos, kc, vc, cap, out);
-  else if (D == 64)
-    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
-                       max_pos, kc, vc, cap, out);
-  else if (D == 128)
-    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
-                       max_pos, kc, vc, cap, out);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  auto go = [&](auto dc) -> hipError_t {
+    constexpr int DD = decltype(dc)::value;
+    if (work && cap >= kAttnSliceMinCap) {
+      const int ns = attn_slices(DD, cap);
+      hipLaunchKernelGGL(attention_slice_kernel<DD>, dim3(KV, H / KV, ns), dim3(kWave), 0, s, qkv, H, KV, cosT,
+                         sinT, pos, max_pos, kc, vc, cap, work);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(attention_merge_kernel<DD>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, work, out);
+    } else {
+      hipLaunchKernelGGL(attention_decode_kernel<DD>, dim3(KV, H / KV), dim3(kAttThreads), 0, s, qkv, H, KV, cosT,
+                         sinT, pos, max_pos, kc, vc, cap, out);
+    }
+    return hipGetLastError();
+  };
+  if (D == 32) return go(std::integral_constant<int, 32>{});
+  if (D == 64) return go(std::integral_constant<int, 64>{});
+  if (D == 128) return go(std::integral_constant<int, 128>{});
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist,

@@ -136,6 +136,9 @@ SIGNATURES = {
     "lbd_gemv_w4a8_fused": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, C.c_void_p, _vp], _int),
     "lbd_argmax_finalize": ([_vp, _vp, _vp, _int, _vp, _int, _vp], _int),
     "lbd_attention_decode": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _vp], _int),
+    "lbd_attention_decode_ws": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _vp, _sz, _vp],
+                                _int),
+    "lbd_attention_decode_work_bytes": ([_int, _int, _int], _sz),
     "lbd_gemm_w4a16_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_gemm_w4a8_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_quantize_int4_g32": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),

@@ -144,6 +144,10 @@ class KVCache:
         self.k = [_buf(nb) for _ in range(cfg.num_layers)]
         self.v = [_buf(nb) for _ in range(cfg.num_layers)]
         self.length = 0
+        # partial sums of the one-token attention's key slices (long caches; the
+        # layers use it in turn on the model's stream)
+        wb = K.lib().lbd_attention_decode_work_bytes(cfg.num_heads, cfg.head_dim, self.capacity)
+        self.attn_work = _buf(wb)
 
 
 @dataclass
@@ -312,9 +316,10 @@ class Model:
         for li, ly in enumerate(self.layers):
             self._fused_linear(ly.qkv, x, self.qkv.ptr, norm=ly.ln1.ptr,
                                bias=None if ly.qkv_bias is None else ly.qkv_bias.ptr)
-            _check(L.lbd_attention_decode(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
-                                          cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
-                                          self.att.ptr, s), "attention decode")
+            _check(L.lbd_attention_decode_ws(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
+                                             cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
+                                             self.att.ptr, cache.attn_work.ptr, cache.attn_work.nbytes, s),
+                   "attention decode")
             self._fused_linear(ly.o, self.att.ptr, x, res=x)
             self._fused_linear(ly.gate_up, x, self.m.ptr, norm=ly.ln2.ptr, glu=True)
             self._fused_linear(ly.down, self.m.ptr, x, res=x)

@@ -291,11 +291,19 @@ def attention_one(qkv, kc, vc, p, H, KV, D, cos, sin):
     return out.reshape(-1), k, v
 
 
+# one round, several, a small position in a large cache, p >= cap; from cap = 1024
+# the workspace entry point takes key slices (one, several, several rounds each at
+# p = 15999: 250 rounds over 32 slices)
 @pytest.mark.parametrize("D,H,KV,p,cap", [(64, 14, 2, 0, 8), (64, 14, 2, 191, 192), (64, 14, 2, 255, 300),
                                           (64, 14, 2, 256, 300), (32, 8, 1, 37, 64), (128, 4, 4, 700, 1000),
                                           (64, 16, 1, 5, 16), (64, 2, 2, 20, 20), (64, 14, 2, 15999, 16000),
-                                          (64, 14, 2, 70, 16000), (32, 8, 2, 300, 301), (128, 8, 8, 4000, 4000)])
-def test_attention_decode(rng, D, H, KV, p, cap):
+                                          (64, 14, 2, 70, 16000), (32, 8, 2, 300, 301), (128, 8, 8, 4000, 4000),
+                                          (64, 14, 2, 1023, 1024), (64, 14, 2, 40, 1024), (32, 16, 4, 5000, 5000),
+                                          (128, 14, 2, 2100, 3000)])
+@pytest.mark.parametrize("ws", [False, True])
+def test_attention_decode(rng, D, H, KV, p, cap, ws):
+    """ws: lbd_attention_decode_ws with a workspace, i.e. key slices on many
+    workgroups and a merge launch for caches of 1024 positions and more."""
     L = K.lib()
     width = (H + 2 * KV) * D
     qkv = rng.standard_normal(width).astype(np.float32)
@@ -305,8 +313,14 @@ def test_attention_decode(rng, D, H, KV, p, cap):
     cos, sin = DM.rope_tables(D, max_pos, 10000.0)
     dk, dv, out = up(kc0), up(vc0), K.DeviceBuffer(4 * H * D)
     dcos, dsin, dpos = up(cos), up(sin), up(np.array([p], np.int32))
-    ok(L.lbd_attention_decode(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, dpos.ptr, max_pos, dk.ptr, dv.ptr, cap,
-                              out.ptr, None))
+    if ws:
+        work = K.DeviceBuffer(L.lbd_attention_decode_work_bytes(H, D, cap))
+        _LIVE.append(work)
+        ok(L.lbd_attention_decode_ws(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, dpos.ptr, max_pos, dk.ptr, dv.ptr,
+                                     cap, out.ptr, work.ptr, work.nbytes, None))
+    else:
+        ok(L.lbd_attention_decode(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, dpos.ptr, max_pos, dk.ptr, dv.ptr, cap,
+                                  out.ptr, None))
     ref, k, v = attention_one(qkv, kc0, vc0, p, H, KV, D, cos, sin)
     got = out.to_array((H * D,), np.float32)
     assert np.abs(got - ref).max() <= 2e-5 * max(np.abs(vc0).max(), np.abs(v).max())
@@ -327,23 +341,26 @@ def test_attention_decode(rng, D, H, KV, p, cap):
     np.testing.assert_array_equal(vc[:, others], vc0[:, others])
 
 
-def test_attention_decode_consecutive_positions(rng):
-    """A run of decode positions on one cache (as the decoder's graph replays it):
-    every step matches the float64 attention, and each step's cache row is there
-    for the next."""
+@pytest.mark.parametrize("cap", [600, 2000])
+def test_attention_decode_consecutive_positions(rng, cap):
+    """A run of decode positions on one cache (as the decoder's graph replays it),
+    through the workspace entry point (key slices from cap = 1024): every step
+    matches the float64 attention, and each step's cache row is there for the next."""
     L = K.lib()
-    D, H, KV, cap = 64, 14, 2, 600
-    max_pos = 1024
+    D, H, KV = 64, 14, 2
+    max_pos = 2048
+    work = K.DeviceBuffer(L.lbd_attention_decode_work_bytes(H, D, cap))
+    _LIVE.append(work)
     cos, sin = DM.rope_tables(D, max_pos, 10000.0)
     kc = rng.standard_normal((KV, cap, D)).astype(np.float32)
     vc = rng.standard_normal((KV, cap, D)).astype(np.float32)
     dk, dv, out = up(kc), up(vc), K.DeviceBuffer(4 * H * D)
     _LIVE.append(out)
     dcos, dsin = up(cos), up(sin)
-    for p in (0, 1, 63, 64, 65, 255, 256, 300, 599):
+    for p in (0, 1, 63, 64, 65, 255, 256, 300, 599, cap - 1, cap + 5):
         qkv = rng.standard_normal((H + 2 * KV) * D).astype(np.float32)
-        ok(L.lbd_attention_decode(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, up(np.array([p], np.int32)).ptr,
-                                  max_pos, dk.ptr, dv.ptr, cap, out.ptr, None))
+        ok(L.lbd_attention_decode_ws(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, up(np.array([p], np.int32)).ptr,
+                                     max_pos, dk.ptr, dv.ptr, cap, out.ptr, work.ptr, work.nbytes, None))
         ref, k, v = attention_one(qkv, kc, vc, p, H, KV, D, cos, sin)
         got = out.to_array((H * D,), np.float32)
         assert np.abs(got - ref).max() <= 2e-5 * max(np.abs(vc).max(), np.abs(v).max()), p
@@ -360,6 +377,10 @@ def test_attention_decode_argument_checks():
     assert L.lbd_attention_decode(*args(14, 2, 48, 8)) == -1   # head_dim
     assert L.lbd_attention_decode(*args(14, 2, 64, 16001)) == -1
     assert L.lbd_attention_decode(*args(14, 2, 64, 8)) == 0
+    wb = L.lbd_attention_decode_work_bytes(14, 64, 2048)
+    w = up(np.zeros(wb // 4, np.float32))
+    assert L.lbd_attention_decode_ws(b.ptr, 14, 2, 64, b.ptr, b.ptr, pos.ptr, 8, w.ptr, w.ptr, 2048, b.ptr, w.ptr,
+                                     wb - 16, None) == -6   # workspace too small
 
 
 # ---------------------------------------------------------------- the model: fused = unfused
