@@ -308,6 +308,14 @@ typedef struct {
    * the epilogue instead of once per workgroup in the next GEMV's SwiGLU prologue.
    * Excludes residual and argmax_key. */
   int glu;
+  /* attention-merge prologue (M == 1, no other prologue): the activation row is the
+   * one-token attention output, Kp = heads x attn_head_dim <= 2048, merged from the
+   * key-slice partials that lbd_attention_slices wrote to attn_part for a cache of
+   * attn_cap positions (at most 8 slices: attn_cap <= 8 * 4096 / attn_head_dim);
+   * the result is bit for bit lbd_attention_merge's. x is not read (may be NULL). */
+  const float *attn_part;
+  int attn_cap;
+  int attn_head_dim;
 } lbd_fusion;
 #define LBD_ARGMAX_SLOTS 1024
 int lbd_gemv_w4a16_fused(const float *x, int M, int Kp, const uint8_t *qw, const float *scales,
@@ -337,6 +345,17 @@ int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *co
  * lbd_attention_decode_work_bytes(H, D, cap) bytes, 16-byte aligned (out too); calls
  * sharing it must be ordered (one stream). */
 size_t lbd_attention_decode_work_bytes(int H, int D, int cap);
+/* The two halves of the key-slice path, for callers that merge elsewhere (the
+ * attention-merge prologue of the fused GEMVs): lbd_attention_slices rotates, writes
+ * the caches and stores every slice's partial to `part` (min(ceil(cap / (4096 / D)),
+ * 32) slices per head, lbd_attention_decode_work_bytes(H, D, cap) bytes; slices past
+ * the keys in use store empty partials); lbd_attention_merge combines them into out. */
+int lbd_attention_slices(const float *qkv, int H, int KV, int D, const float *cos_table,
+                         const float *sin_table, const int32_t *pos, int max_pos,
+                         float *k_cache, float *v_cache, int cap, float *part,
+                         size_t part_bytes, void *stream);
+int lbd_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap,
+                        float *out, void *stream);
 int lbd_attention_decode_ws(const float *qkv, int H, int KV, int D, const float *cos_table,
                             const float *sin_table, const int32_t *pos, int max_pos,
                             float *k_cache, float *v_cache, int cap, float *out, void *work,

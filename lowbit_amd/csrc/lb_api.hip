@@ -699,6 +699,18 @@ int fused_args(int fmt, const lbd_fusion *f, lbk::GemmArgs &a) {
   if (f->glu && (f->residual || f->argmax_key))
     return fail(LB_ERR_ARG, "the glu epilogue excludes the residual and the argmax key");
   if (f->glu && (a.N & 1)) return fail(LB_ERR_SHAPE, "the glu epilogue takes an even N (gate/up row pairs)");
+  if (f->attn_part) {
+    const int D = f->attn_head_dim;
+    if (a.M != 1 || f->norm_w || f->swiglu)
+      return fail(LB_ERR_ARG, "the attention-merge prologue needs M == 1 and no other prologue");
+    if ((D != 32 && D != 64 && D != 128) || a.Kp % D || a.Kp > 2048 || f->attn_cap <= 0 ||
+        f->attn_cap > 16000 || lbk::attn_slices(D, f->attn_cap) > lbk::kAttnMaxFusedSlices)
+      return fail(LB_ERR_SHAPE, "attention merge: Kp = heads x head_dim <= 2048, at most 8 key slices");
+    if (!aligned16(f->attn_part)) return fail(LB_ERR_ARG, "attn_part must be 16-byte aligned");
+    a.attn_part = f->attn_part;
+    a.attn_ns = lbk::attn_slices(D, f->attn_cap);
+    a.attn_d = D;
+  }
   a.norm_w = f->norm_w;
   a.norm_eps = f->norm_eps;
   a.swiglu = f->swiglu != 0;
@@ -726,8 +738,8 @@ int lbd_gemv_w4a16_fused(const float *x, int M, int Kp, const uint8_t *qw, const
                          const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream) {
   int rc = check_shape(M, Kp, N, LB_GROUP);
   if (rc < 0) return rc;
-  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
-  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  if ((!x && !(f && f->attn_part)) || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if ((x && !aligned16(x)) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
   lbk::GemmArgs a;
   a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
   a.M = M; a.Kp = Kp; a.N = N;
@@ -739,8 +751,8 @@ int lbd_gemv_mxfp4_fused(const float *x, int M, int Kp, const uint8_t *qw, const
                          int N, float *y, const lbd_fusion *f, void *stream) {
   int rc = check_shape(M, Kp, N, LB_MXBLOCK);
   if (rc < 0) return rc;
-  if (!x || !qw || !e8m0 || !y) return fail(LB_ERR_ARG, "null pointer");
-  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  if ((!x && !(f && f->attn_part)) || !qw || !e8m0 || !y) return fail(LB_ERR_ARG, "null pointer");
+  if ((x && !aligned16(x)) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
   lbk::GemmArgs a;
   a.x = x; a.qw = qw; a.e8m0 = e8m0; a.y = y;
   a.M = M; a.Kp = Kp; a.N = N;
@@ -752,8 +764,8 @@ int lbd_gemv_w4a8_fused(const float *x, int M, int Kp, const uint8_t *qw, const 
                         const uint8_t *zeros, int N, float *y, const lbd_fusion *f, void *stream) {
   int rc = check_shape(M, Kp, N, LB_GROUP);
   if (rc < 0) return rc;
-  if (!x || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
-  if (!aligned16(x) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
+  if ((!x && !(f && f->attn_part)) || !qw || !scales || !y) return fail(LB_ERR_ARG, "null pointer");
+  if ((x && !aligned16(x)) || !aligned16(qw)) return fail(LB_ERR_ARG, "x and qw must be 16-byte aligned");
   lbk::GemmArgs a;
   a.x = x; a.qw = qw; a.scales = scales; a.zeros = zeros; a.y = y;
   a.M = M; a.Kp = Kp; a.N = N;
@@ -856,6 +868,32 @@ int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *co
 size_t lbd_attention_decode_work_bytes(int H, int D, int cap) {
   if (H <= 0 || (D != 32 && D != 64 && D != 128) || cap <= 0) return 0;
   return lbk::attn_work_bytes(H, D, cap);
+}
+
+int lbd_attention_slices(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,
+                         const int32_t *pos, int max_pos, float *k_cache, float *v_cache, int cap, float *part,
+                         size_t part_bytes, void *stream) {
+  if (H <= 0 || KV <= 0 || H % KV || H / KV > lbk::kAttnMaxGroup || (D != 32 && D != 64 && D != 128) ||
+      max_pos <= 0 || cap <= 0 || cap > 16000)
+    return fail(LB_ERR_SHAPE, "bad shape");
+  if (!qkv || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !part)
+    return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(qkv) || !aligned16(cos_table) || !aligned16(sin_table) || !aligned16(k_cache) ||
+      !aligned16(v_cache) || !aligned16(part))
+    return fail(LB_ERR_ARG, "qkv, the tables, the caches and part must be 16-byte aligned");
+  if (part_bytes < lbk::attn_work_bytes(H, D, cap))
+    return fail(LB_ERR_ARG, "part smaller than lbd_attention_decode_work_bytes");
+  LB_LAUNCH(lbk::launch_attention_slices(qkv, H, KV, D, cos_table, sin_table, pos, max_pos, k_cache, v_cache, cap,
+                                         part, static_cast<hipStream_t>(stream)),
+            "attention slices launch");
+}
+
+int lbd_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap, float *out, void *stream) {
+  if (H <= 0 || (D != 32 && D != 64 && D != 128) || cap <= 0 || cap > 16000) return fail(LB_ERR_SHAPE, "bad shape");
+  if (!part || !pos || !out) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(part) || !aligned16(out)) return fail(LB_ERR_ARG, "part and out must be 16-byte aligned");
+  LB_LAUNCH(lbk::launch_attention_merge(part, H, D, pos, cap, out, static_cast<hipStream_t>(stream)),
+            "attention merge launch");
 }
 
 int lbd_attention_decode_ws(const float *qkv, int H, int KV, int D, const float *cos_table, const float *sin_table,

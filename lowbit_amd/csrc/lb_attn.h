@@ -29,6 +29,12 @@ struct AttnCfg {
   static constexpr int kKB = kU * kRPL;       // keys per wave and round
 };
 
+// Key slices (of KB keys) that hold keys below S, at least one, at most NS.
+__host__ __device__ __forceinline__ int attn_active_slices(int S, int KB, int NS) {
+  const int n = (S + KB - 1) / KB;
+  return n < 1 ? 1 : (n < NS ? n : NS);
+}
+
 // Registers holding one round of a wave's key and value rows.
 template <int D>
 struct AttnRound {
@@ -182,6 +188,76 @@ __device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, f
     }
     out[e] = num / den;
   }
+}
+
+// Partials of up to 8 key slices of one head, for the float4 at elements 4 e4 ..:
+// p * v, max and sum of each (attn_fetch8), combined by attn_combine8.
+struct AttnPart8 {
+  float4 a[8];
+  float m[8], l[8];
+};
+
+// Slices s0 .. s0 + 7 of the head's partials ph (PS floats each: p * v [D], max,
+// sum; ph and PS keep every partial 16-byte aligned); slots past slice n - 1 read
+// slice n - 1 again. All loads issued together.
+__device__ __forceinline__ void attn_fetch8(AttnPart8 &q, const float *ph, int PS, int D, int s0, int n, int e4) {
+#pragma unroll
+  for (int b = 0; b < 8; b++) {
+    const int s = s0 + b < n ? s0 + b : n - 1;
+    q.a[b] = *reinterpret_cast<const float4 *>(ph + (size_t)s * PS + 4 * e4);
+    const float2 ml = *reinterpret_cast<const float2 *>(ph + (size_t)s * PS + D);  // max and sum: one load
+    q.m[b] = ml.x;
+    q.l[b] = ml.y;
+  }
+}
+
+// Adds slices s0 .. min(s0 + 8, n) - 1 of q, weighted by exp(m - M), to num / den
+// in slice order.
+__device__ __forceinline__ void attn_combine8(const AttnPart8 &q, int s0, int n, float M, float4 &num, float &den) {
+#pragma unroll
+  for (int b = 0; b < 8; b++) {
+    if (s0 + b >= n) break;
+    const float f = expf(q.m[b] - M);
+    num.x = __builtin_fmaf(q.a[b].x, f, num.x);
+    num.y = __builtin_fmaf(q.a[b].y, f, num.y);
+    num.z = __builtin_fmaf(q.a[b].z, f, num.z);
+    num.w = __builtin_fmaf(q.a[b].w, f, num.w);
+    den = __builtin_fmaf(q.l[b], f, den);
+  }
+}
+
+// The merged float4 of at most 8 slices already fetched: sum_s acc_s f_s /
+// sum_s l_s f_s, f_s = exp(m_s - M), M = max_s m_s.
+__device__ __forceinline__ float4 attn_merge8(const AttnPart8 &q, int n) {
+  float M = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < 8; b++) M = fmaxf(M, q.m[b]);  // repeats of the last slice change nothing
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float den = 0.0f;
+  attn_combine8(q, 0, n, M, num, den);
+  return make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+}
+
+// Elements 4 e4 .. 4 e4 + 3 of one head's attention output from the partials of its
+// n key slices (the same arithmetic as attn_merge8 for n <= 8, where it is one
+// round trip; more slices take two passes of 8 at a time).
+__device__ __forceinline__ float4 attn_merge4(const float *ph, int PS, int D, int n, int e4) {
+  AttnPart8 q;
+  attn_fetch8(q, ph, PS, D, 0, n, e4);
+  if (n <= 8) return attn_merge8(q, n);
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < n; s0 += 8) {
+    if (s0) attn_fetch8(q, ph, PS, D, s0, n, e4);
+#pragma unroll
+    for (int b = 0; b < 8; b++) M = fmaxf(M, q.m[b]);
+  }
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float den = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += 8) {
+    attn_fetch8(q, ph, PS, D, s0, n, e4);
+    attn_combine8(q, s0, n, M, num, den);
+  }
+  return make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
 }
 
 // Rotate the pair (x1, x2) of element i of a head at the table row pc

@@ -4,6 +4,7 @@
 // templates only; the host entry points are declared in lb_internal.h.
 #pragma once
 
+#include "lb_attn.h"
 #include "lb_device.h"
 #include "lb_internal.h"
 
@@ -250,7 +251,9 @@ struct GemvMinWaves {
 
 // PRO selects a fused prologue on the (single, register-held) activation row:
 // 0 none, 1 RMSNorm (x * (1 / sqrt(mean(x^2) + eps)) * norm_w, the mean over Kp),
-// 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up). The epilogue
+// 2 SwiGLU (the row is [gate | up], Kp floats each: silu(gate) * up), 3 attention
+// merge (the row is merged from one-token attention partials, attn_merge8: every
+// thread's partials are requested before the weights, rows up to 2048). The epilogue
 // adds `bias` and `res` when given and max-combines argmax keys into `amax_key`;
 // under `glu` it writes silu(gate) * up of each (gate, up) row pair instead.
 // HW (rows of at most 1024 elements, one activation row): every wave load covers
@@ -290,8 +293,14 @@ void gemv_kernel(GemmArgs a) {
   constexpr bool kXReg = (F != F_W4A8Q) && MB * S <= kXRegs;
   static_assert(PRO == 0 || (MB == 1 && kXReg), "prologues take one register-held activation row");
   float4 xr[kXReg ? MB * S : 1];
-  float4 xe[PRO ? S : 1];  // RMSNorm weights, or the up half of a SwiGLU row
-  if constexpr (kXReg) {
+  float4 xe[(PRO == 1 || PRO == 2) ? S : 1];  // RMSNorm weights, or the up half of a SwiGLU row
+  static_assert(PRO != 3 || S == 1, "the attention-merge prologue takes rows up to 2048 elements");
+  AttnPart8 apt[1];  // attention merge: the partials of this thread's float4
+  if constexpr (PRO == 3) {
+    // this thread's float4 belongs to head e / D: all its slices' partials
+    const int e = threadIdx.x * 4, D = a.attn_d, PS = D + 4;
+    if (e < Kp) attn_fetch8(apt[0], a.attn_part + (size_t)(e / D) * a.attn_ns * PS, PS, D, 0, a.attn_ns, (e % D) / 4);
+  } else if constexpr (kXReg) {
 #pragma unroll
     for (int m = 0; m < MB; m++) {
       const Rsrc rx = make_rsrc(a.x + (size_t)m * Kp, (uint32_t)Kp * 4);
@@ -351,6 +360,8 @@ void gemv_kernel(GemmArgs a) {
       xr[i].z = xr[i].z * rn * xe[i].z;
       xr[i].w = xr[i].w * rn * xe[i].w;
     }
+  } else if constexpr (PRO == 3) {
+    xr[0] = threadIdx.x * 4 < Kp ? attn_merge8(apt[0], a.attn_ns) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   } else if constexpr (PRO == 2) {
 #pragma unroll
     for (int i = 0; i < S; i++) {
@@ -559,12 +570,16 @@ static GemvFn pick_gemv(int nit, int nch, int rpw) {
   if constexpr (MB == 1 && !fmt_g32(F)) {
     if (nch <= kWave / 2 && rpw >= 2) return pick_gemv_hw<F, PRO>(rpw);
   }
-  if (nit <= 1) return pick_gemv_nit<F, MB, 1, PRO>(rpw);
-  if (nit <= 2) return pick_gemv_nit<F, MB, 2, PRO>(rpw);
-  if (nit <= 4) return pick_gemv_nit<F, MB, 4, PRO>(rpw);
-  // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
-  if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return nullptr;
-  else return pick_gemv_nit<F, MB, 8, PRO>(rpw);
+  if constexpr (PRO == 3) {
+    return nit <= 1 ? pick_gemv_nit<F, MB, 1, PRO>(rpw) : nullptr;
+  } else {
+    if (nit <= 1) return pick_gemv_nit<F, MB, 1, PRO>(rpw);
+    if (nit <= 2) return pick_gemv_nit<F, MB, 2, PRO>(rpw);
+    if (nit <= 4) return pick_gemv_nit<F, MB, 4, PRO>(rpw);
+    // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
+    if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return nullptr;
+    else return pick_gemv_nit<F, MB, 8, PRO>(rpw);
+  }
 }
 
 // Persistent grid of at most two workgroups per CU, fewer when there are few rows.
@@ -606,7 +621,9 @@ static hipError_t launch_gemv_f(const GemmArgs &a, int num_cus, size_t lds, hipS
     // the prologues act on fp32 rows, and the group-32 formats have none
     if constexpr (F == F_W4A8Q || fmt_g32(F)) return hipErrorInvalidValue;
     else if (pro == 1) return launch_gemv_mb<F, 1, 1>(a, num_cus, lds, s);
-    else return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s);
+    else if (pro == 2) return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s);
+    else if (a.Kp > kWave * 32) return hipErrorInvalidValue;  // one chunk per lane
+    else return launch_gemv_mb<F, 1, 3>(a, num_cus, lds, s);
   }
   switch (a.M) {
     case 1: return launch_gemv_mb<F, 1, 0>(a, num_cus, lds, s);

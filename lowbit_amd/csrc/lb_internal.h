@@ -35,6 +35,10 @@ struct GemmArgs {
   const float *norm_w = nullptr;  // RMSNorm of the activation row over Kp elements, times norm_w
   float norm_eps = 0.0f;
   bool swiglu = false;            // x row is [gate (Kp) | up (Kp)]; the activation is silu(gate) * up
+  // the activation row is the one-token attention output (Kp = heads x attn_d) merged
+  // from attn_ns key-slice partials [heads][attn_ns][attn_d + 4] (x is not read)
+  const float *attn_part = nullptr;
+  int attn_ns = 0, attn_d = 0;
   // Epilogue: y = res + (x . w^T + bias); res may alias y.
   const float *bias = nullptr;    // [N]
   const float *res = nullptr;     // [M, N]
@@ -46,8 +50,8 @@ struct GemmArgs {
 // slot count), so that no single address serialises thousands of atomics.
 constexpr int kArgmaxSlots = 1024;
 
-// Prologue of a fused GEMV: 0 none, 1 RMSNorm, 2 SwiGLU.
-inline int gemv_prologue(const GemmArgs &a) { return a.norm_w ? 1 : (a.swiglu ? 2 : 0); }
+// Prologue of a fused GEMV: 0 none, 1 RMSNorm, 2 SwiGLU, 3 attention merge.
+inline int gemv_prologue(const GemmArgs &a) { return a.norm_w ? 1 : (a.swiglu ? 2 : (a.attn_part ? 3 : 0)); }
 
 // MFMA tile layout ("t16") of int4 g128 weights, a device-private copy of the
 // packed matrix in the order the int8 MFMA path consumes it. With S = ceil(N/16)
@@ -129,10 +133,12 @@ hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t
 // With a workspace and a cache of at least kAttnSliceMinCap positions, each query
 // head's keys are cut into slices of one wave round (4096 / D keys), at most
 // kAttnMaxSplit per head, whose partials [H][slices][D + 4] floats a second kernel
+// (or a fused GEMV's attention-merge prologue, up to kAttnMaxFusedSlices slices)
 // merges; otherwise one workgroup per query head (work may be null).
 constexpr int kAttnMaxGroup = 16;     // query heads per KV head
 constexpr int kAttnMaxSplit = 32;     // key slices per head
 constexpr int kAttnSliceMinCap = 1024;
+constexpr int kAttnMaxFusedSlices = 8;
 inline int attn_slices(int D, int cap) {
   const int kb = 64 * 64 / D;
   const int n = (cap + kb - 1) / kb;
@@ -144,5 +150,10 @@ inline size_t attn_work_bytes(int H, int D, int cap) {
 hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
                                    const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
                                    float *work, hipStream_t s);
+hipError_t launch_attention_slices(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
+                                   const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *part,
+                                   hipStream_t s);
+hipError_t launch_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap, float *out,
+                                  hipStream_t s);
 
 }  // namespace lbk

@@ -215,16 +215,20 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
   attn_run<D, kAttThreads>(pre, q4, kn4, vn4, kb, vb, S, Sc, newk, cap, sh, out + (size_t)h * D);
 }
 
-// Long caches (cap >= kAttnSliceMinCap, with a workspace): the same one-token
-// attention with each query head's keys cut into slices of one wave round (KB keys,
-// lb_attn.h) on one-wave workgroups, grid KV x H/KV x NS, so that a head's keys
-// stream through NS compute units instead of one. Workgroup (g, j, sl) takes the
-// rounds sl, sl + NS, ... below S and stores its (p * v, max, sum) partial;
-// attention_merge_kernel combines them after the kernel boundary (no fence, no
-// counter: an in-kernel merge through an agent-scope fence and an atomic cost more
-// than the split saved). Slices past the keys in use return after reading *pos,
-// before loading anything. Rotation and the cache write are those of
-// attention_decode_kernel.
+// Key slices: the same one-token attention with each query head's keys cut into
+// slices of one wave round (KB keys, lb_attn.h) on one-wave workgroups, grid
+// KV x H/KV x NS, so that a head's keys stream through NS compute units instead of
+// one. Workgroup (g, j, sl) takes the rounds sl, sl + NS, ... below S and stores
+// its (p * v, max, sum) partial; attention_merge_kernel (long caches) or the fused
+// GEMVs' attention-merge prologue (the decoder's o projection) combines them after
+// the kernel boundary (no fence, no counter: an in-kernel merge through an
+// agent-scope fence and an atomic cost more than the split saved). The slices
+// holding keys below 256 request their first round before *pos arrives; slices
+// past the keys in use store an empty partial (max -inf, sum 0) without loading
+// anything, so that a merge may take all slices. Rotation and the cache write are
+// those of attention_decode_kernel.
+constexpr int kAttnPrefetchKeys = 256;
+
 template <int D>
 __global__ __launch_bounds__(kWave) void attention_slice_kernel(
     const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
@@ -237,16 +241,26 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   const int lane = threadIdx.x, r = lane / LPR, e4 = lane % LPR;
   const float *kb = kc + (size_t)g * cap * D;
   const float *vb = vc + (size_t)g * cap * D;
+  // the slices holding keys below 256 request their first round before *pos arrives
+  AttnRound<D> rd;
+  const bool early = KB * sl < kAttnPrefetchKeys;
+  if (early) attn_load_round<D>(rd, kb, vb, KB * sl, cap);
   const int p = *pos;
   const int pc = p < 0 ? 0 : (p < max_pos ? p : max_pos - 1);
   const bool newk = p >= 0 && p < cap;
   const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
   const int Sc = newk ? S - 1 : S;
-  int nact = (S + KB - 1) / KB;
-  nact = nact < 1 ? 1 : (nact < NS ? nact : NS);
-  if (sl >= nact) return;
-  AttnRound<D> rd;
-  attn_load_round<D>(rd, kb, vb, KB * sl, cap);
+  float *pp = part + ((size_t)h * NS + sl) * PS;
+  if (sl >= attn_active_slices(S, KB, NS)) {
+    // no key: an empty partial (weight exp(-inf) = 0 in any merge over all slices)
+    if (r == 0) *reinterpret_cast<float4 *>(pp + 4 * e4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (lane == 0) {
+      pp[D] = -INFINITY;
+      pp[D + 1] = 0.0f;
+    }
+    return;
+  }
+  if (!early) attn_load_round<D>(rd, kb, vb, KB * sl, cap);
   const float4 q4 = rope4<D>(qkv + (size_t)h * D, cosT, sinT, pc, e4);
   const float4 kn4 = rope4<D>(qkv + (size_t)(H + g) * D, cosT, sinT, pc, e4);
   const float4 vn4 = *reinterpret_cast<const float4 *>(qkv + (size_t)(H + KV + g) * D + 4 * e4);
@@ -300,7 +314,6 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   acc.z = column_sum<LPR>(acc.z);
   acc.w = column_sum<LPR>(acc.w);
   l = column_sum<LPR>(l);
-  float *pp = part + ((size_t)h * NS + sl) * PS;
   if (r == 0) *reinterpret_cast<float4 *>(pp + 4 * e4) = acc;
   if (lane == 0) {
     pp[D] = m;
@@ -308,45 +321,19 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   }
 }
 
-// out[h] = the slices' partials of head h combined:
-// sum_s acc_s exp(m_s - M) / sum_s l_s exp(m_s - M), M = max_s m_s. One wave per
-// head; every load is issued before the first wait (lane s holds slice s's max and
-// sum, and the partial vectors are read for all kAttnMaxSplit slots, slots past the
-// active slices re-reading the last one with weight 0), so the merge costs one
-// round trip, not one per slice.
+// out[h] = the slices' partials of head h combined (attn_merge4, the arithmetic of
+// the attention-merge prologue of the fused GEMVs). One wave per head.
 template <int D>
 __global__ __launch_bounds__(kWave) void attention_merge_kernel(const int32_t *__restrict__ pos, int cap, int NS,
                                                                 const float *__restrict__ part,
                                                                 float *__restrict__ out) {
-  static_assert(kAttnMaxSplit <= kWave, "one lane per slice");
-  constexpr int KB = AttnCfg<D>::kKB, PS = D + 4, LPR = D / 4;
-  const int h = blockIdx.x, lane = threadIdx.x, e4 = lane % LPR;
+  constexpr int KB = AttnCfg<D>::kKB, LPR = D / 4;
+  const int h = blockIdx.x, lane = threadIdx.x;
   const int p = *pos;
   const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
-  int nact = (S + KB - 1) / KB;
-  nact = nact < 1 ? 1 : (nact < NS ? nact : NS);
-  const float *ph = part + (size_t)h * NS * PS;
-  const int sl = lane < nact ? lane : nact - 1;
-  float4 a[kAttnMaxSplit];
-#pragma unroll
-  for (int s = 0; s < kAttnMaxSplit; s++)
-    a[s] = *reinterpret_cast<const float4 *>(ph + (size_t)(s < nact ? s : nact - 1) * PS + 4 * e4);
-  const float ms = ph[(size_t)sl * PS + D], ls = ph[(size_t)sl * PS + D + 1];
-  const float M = wave_max(lane < nact ? ms : -INFINITY);
-  const float f = lane < nact ? expf(ms - M) : 0.0f;
-  const float den = wave_sum(ls * f);
-  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-  for (int s = 0; s < kAttnMaxSplit; s++) {
-    const float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s));  // 0 past the active slices
-    num.x = __builtin_fmaf(a[s].x, fs, num.x);
-    num.y = __builtin_fmaf(a[s].y, fs, num.y);
-    num.z = __builtin_fmaf(a[s].z, fs, num.z);
-    num.w = __builtin_fmaf(a[s].w, fs, num.w);
-  }
-  if (lane < LPR)
-    *reinterpret_cast<float4 *>(out + (size_t)h * D + 4 * e4) =
-        make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+  if (lane >= LPR) return;
+  *reinterpret_cast<float4 *>(out + (size_t)h * D + 4 * lane) =
+      attn_merge4(part + (size_t)h * NS * (D + 4), D + 4, D, attn_active_slices(S, KB, NS), lane);
 }
 
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
@@ -520,29 +507,62 @@ hipError_t launch_argmax(const float *v, int n, int32_t *tok, int32_t *pos, int 
   return hipGetLastError();
 }
 
+hipError_t launch_attention_slices(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
+                                   const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *part,
+                                   hipStream_t s) {
+  if (KV <= 0 || H % KV || H / KV > kAttnMaxGroup || cap <= 0) return hipErrorInvalidValue;
+  const dim3 grid(KV, H / KV, attn_slices(D, cap));
+  if (D == 32)
+    hipLaunchKernelGGL(attention_slice_kernel<32>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos, kc,
+                       vc, cap, part);
+  else if (D == 64)
+    hipLaunchKernelGGL(attention_slice_kernel<64>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos, kc,
+                       vc, cap, part);
+  else if (D == 128)
+    hipLaunchKernelGGL(attention_slice_kernel<128>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos,
+                       kc, vc, cap, part);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap, float *out,
+                                  hipStream_t s) {
+  if (H <= 0 || cap <= 0) return hipErrorInvalidValue;
+  const int ns = attn_slices(D, cap);
+  if (D == 32)
+    hipLaunchKernelGGL(attention_merge_kernel<32>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+  else if (D == 64)
+    hipLaunchKernelGGL(attention_merge_kernel<64>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+  else if (D == 128)
+    hipLaunchKernelGGL(attention_merge_kernel<128>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_attention_decode(const float *qkv, int H, int KV, int D, const float *cosT, const float *sinT,
                                    const int32_t *pos, int max_pos, float *kc, float *vc, int cap, float *out,
                                    float *work, hipStream_t s) {
   if (KV <= 0 || H % KV || H / KV > kAttnMaxGroup || cap <= 0) return hipErrorInvalidValue;
-  auto go = [&](auto dc) -> hipError_t {
-    constexpr int DD = decltype(dc)::value;
-    if (work && cap >= kAttnSliceMinCap) {
-      const int ns = attn_slices(DD, cap);
-      hipLaunchKernelGGL(attention_slice_kernel<DD>, dim3(KV, H / KV, ns), dim3(kWave), 0, s, qkv, H, KV, cosT,
-                         sinT, pos, max_pos, kc, vc, cap, work);
-      hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(attention_merge_kernel<DD>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, work, out);
-    } else {
-      hipLaunchKernelGGL(attention_decode_kernel<DD>, dim3(KV, H / KV), dim3(kAttThreads), 0, s, qkv, H, KV, cosT,
-                         sinT, pos, max_pos, kc, vc, cap, out);
-    }
-    return hipGetLastError();
-  };
-  if (D == 32) return go(std::integral_constant<int, 32>{});
-  if (D == 64) return go(std::integral_constant<int, 64>{});
-  if (D == 128) return go(std::integral_constant<int, 128>{});
-  return hipErrorInvalidValue;
+  if (work && cap >= kAttnSliceMinCap) {
+    const hipError_t e = launch_attention_slices(qkv, H, KV, D, cosT, sinT, pos, max_pos, kc, vc, cap, work, s);
+    if (e != hipSuccess) return e;
+    return launch_attention_merge(work, H, D, pos, cap, out, s);
+  }
+  const dim3 grid(KV, H / KV);
+  if (D == 32)
+    hipLaunchKernelGGL(attention_decode_kernel<32>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else if (D == 64)
+    hipLaunchKernelGGL(attention_decode_kernel<64>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else if (D == 128)
+    hipLaunchKernelGGL(attention_decode_kernel<128>, grid, dim3(kAttThreads), 0, s, qkv, H, KV, cosT, sinT, pos,
+                       max_pos, kc, vc, cap, out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t *pos, int inc, int32_t *hist,

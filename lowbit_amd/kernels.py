@@ -139,6 +139,8 @@ SIGNATURES = {
     "lbd_attention_decode_ws": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _vp, _sz, _vp],
                                 _int),
     "lbd_attention_decode_work_bytes": ([_int, _int, _int], _sz),
+    "lbd_attention_slices": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _sz, _vp], _int),
+    "lbd_attention_merge": ([_vp, _int, _int, _vp, _int, _vp, _vp], _int),
     "lbd_gemm_w4a16_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_gemm_w4a8_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_quantize_int4_g32": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),
@@ -150,7 +152,7 @@ class LbdFusion(C.Structure):
     (pass C.byref(f) as the `f` argument)."""
     _fields_ = [("norm_w", C.c_void_p), ("norm_eps", C.c_float), ("swiglu", C.c_int),
                 ("bias", C.c_void_p), ("residual", C.c_void_p), ("argmax_key", C.c_void_p),
-                ("glu", C.c_int)]
+                ("glu", C.c_int), ("attn_part", C.c_void_p), ("attn_cap", C.c_int), ("attn_head_dim", C.c_int)]
 
 
 @lru_cache(maxsize=1)

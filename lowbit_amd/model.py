@@ -18,9 +18,11 @@ linear layer is one fused GEMV (`lbd_gemv_*_fused`) whose prologue applies the
 RMSNorm (q/k/v, gate/up, LM head) to its activation row and whose epilogue adds
 the q/k/v bias or the residual in place, or (gate/up) writes the SwiGLU of each
 gate/up output pair, so the down projection reads its activations ready-made;
-the rotary embedding
-and the KV-cache write run inside the one-token attention
-(`lbd_attention_decode`); the LM head's epilogue folds the greedy argmax into a
+the rotary embedding and the KV-cache write run inside the one-token attention,
+which cuts each head's keys into slices on many compute units
+(`lbd_attention_slices`) whose partial sums the o projection's prologue merges
+(caches of more than 8 slices take `lbd_attention_decode_ws`, which merges in a
+launch of its own); the LM head's epilogue folds the greedy argmax into a
 64-bit key that `lbd_argmax_finalize` turns into the next token. Prompts (T > 1)
 run the unfused sequence on the matrix-core GEMMs.
 
@@ -144,10 +146,14 @@ class KVCache:
         self.k = [_buf(nb) for _ in range(cfg.num_layers)]
         self.v = [_buf(nb) for _ in range(cfg.num_layers)]
         self.length = 0
-        # partial sums of the one-token attention's key slices (long caches; the
-        # layers use it in turn on the model's stream)
+        # partial sums of the one-token attention's key slices (the layers use it
+        # in turn on the model's stream)
         wb = K.lib().lbd_attention_decode_work_bytes(cfg.num_heads, cfg.head_dim, self.capacity)
         self.attn_work = _buf(wb)
+        # the o projection's prologue merges up to 8 slices of 4096 / head_dim keys
+        # over rows of at most 2048 elements; longer caches take the merge launch
+        slices = wb // (cfg.num_heads * (cfg.head_dim + 4) * 4)
+        self.fused_merge = slices <= 8 and cfg.num_heads * cfg.head_dim <= 2048
 
 
 @dataclass
@@ -291,12 +297,17 @@ class Model:
                                      ws.nbytes, s)
         _check(rc, f"{self.backend} linear")
 
-    def _fused_linear(self, w, x: int, y: int, norm: int | None = None, glu: bool = False,
-                      bias: int | None = None, res: int | None = None, key: int | None = None):
+    def _fused_linear(self, w, x: int | None, y: int, norm: int | None = None, glu: bool = False,
+                      bias: int | None = None, res: int | None = None, key: int | None = None,
+                      attn: tuple | None = None):
         """y[0, n] = res[n] + (act(x) . w^T)[n] + bias[n] for one token, one launch;
         act is the RMSNorm with weights `norm` (or the identity). With glu the rows
-        of w are (gate, up) pairs and y[0, p] = silu(gate) * up of pair p."""
-        f = K.LbdFusion(norm, self.cfg.rms_norm_eps if norm else 0.0, 0, bias, res, key, int(glu))
+        of w are (gate, up) pairs and y[0, p] = silu(gate) * up of pair p. With
+        attn = (partials, cache capacity) the activation row is the one-token
+        attention merged from its key-slice partials (x unused)."""
+        part, cap = attn if attn else (None, 0)
+        f = K.LbdFusion(norm, self.cfg.rms_norm_eps if norm else 0.0, 0, bias, res, key, int(glu), part, cap,
+                        self.cfg.head_dim if attn else 0)
         L, s = self.L, self.stream
         if self.backend == "mxfp4":
             rc = L.lbd_gemv_mxfp4_fused(x, 1, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, y, C.byref(f), s)
@@ -316,11 +327,18 @@ class Model:
         for li, ly in enumerate(self.layers):
             self._fused_linear(ly.qkv, x, self.qkv.ptr, norm=ly.ln1.ptr,
                                bias=None if ly.qkv_bias is None else ly.qkv_bias.ptr)
-            _check(L.lbd_attention_decode_ws(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
-                                             cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
-                                             self.att.ptr, cache.attn_work.ptr, cache.attn_work.nbytes, s),
-                   "attention decode")
-            self._fused_linear(ly.o, self.att.ptr, x, res=x)
+            if cache.fused_merge:
+                # key slices, merged in the o projection's prologue
+                _check(L.lbd_attention_slices(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
+                                              cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
+                                              cache.attn_work.ptr, cache.attn_work.nbytes, s), "attention slices")
+                self._fused_linear(ly.o, None, x, res=x, attn=(cache.attn_work.ptr, cache.capacity))
+            else:
+                _check(L.lbd_attention_decode_ws(self.qkv.ptr, H, KV, D, self.cos.ptr, self.sin.ptr, self.pos.ptr,
+                                                 cfg.max_position, cache.k[li].ptr, cache.v[li].ptr, cache.capacity,
+                                                 self.att.ptr, cache.attn_work.ptr, cache.attn_work.nbytes, s),
+                       "attention decode")
+                self._fused_linear(ly.o, self.att.ptr, x, res=x)
             self._fused_linear(ly.gate_up, x, self.m.ptr, norm=ly.ln2.ptr, glu=True)
             self._fused_linear(ly.down, self.m.ptr, x, res=x)
         if logits == "none":

@@ -367,6 +367,67 @@ def test_attention_decode_consecutive_positions(rng, cap):
         kc, vc = dk.to_array(kc.shape, np.float32), dv.to_array(vc.shape, np.float32)
 
 
+# slices 1, 3, 4 (all active), 8 with 2 active, 8 with p >= cap, 7 at D = 128, 2 at D = 32
+@pytest.mark.parametrize("D,H,KV,p,cap", [(64, 14, 2, 30, 64), (64, 14, 2, 150, 193), (64, 14, 2, 255, 256),
+                                          (64, 14, 2, 100, 512), (64, 14, 2, 600, 512), (128, 8, 2, 200, 224),
+                                          (32, 16, 4, 200, 256)])
+def test_attention_slices_merge_and_fused_prologue(rng, D, H, KV, p, cap):
+    """lbd_attention_slices + lbd_attention_merge against the float64 attention, and
+    the fused o projection whose prologue merges the same partials equal to the
+    merge kernel's output followed by the plain fused GEMV, bit for bit."""
+    L = K.lib()
+    qkv = rng.standard_normal((H + 2 * KV) * D).astype(np.float32)
+    kc0 = rng.standard_normal((KV, cap, D)).astype(np.float32)
+    vc0 = rng.standard_normal((KV, cap, D)).astype(np.float32)
+    max_pos = 1024
+    cos, sin = DM.rope_tables(D, max_pos, 10000.0)
+    dk, dv = up(kc0), up(vc0)
+    dcos, dsin, dpos = up(cos), up(sin), up(np.array([p], np.int32))
+    part = K.DeviceBuffer(L.lbd_attention_decode_work_bytes(H, D, cap))
+    out = K.DeviceBuffer(4 * H * D)
+    _LIVE.extend([part, out])
+    ok(L.lbd_attention_slices(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, dpos.ptr, max_pos, dk.ptr, dv.ptr, cap,
+                              part.ptr, part.nbytes, None))
+    ok(L.lbd_attention_merge(part.ptr, H, D, dpos.ptr, cap, out.ptr, None))
+    ref, k, v = attention_one(qkv, kc0, vc0, p, H, KV, D, cos, sin)
+    att = out.to_array((H * D,), np.float32)
+    assert np.abs(att - ref).max() <= 2e-5 * max(np.abs(vc0).max(), np.abs(v).max())
+    if p < cap:
+        np.testing.assert_allclose(dk.to_array(kc0.shape, np.float32)[:, p], k, rtol=0, atol=1e-5)
+    n = 300
+    r = rng.standard_normal(n).astype(np.float32)
+    for fmt in FORMATS:
+        hw, dw = weights(rng, fmt, n, H * D, asym=(fmt == "w4a8"))
+        y_ref, y_fz = up(r), up(r)
+        ok(fused(fmt, dw, out.ptr, y_ref.ptr, res=y_ref.ptr))
+        f = K.LbdFusion(None, 0.0, 0, None, y_fz.ptr, None, 0, part.ptr, cap, D)
+        if fmt == "mxfp4":
+            ok(L.lbd_gemv_mxfp4_fused(None, 1, dw.kp, dw.qw.ptr, dw.e8m0.ptr, n, y_fz.ptr, C.byref(f), None))
+        else:
+            fn = L.lbd_gemv_w4a16_fused if fmt == "w4a16" else L.lbd_gemv_w4a8_fused
+            zp = None if dw.zeros is None else dw.zeros.ptr
+            ok(fn(None, 1, dw.kp, dw.qw.ptr, dw.scales.ptr, zp, n, y_fz.ptr, C.byref(f), None))
+        np.testing.assert_array_equal(y_fz.to_array((n,), np.float32), y_ref.to_array((n,), np.float32))
+
+
+def test_attention_merge_prologue_argument_checks(rng):
+    L = K.lib()
+    hw, dw = weights(rng, "w4a16", 64, 896)
+    part, y = up(np.zeros(1 << 16, np.float32)), K.DeviceBuffer(4 * 64 * 2)
+    _LIVE.append(y)
+    nw = up(np.ones(896, np.float32))
+
+    def call(m=1, cap=193, d=64, norm=None):
+        f = K.LbdFusion(norm, 0.0, 0, None, None, None, 0, part.ptr, cap, d)
+        return L.lbd_gemv_w4a16_fused(None, m, dw.kp, dw.qw.ptr, dw.scales.ptr, None, 64, y.ptr, C.byref(f), None)
+    assert call() == K.ISA_GFX950
+    assert call(m=2) == -6                 # one activation row
+    assert call(norm=nw.ptr) == -6         # one prologue
+    assert call(cap=513) == -1             # nine slices of 64 keys
+    assert call(d=48) == -1                # head_dim
+    assert call(d=128, cap=257) == -1      # nine slices of 32 keys
+
+
 def test_attention_decode_argument_checks():
     L = K.lib()
     b = up(np.zeros(4096, np.float32))
@@ -384,6 +445,25 @@ def test_attention_decode_argument_checks():
 
 
 # ---------------------------------------------------------------- the model: fused = unfused
+
+@pytest.mark.parametrize("backend", ["w4a8", "mxfp4"])
+def test_fused_decode_long_prompt(backend):
+    """Decode steps after a 200-token prompt (cache of 210: four key slices merged in
+    the o projection's prologue, three of them in use) against the unfused step."""
+    cfg = DM.qwen2_config(num_layers=2, vocab_size=4096, max_position=512)
+    W = DM.random_weights(cfg, seed=3)
+    toks = np.random.default_rng(9).integers(0, cfg.vocab_size, 205)
+    out = {}
+    for fz in (True, False):
+        m = DM.Model(cfg, W, backend, fused=fz)
+        c = m.new_cache(210)
+        assert c.fused_merge
+        m.forward(toks[:200], c)
+        out[fz] = np.stack([m.forward([t], c) for t in toks[200:]])
+    scale = np.abs(out[False]).max()
+    assert np.abs(out[True] - out[False]).max() <= 1e-4 * scale
+    assert (out[True].argmax(-1) == out[False].argmax(-1)).all()
+
 
 @pytest.mark.parametrize("backend", ["w4a16", "w4a8", "mxfp4"])
 def test_fused_decode_matches_unfused_and_oracle(backend):
