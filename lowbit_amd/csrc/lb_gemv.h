@@ -346,12 +346,13 @@ void gemv_kernel(GemmArgs a) {
       ss = __builtin_fmaf(xr[i].w, xr[i].w, ss);
     }
     ss = wave_sum(ss);
-    if (lane == 0) red[0][wave] = ss;
+    // red[1]: the one-row quantizer below uses red[0] only, so no second barrier
+    // is needed before it overwrites anything
+    if (lane == 0) red[1][wave] = ss;
     __syncthreads();
-    float tot = red[0][0];
+    float tot = red[1][0];
 #pragma unroll
-    for (int w = 1; w < kGemvWaves; w++) tot += red[0][w];
-    __syncthreads();  // red is reused by the quantizer below
+    for (int w = 1; w < kGemvWaves; w++) tot += red[1][w];
     const float rn = 1.0f / sqrtf(tot / (float)Kp + a.norm_eps);
 #pragma unroll
     for (int i = 0; i < S; i++) {
