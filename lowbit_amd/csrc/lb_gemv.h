@@ -588,13 +588,18 @@ static GemvFn pick_gemv(int nit, int nch, int rpw) {
 // both): otherwise the second waits for the first to finish, and one workgroup per
 // CU with twice the rows is faster (long rows: 9-16 % at 1 x 4096 x 11008 cold).
 // W4A8 quantizes the activation row in every workgroup, so below two rows per wave
-// it takes one workgroup per CU as well (3-9 % at N = 3072 .. 6144).
+// it takes one workgroup per CU as well (3-9 % at N = 3072 .. 6144), and so does a
+// W4A8 GEMV with a prologue whose workgroups would get under 32 KB of weights.
 template <int F, int MB, int PRO>
 static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
   constexpr bool kQuant = (F == F_W4A8 || F == F_W4A8G32);
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
   const int cus = num_cus > 0 ? num_cus : 256;
-  int per_cu = (kQuant && a.N < 2 * 2 * cus * kGemvWaves) ? 1 : 2;
+  // W4A8 with a fused prologue (RMSNorm before the quantizer) and a small share of
+  // weights per workgroup: the prologue, not the weight stream, sets the time, and
+  // it runs faster with the CU to itself (gate/up 9728 x 896: 5.1 -> 4.5 us)
+  const double wg_bytes = (double)a.N * (a.Kp / 2) / (2.0 * cus);
+  int per_cu = (kQuant && (a.N < 2 * 2 * cus * kGemvWaves || (PRO != 0 && wg_bytes < 32768.0))) ? 1 : 2;
   for (;;) {
     int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
     grid = grid < per_cu * cus ? grid : per_cu * cus;
