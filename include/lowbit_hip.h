@@ -354,8 +354,8 @@ int lbd_attention_slices(const float *qkv, int H, int KV, int D, const float *co
                          const float *sin_table, const int32_t *pos, int max_pos,
                          float *k_cache, float *v_cache, int cap, float *part,
                          size_t part_bytes, void *stream);
-int lbd_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap,
-                        float *out, void *stream);
+int lbd_attention_merge(const float *part, size_t part_bytes, int H, int D, const int32_t *pos,
+                        int cap, float *out, void *stream);
 int lbd_attention_decode_ws(const float *qkv, int H, int KV, int D, const float *cos_table,
                             const float *sin_table, const int32_t *pos, int max_pos,
                             float *k_cache, float *v_cache, int cap, float *out, void *work,

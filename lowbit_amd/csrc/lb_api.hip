@@ -888,10 +888,13 @@ int lbd_attention_slices(const float *qkv, int H, int KV, int D, const float *co
             "attention slices launch");
 }
 
-int lbd_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap, float *out, void *stream) {
+int lbd_attention_merge(const float *part, size_t part_bytes, int H, int D, const int32_t *pos, int cap, float *out,
+                        void *stream) {
   if (H <= 0 || (D != 32 && D != 64 && D != 128) || cap <= 0 || cap > 16000) return fail(LB_ERR_SHAPE, "bad shape");
   if (!part || !pos || !out) return fail(LB_ERR_ARG, "null pointer");
   if (!aligned16(part) || !aligned16(out)) return fail(LB_ERR_ARG, "part and out must be 16-byte aligned");
+  if (part_bytes < lbk::attn_work_bytes(H, D, cap))
+    return fail(LB_ERR_ARG, "part smaller than lbd_attention_decode_work_bytes");
   LB_LAUNCH(lbk::launch_attention_merge(part, H, D, pos, cap, out, static_cast<hipStream_t>(stream)),
             "attention merge launch");
 }

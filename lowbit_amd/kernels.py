@@ -140,7 +140,7 @@ SIGNATURES = {
                                 _int),
     "lbd_attention_decode_work_bytes": ([_int, _int, _int], _sz),
     "lbd_attention_slices": ([_vp, _int, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int, _vp, _sz, _vp], _int),
-    "lbd_attention_merge": ([_vp, _int, _int, _vp, _int, _vp, _vp], _int),
+    "lbd_attention_merge": ([_vp, _sz, _int, _int, _vp, _int, _vp, _vp], _int),
     "lbd_gemm_w4a16_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_gemm_w4a8_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_quantize_int4_g32": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),

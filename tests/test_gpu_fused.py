@@ -388,7 +388,8 @@ def test_attention_slices_merge_and_fused_prologue(rng, D, H, KV, p, cap):
     _LIVE.extend([part, out])
     ok(L.lbd_attention_slices(up(qkv).ptr, H, KV, D, dcos.ptr, dsin.ptr, dpos.ptr, max_pos, dk.ptr, dv.ptr, cap,
                               part.ptr, part.nbytes, None))
-    ok(L.lbd_attention_merge(part.ptr, H, D, dpos.ptr, cap, out.ptr, None))
+    ok(L.lbd_attention_merge(part.ptr, part.nbytes, H, D, dpos.ptr, cap, out.ptr, None))
+    assert L.lbd_attention_merge(part.ptr, part.nbytes - 16, H, D, dpos.ptr, cap, out.ptr, None) == -6
     ref, k, v = attention_one(qkv, kc0, vc0, p, H, KV, D, cos, sin)
     att = out.to_array((H * D,), np.float32)
     assert np.abs(att - ref).max() <= 2e-5 * max(np.abs(vc0).max(), np.abs(v).max())
