@@ -4,6 +4,9 @@
 // S = min(p + 1, cap), where (when p < cap) key p is the new one, held in
 // registers and never read back from the cache.
 //
+// Exponentials of the softmax and of the merges are the hardware's (__expf: their
+// arguments are <= 0, and a few ulp of exp(x) stay far inside the attention bound).
+//
 // Memory layout of the work: D / 4 lanes share a key (or value) row, each lane
 // holding one float4 of it, so a wave load covers RPL = 256 / D consecutive rows
 // (1 KiB contiguous). A wave takes KB = 16 RPL keys per round (16 key loads and 16
@@ -142,7 +145,7 @@ __device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, f
     }
     // ---- running maximum (the round has a key below S: row k0), rescale, p * v
     const float mnew = fmaxf(m, wave_max(mx));
-    const float alpha = expf(m - mnew);  // 0 on the wave's first round
+    const float alpha = __expf(m - mnew);  // 0 on the wave's first round
     m = mnew;
     l *= alpha;
     acc.x *= alpha;
@@ -152,7 +155,7 @@ __device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, f
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int row = k0 + RPL * u + r;
-      const float pr = expf(sc[u] - m);  // 0 for masked keys
+      const float pr = __expf(sc[u] - m);  // 0 for masked keys
       // masked rows (past the keys in use) may hold anything, NaN included: 0 * NaN
       // would poison the sum, so their values are replaced, not just weighted by 0
       const float4 vv = row < S ? ((newk && row == Sc) ? vn4 : rd.v[u]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -182,7 +185,7 @@ __device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, f
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-      const float f = expf(sh.mw[w] - M);  // 0 for a wave that saw no key
+      const float f = __expf(sh.mw[w] - M);  // 0 for a wave that saw no key
       num = __builtin_fmaf(sh.part[w][e], f, num);
       den = __builtin_fmaf(sh.lw[w], f, den);
     }
@@ -217,7 +220,7 @@ __device__ __forceinline__ void attn_combine8(const AttnPart8 &q, int s0, int n,
 #pragma unroll
   for (int b = 0; b < 8; b++) {
     if (s0 + b >= n) break;
-    const float f = expf(q.m[b] - M);
+    const float f = __expf(q.m[b] - M);
     num.x = __builtin_fmaf(q.a[b].x, f, num.x);
     num.y = __builtin_fmaf(q.a[b].y, f, num.y);
     num.z = __builtin_fmaf(q.a[b].z, f, num.z);
@@ -235,7 +238,8 @@ __device__ __forceinline__ float4 attn_merge8(const AttnPart8 &q, int n) {
   float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   float den = 0.0f;
   attn_combine8(q, 0, n, M, num, den);
-  return make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+  const float rd = 1.0f / den;
+  return make_float4(num.x * rd, num.y * rd, num.z * rd, num.w * rd);
 }
 
 // Elements 4 e4 .. 4 e4 + 3 of one head's attention output from the partials of its
@@ -257,7 +261,8 @@ __device__ __forceinline__ float4 attn_merge4(const float *ph, int PS, int D, in
     attn_fetch8(q, ph, PS, D, s0, n, e4);
     attn_combine8(q, s0, n, M, num, den);
   }
-  return make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+  const float rd = 1.0f / den;
+  return make_float4(num.x * rd, num.y * rd, num.z * rd, num.w * rd);
 }
 
 // Rotate the pair (x1, x2) of element i of a head at the table row pc

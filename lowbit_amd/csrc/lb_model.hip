@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
       mx = fmaxf(mx, sc[u]);
     }
     const float mnew = fmaxf(m, wave_max(mx));  // the round has a key below S: row k0
-    const float alpha = expf(m - mnew);         // 0 on the first round
+    const float alpha = __expf(m - mnew);       // 0 on the first round
     m = mnew;
     l *= alpha;
     acc.x *= alpha;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int row = k0 + RPL * u + r;
-      const float pr = expf(sc[u] - m);
+      const float pr = __expf(sc[u] - m);
       // masked rows may hold anything, NaN included: their values are replaced
       const float4 vv = row < S ? ((newk && row == Sc) ? vn4 : rd.v[u]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       l += pr;
