@@ -347,9 +347,10 @@ int lbd_attention_decode(const float *qkv, int H, int KV, int D, const float *co
 size_t lbd_attention_decode_work_bytes(int H, int D, int cap);
 /* The two halves of the key-slice path, for callers that merge elsewhere (the
  * attention-merge prologue of the fused GEMVs): lbd_attention_slices rotates, writes
- * the caches and stores every slice's partial to `part` (min(ceil(cap / (4096 / D)),
- * 32) slices per head, lbd_attention_decode_work_bytes(H, D, cap) bytes; slices past
- * the keys in use store empty partials); lbd_attention_merge combines them into out. */
+ * the caches and stores every slice's partial to `part` (slices of 2048 / D keys
+ * where 8 of them hold the cache, else 4096 / D, at most 32 per head;
+ * lbd_attention_decode_work_bytes(H, D, cap) bytes; slices past the keys in use
+ * store empty partials); lbd_attention_merge combines them into out. */
 int lbd_attention_slices(const float *qkv, int H, int KV, int D, const float *cos_table,
                          const float *sin_table, const int32_t *pos, int max_pos,
                          float *k_cache, float *v_cache, int cap, float *part,

@@ -24,11 +24,11 @@
 
 namespace lbk {
 
-template <int D>
+template <int D, int UU = 16>
 struct AttnCfg {
   static constexpr int kLPR = D / 4;          // lanes per key row
   static constexpr int kRPL = kWave / kLPR;   // key rows per wave load
-  static constexpr int kU = 16;               // key (and value) loads per lane and round
+  static constexpr int kU = UU;               // key (and value) loads per lane and round
   static constexpr int kKB = kU * kRPL;       // keys per wave and round
 };
 
@@ -39,10 +39,10 @@ __host__ __device__ __forceinline__ int attn_active_slices(int S, int KB, int NS
 }
 
 // Registers holding one round of a wave's key and value rows.
-template <int D>
+template <int D, int UU = 16>
 struct AttnRound {
-  float4 k[AttnCfg<D>::kU];
-  float4 v[AttnCfg<D>::kU];
+  float4 k[AttnCfg<D, UU>::kU];
+  float4 v[AttnCfg<D, UU>::kU];
 };
 
 // LDS of the final merge for NT threads.
@@ -77,10 +77,10 @@ __device__ __forceinline__ float column_sum(float v) {
 // Key and value rows of one round of this wave, starting at key k0; rows clamped
 // below cap, so every address is inside the cache (rows past the keys in use are
 // masked out of the softmax). kb / vb: the KV head's cache rows [cap][D].
-template <int D>
-__device__ __forceinline__ void attn_load_round(AttnRound<D> &rd, const float *__restrict__ kb,
+template <int D, int UU = 16>
+__device__ __forceinline__ void attn_load_round(AttnRound<D, UU> &rd, const float *__restrict__ kb,
                                                 const float *__restrict__ vb, int k0, int cap) {
-  constexpr int LPR = AttnCfg<D>::kLPR, RPL = AttnCfg<D>::kRPL, U = AttnCfg<D>::kU;
+  constexpr int LPR = AttnCfg<D, UU>::kLPR, RPL = AttnCfg<D, UU>::kRPL, U = AttnCfg<D, UU>::kU;
   const int lane = threadIdx.x & (kWave - 1), r = lane / LPR, e4 = lane % LPR;
 #pragma unroll
   for (int u = 0; u < U; u++) {

@@ -131,16 +131,22 @@ hipError_t launch_argmax_finalize(unsigned long long *key, int32_t *tok, int32_t
                                   int hist_len, hipStream_t s);
 // One-token attention with the rotary embedding and the KV-cache write folded in.
 // With a workspace and a cache of at least kAttnSliceMinCap positions, each query
-// head's keys are cut into slices of one wave round (4096 / D keys), at most
+// head's keys are cut into slices of one wave round (attn_slice_keys), at most
 // kAttnMaxSplit per head, whose partials [H][slices][D + 4] floats a second kernel
 // (or a fused GEMV's attention-merge prologue, up to kAttnMaxFusedSlices slices)
 // merges; otherwise one workgroup per query head (work may be null).
 constexpr int kAttnMaxGroup = 16;     // query heads per KV head
 constexpr int kAttnMaxSplit = 32;     // key slices per head
+constexpr int kAttnMaxFusedSlices = 8;  // slices a fused GEMV's prologue merges
 constexpr int kAttnSliceMinCap = 1024;
-constexpr int kAttnMaxFusedSlices = 8;
+// Keys per slice: one wave round of 8 loads per lane (2048 / D keys) where 8 such
+// slices hold the cache (more workgroups, each one shorter), else 16 (4096 / D).
+inline int attn_slice_keys(int D, int cap) {
+  const int k8 = 32 * 64 / D;
+  return (cap + k8 - 1) / k8 <= kAttnMaxFusedSlices ? k8 : 2 * k8;
+}
 inline int attn_slices(int D, int cap) {
-  const int kb = 64 * 64 / D;
+  const int kb = attn_slice_keys(D, cap);
   const int n = (cap + kb - 1) / kb;
   return n < kAttnMaxSplit ? n : kAttnMaxSplit;
 }

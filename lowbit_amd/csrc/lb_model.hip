@@ -216,7 +216,8 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
 }
 
 // Key slices: the same one-token attention with each query head's keys cut into
-// slices of one wave round (KB keys, lb_attn.h) on one-wave workgroups, grid
+// slices of one wave round (KB keys, lb_attn.h; 8 loads per lane and round, i.e.
+// 2048 / D keys, where 8 such slices hold the cache, else 16) on one-wave workgroups, grid
 // KV x H/KV x NS, so that a head's keys stream through NS compute units instead of
 // one. Workgroup (g, j, sl) takes the rounds sl, sl + NS, ... below S and stores
 // its (p * v, max, sum) partial; attention_merge_kernel (long caches) or the fused
@@ -229,12 +230,12 @@ __global__ __launch_bounds__(kAttThreads) void attention_decode_kernel(
 // those of attention_decode_kernel.
 constexpr int kAttnPrefetchKeys = 256;
 
-template <int D>
+template <int D, int UU>
 __global__ __launch_bounds__(kWave) void attention_slice_kernel(
     const float *__restrict__ qkv, int H, int KV, const float *__restrict__ cosT, const float *__restrict__ sinT,
     const int32_t *__restrict__ pos, int max_pos, float *__restrict__ kc, float *__restrict__ vc, int cap,
     float *__restrict__ part) {
-  using Cfg = AttnCfg<D>;
+  using Cfg = AttnCfg<D, UU>;
   constexpr int LPR = Cfg::kLPR, RPL = Cfg::kRPL, U = Cfg::kU, KB = Cfg::kKB, PS = D + 4;
   const int g = blockIdx.x, j = blockIdx.y, HG = gridDim.y, h = g * HG + j;
   const int sl = blockIdx.z, NS = gridDim.z;
@@ -242,9 +243,9 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   const float *kb = kc + (size_t)g * cap * D;
   const float *vb = vc + (size_t)g * cap * D;
   // the slices holding keys below 256 request their first round before *pos arrives
-  AttnRound<D> rd;
+  AttnRound<D, UU> rd;
   const bool early = KB * sl < kAttnPrefetchKeys;
-  if (early) attn_load_round<D>(rd, kb, vb, KB * sl, cap);
+  if (early) attn_load_round<D, UU>(rd, kb, vb, KB * sl, cap);
   const int p = *pos;
   const int pc = p < 0 ? 0 : (p < max_pos ? p : max_pos - 1);
   const bool newk = p >= 0 && p < cap;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
     }
     return;
   }
-  if (!early) attn_load_round<D>(rd, kb, vb, KB * sl, cap);
+  if (!early) attn_load_round<D, UU>(rd, kb, vb, KB * sl, cap);
   const float4 q4 = rope4<D>(qkv + (size_t)h * D, cosT, sinT, pc, e4);
   const float4 kn4 = rope4<D>(qkv + (size_t)(H + g) * D, cosT, sinT, pc, e4);
   const float4 vn4 = *reinterpret_cast<const float4 *>(qkv + (size_t)(H + KV + g) * D + 4 * e4);
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int c = sl; KB * c < S; c += NS) {
     const int k0 = KB * c;
-    if (c != sl) attn_load_round<D>(rd, kb, vb, k0, cap);
+    if (c != sl) attn_load_round<D, UU>(rd, kb, vb, k0, cap);
     float sc[U];
     float mx = -INFINITY;
 #pragma unroll
@@ -321,19 +322,52 @@ __global__ __launch_bounds__(kWave) void attention_slice_kernel(
   }
 }
 
-// out[h] = the slices' partials of head h combined (attn_merge4, the arithmetic of
-// the attention-merge prologue of the fused GEMVs). One wave per head.
+// out[h] = the slices' partials of head h combined. Up to 8 active slices:
+// attn_merge8, the arithmetic of the attention-merge prologue of the fused GEMVs
+// (so that both give the same bits). More (long caches): every load is issued
+// before the first wait (lane s holds slice s's max and sum, and the partial
+// vectors are read for all kAttnMaxSplit slots, slots past the active slices
+// re-reading the last one with weight 0), so the merge costs one round trip, not
+// one per group of slices. One wave per head.
 template <int D>
 __global__ __launch_bounds__(kWave) void attention_merge_kernel(const int32_t *__restrict__ pos, int cap, int NS,
-                                                                const float *__restrict__ part,
+                                                                int KB, const float *__restrict__ part,
                                                                 float *__restrict__ out) {
-  constexpr int KB = AttnCfg<D>::kKB, LPR = D / 4;
-  const int h = blockIdx.x, lane = threadIdx.x;
+  static_assert(kAttnMaxSplit <= kWave, "one lane per slice");
+  constexpr int LPR = D / 4, PS = D + 4;
+  const int h = blockIdx.x, lane = threadIdx.x, e4 = lane % LPR;
   const int p = *pos;
   const int S = p < 0 ? 0 : (p + 1 < cap ? p + 1 : cap);
-  if (lane >= LPR) return;
-  *reinterpret_cast<float4 *>(out + (size_t)h * D + 4 * lane) =
-      attn_merge4(part + (size_t)h * NS * (D + 4), D + 4, D, attn_active_slices(S, KB, NS), lane);
+  const int nact = attn_active_slices(S, KB, NS);
+  const float *ph = part + (size_t)h * NS * PS;
+  float4 *o4 = reinterpret_cast<float4 *>(out + (size_t)h * D) + e4;
+  if (nact <= 8) {
+    if (lane >= LPR) return;
+    AttnPart8 q;
+    attn_fetch8(q, ph, PS, D, 0, nact, e4);
+    *o4 = attn_merge8(q, nact);
+    return;
+  }
+  float4 a[kAttnMaxSplit];
+#pragma unroll
+  for (int s = 0; s < kAttnMaxSplit; s++)
+    a[s] = *reinterpret_cast<const float4 *>(ph + (size_t)(s < nact ? s : nact - 1) * PS + 4 * e4);
+  const int sl = lane < nact ? lane : nact - 1;
+  const float2 ml = *reinterpret_cast<const float2 *>(ph + (size_t)sl * PS + D);
+  const float M = wave_max(lane < nact ? ml.x : -INFINITY);
+  const float f = lane < nact ? __expf(ml.x - M) : 0.0f;
+  const float den = wave_sum(ml.y * f);
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int s = 0; s < kAttnMaxSplit; s++) {
+    const float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s));  // 0 past the active slices
+    num.x = __builtin_fmaf(a[s].x, fs, num.x);
+    num.y = __builtin_fmaf(a[s].y, fs, num.y);
+    num.z = __builtin_fmaf(a[s].z, fs, num.z);
+    num.w = __builtin_fmaf(a[s].w, fs, num.w);
+  }
+  const float rd = 1.0f / den;
+  if (lane < LPR) *o4 = make_float4(num.x * rd, num.y * rd, num.z * rd, num.w * rd);
 }
 
 // tok[0] = the index of the largest of the kArgmaxSlots keys that lbd_gemv_*_fused
@@ -512,30 +546,27 @@ hipError_t launch_attention_slices(const float *qkv, int H, int KV, int D, const
                                    hipStream_t s) {
   if (KV <= 0 || H % KV || H / KV > kAttnMaxGroup || cap <= 0) return hipErrorInvalidValue;
   const dim3 grid(KV, H / KV, attn_slices(D, cap));
-  if (D == 32)
-    hipLaunchKernelGGL(attention_slice_kernel<32>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos, kc,
-                       vc, cap, part);
-  else if (D == 64)
-    hipLaunchKernelGGL(attention_slice_kernel<64>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos, kc,
-                       vc, cap, part);
-  else if (D == 128)
-    hipLaunchKernelGGL(attention_slice_kernel<128>, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos,
-                       kc, vc, cap, part);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const bool half = attn_slice_keys(D, cap) * D == 32 * kWave;  // 8 loads per lane and round
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kWave), 0, s, qkv, H, KV, cosT, sinT, pos, max_pos, kc, vc, cap, part);
+    return hipGetLastError();
+  };
+  if (D == 32) return half ? go(attention_slice_kernel<32, 8>) : go(attention_slice_kernel<32, 16>);
+  if (D == 64) return half ? go(attention_slice_kernel<64, 8>) : go(attention_slice_kernel<64, 16>);
+  if (D == 128) return half ? go(attention_slice_kernel<128, 8>) : go(attention_slice_kernel<128, 16>);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_attention_merge(const float *part, int H, int D, const int32_t *pos, int cap, float *out,
                                   hipStream_t s) {
   if (H <= 0 || cap <= 0) return hipErrorInvalidValue;
-  const int ns = attn_slices(D, cap);
+  const int ns = attn_slices(D, cap), kb = attn_slice_keys(D, cap);
   if (D == 32)
-    hipLaunchKernelGGL(attention_merge_kernel<32>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+    hipLaunchKernelGGL(attention_merge_kernel<32>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, kb, part, out);
   else if (D == 64)
-    hipLaunchKernelGGL(attention_merge_kernel<64>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+    hipLaunchKernelGGL(attention_merge_kernel<64>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, kb, part, out);
   else if (D == 128)
-    hipLaunchKernelGGL(attention_merge_kernel<128>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, part, out);
+    hipLaunchKernelGGL(attention_merge_kernel<128>, dim3(H), dim3(kWave), 0, s, pos, cap, ns, kb, part, out);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
