@@ -33,6 +33,7 @@ import json
 import math
 import os
 import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -121,6 +122,15 @@ class Dev:
         L.lb_event_destroy(e0)
         L.lb_event_destroy(e1)
         return ms / n_launch
+
+
+MIN_LAUNCHES = 100  # timed launches per measurement, at least (BASELINE: >= 100 launches)
+
+
+def timed_launches(steps: int, pool: int) -> int:
+    """Launches in one timed graph: the requested steps, but never fewer than one pass
+    over the weight pool (so a cold measurement reads every copy) or MIN_LAUNCHES."""
+    return max(steps, pool, MIN_LAUNCHES)
 
 
 def weight_pool(dev: Dev, arrays: list[np.ndarray], nbytes: int, cold: bool):
@@ -212,16 +222,91 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
     path = launch(0)
     dev.check(L.lb_stream_synchronize(s), "sync")
     y = dy.to_array((m, n), np.float32)
-    ms = dev.time_launches(launch, steps, warmup, graph=graph)
+    # every timed graph covers the whole pool at least once and at least MIN_LAUNCHES
+    # launches, whatever --steps asks for
+    n_launch = timed_launches(steps, len(pool))
+    ms = dev.time_launches(launch, n_launch, warmup, graph=graph)
     t = ms * 1e-3
+    call_us = call_time(dev, fmt, W, x, pool, layout, n_launch, warmup)
     return {
         "format": fmt, "M": m, "N": n, "K": k, "cache": "cold" if cold else "hot",
         "path": K.ISA_NAMES.get(path, "?"), "weight_layout": layout, "pool_copies": len(pool),
-        "us_per_call": round(ms * 1e3, 3), "weight_bytes": int(W.nbytes),
+        "timed_launches": n_launch, "bytes_rotated": int(min(n_launch, len(pool)) * W.nbytes),
+        "us_per_call": round(ms * 1e3, 3), "call_us": call_us, "weight_bytes": int(W.nbytes),
         "weight_gbps": round(W.nbytes / t / 1e9, 1),
         "gflops": round(2.0 * m * n * k / t / 1e9, 1),
         "y": y,
     }
+
+
+# Configurations of the plain-read sweep: (workgroups, threads, 16-byte loads in flight per thread)
+FLOOR_CONFIGS = [(wg, th, ld) for wg in (256, 512, 1024, 2048) for th in (256, 512) for ld in (1, 2, 4, 8)]
+
+
+def read_floor(dev: Dev, nbytes: int, steps: int, warmup: int, graph: bool = True) -> dict:
+    """The fastest plain streaming read (lbd_read_kernel) of `nbytes` over the sweep
+    FLOOR_CONFIGS, timed like the GEMMs: cold (one copy of a pool larger than
+    COLD_POOL_BYTES per launch) and hot (one buffer), HIP events over a replayed graph."""
+    K, L = dev.K, dev.L
+    nbytes = (nbytes + 15) // 16 * 16
+    copies = max(1, math.ceil(COLD_POOL_BYTES / nbytes))
+    pool = [K.DeviceBuffer(nbytes) for _ in range(copies)]
+    for i, b in enumerate(pool):
+        dev.check(L.lb_memset_d(b.ptr, 0x11 + i % 200, nbytes), "memset")
+    sink = K.DeviceBuffer(16)
+    rows = []
+    for wg, th, ld in FLOOR_CONFIGS:
+        row = {"workgroups": wg, "threads": th, "loads": ld}
+        for cache in ("cold", "hot"):
+            def launch(i, cache=cache):
+                b = pool[i % copies] if cache == "cold" else pool[0]
+                return dev.check(L.lbd_read_kernel(b.ptr, nbytes, wg, th, ld, sink.ptr, dev.stream), "read kernel")
+
+            n_launch = timed_launches(steps, copies)
+            row[f"{cache}_us"] = round(dev.time_launches(launch, n_launch, warmup, graph=graph) * 1e3, 3)
+        rows.append(row)
+    best = {c: min(rows, key=lambda r: r[f"{c}_us"]) for c in ("cold", "hot")}
+    out = {"bytes": nbytes, "pool_copies": copies, "timed_launches": timed_launches(steps, copies), "sweep": rows}
+    for c in ("cold", "hot"):
+        b = best[c]
+        out[c] = {"us": b[f"{c}_us"], "gbps": round(nbytes / (b[f"{c}_us"] * 1e-6) / 1e9, 1),
+                  "config": {k: b[k] for k in ("workgroups", "threads", "loads")}}
+    log(f"read floor {nbytes} B: cold {out['cold']['us']:.2f} us ({out['cold']['gbps']:.0f} GB/s) "
+        f"{out['cold']['config']}, hot {out['hot']['us']:.2f} us ({out['hot']['gbps']:.0f} GB/s) {out['hot']['config']}")
+    return out
+
+
+def call_time(dev: Dev, fmt: str, W, x: np.ndarray, pool, layout: str, n_calls: int, warmup: int) -> float:
+    """Median wall time (us) of one Python call lowbit_amd.gemm_<fmt>(x, handle) on
+    resident weights, rotating over the same pool of copies as the kernel timing: the
+    whole synchronous call through ctypes (pad X, X to the device, the GEMM, Y back),
+    as the reference times its calls (src/lowbit/bench.py:116-124)."""
+    K = dev.K
+    handles = []
+    for b in pool:
+        if fmt == "mxfp4":
+            h = K.DeviceMXFP4Weights(None, None, W.n, W.kp, W.k, W.nbytes)
+            if layout == "t16":
+                h.t16 = (b[0], b[1])
+            else:
+                h.qw, h.e8m0 = b[0], b[1]
+        else:
+            h = K.DeviceInt4Weights(None, None, None, W.n, W.kp, W.k, W.nbytes)
+            if layout == "t16":
+                h.t16 = (b[0], b[1], b[2])
+            else:
+                h.qw, h.scales, h.zeros = b[0], b[1], (b[2] if len(b) > 2 else None)
+        handles.append(h)
+    fn = K.GEMMS[fmt]
+    for i in range(max(3, warmup)):
+        fn(x, handles[i % len(handles)])
+    ts = []
+    for i in range(n_calls):
+        h = handles[i % len(handles)]
+        t0 = time.perf_counter()
+        fn(x, h)
+        ts.append(time.perf_counter() - t0)
+    return round(float(np.median(ts)) * 1e6, 2)
 
 
 def rel_err(fmt: str, W, x, y) -> float:
@@ -263,53 +348,134 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(W, x: np.ndarray, budget_s: float) -> dict | None:
-    """lb_gemm_w4a8 of the reference's C library at M=1 11008x4096, weights rotated past
-    2x the host LLC, median of >= 3 reps after a warm-up (src/lowbit/bench.py:116-124)."""
+def host_cpu() -> dict:
+    """nproc, the CPUs this process may use, the lscpu model name, sockets and cores
+    per socket (the run metadata the reference's bench records, src/lowbit/bench.py:280-291)."""
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": cpu_model(),
+            "sockets": None, "cores_per_socket": None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for ln in out.splitlines():
+            key, _, val = ln.partition(":")
+            if key.strip() == "Socket(s)":
+                info["sockets"] = int(val.strip())
+            elif key.strip() == "Core(s) per socket":
+                info["cores_per_socket"] = int(val.strip())
+            elif key.strip() == "Model name":
+                info["model"] = val.strip()
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    info["avx512_vnni"] = "avx512_vnni" in Path("/proc/cpuinfo").read_text() if Path("/proc/cpuinfo").exists() else None
+    return info
+
+
+# The CPU share a one-GPU job may use on the GPU boxes (their worker pools are sized
+# to it): the baseline never runs more threads than this.
+CPU_SHARE = 16
+
+
+def cpu_threads(info: dict) -> int:
+    """Threads for the multi-thread leg: the cores of one socket, capped by the CPUs
+    this process may use and by the job's CPU share."""
+    one_socket = info.get("cores_per_socket") or info["affinity"]
+    return max(1, min(one_socket, info["affinity"], CPU_SHARE))
+
+
+def cpu_baseline_run(budget_s: float) -> dict | None:
+    """Every decode format of the reference's own C library (oracle/_ref) at M=1
+    11008x4096, at 1 thread and at cpu_threads() threads, weights rotated past 2x the
+    host LLC, median of >= 3 calls after a warm-up (src/lowbit/bench.py:116-124).
+    Runs in a child process started with OMP_PROC_BIND=close, OMP_PLACES=cores."""
     from dataclasses import replace
 
+    import lowbit_amd as lb
     from lowbit_amd import formats as F
     from oracle import cref
     L = cref.ref_lib()
     if L is None:
         return None
-    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    info = host_cpu()
+    threads = cpu_threads(info)
+    rng = np.random.default_rng(0)
+    m, n, k = DECODE
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w4 = lb.quantize_int4(w, asym=True)
+    weights = {"w4a8": w4, "w4a16": w4, "mxfp4": lb.quantize_mxfp4(w)}
     llc = host_llc_bytes()
-    copies = min(max(1, math.ceil(max(2 * llc, 512 << 20) / W.nbytes)), max(1, (3 << 30) // W.nbytes))
-    pool = [W] + [replace(W, qw=W.qw.copy(), scales=W.scales.copy(),
-                          zeros=None if W.zeros is None else W.zeros.copy()) for _ in range(copies - 1)]
-    xp = F.pad_acts(x, W.kp)
-    y = np.empty((x.shape[0], W.n), np.float32)
-    res = {}
-    for nt in sorted({1, threads}):
-        p = cref.RefParams(-1, 0, 0, 0, 0, 0, nt)
-        isa = L.lb_effective_isa(2, -1)
+    legs = {}
+    kind_id = {"w4a16": 0, "mxfp4": 1, "w4a8": 2}
+    isa_names = {0: "scalar", 1: "avx2", 2: "avx512"}
+    for fmt, W in weights.items():
+        copies = min(max(1, math.ceil(max(2 * llc, 512 << 20) / W.nbytes)), max(1, (3 << 30) // W.nbytes))
+        if fmt == "mxfp4":
+            pool = [W] + [replace(W, qw=W.qw.copy(), e8m0=W.e8m0.copy()) for _ in range(copies - 1)]
+        else:
+            pool = [W] + [replace(W, qw=W.qw.copy(), scales=W.scales.copy(),
+                                  zeros=None if W.zeros is None else W.zeros.copy()) for _ in range(copies - 1)]
+        xp = F.pad_acts(x, W.kp)
+        y = np.empty((m, n), np.float32)
+        for nt in sorted({1, threads}):
+            p = cref.RefParams(-1, 0, 0, 0, 0, 0, nt)
 
-        def call(i):
-            w = pool[i % len(pool)]
-            rc = L.lb_gemm_w4a8(xp, xp.shape[0], w.kp, w.qw, w.scales, cref.zp(w.zeros), w.n, y, C.byref(p))
-            assert rc >= 0, rc
+            def call(i):
+                wi = pool[i % len(pool)]
+                if fmt == "w4a8":
+                    rc = L.lb_gemm_w4a8(xp, m, wi.kp, wi.qw, wi.scales, cref.zp(wi.zeros), n, y, C.byref(p))
+                elif fmt == "w4a16":
+                    rc = L.lb_gemm_w4a16(xp, m, wi.kp, wi.qw, wi.scales, cref.zp(wi.zeros), n, y, C.byref(p))
+                else:
+                    rc = L.lb_gemm_mxfp4(xp, m, wi.kp, wi.qw, wi.e8m0, n, y, C.byref(p))
+                assert rc >= 0, rc
 
-        call(0)
-        ts, i, t_end = [], 1, time.perf_counter() + budget_s / 2
-        while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 2000):
-            t0 = time.perf_counter()
-            call(i)
-            ts.append(time.perf_counter() - t0)
-            i += 1
-        med = float(np.median(ts))
-        res[nt] = {"s": med, "reps": len(ts), "isa": {0: "scalar", 1: "avx2", 2: "avx512-vnni"}.get(isa, isa)}
-    nt = threads
+            call(0)
+            ts, i, t_end = [], 1, time.perf_counter() + budget_s / (2 * len(weights))
+            while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 2000):
+                t0 = time.perf_counter()
+                call(i)
+                ts.append(time.perf_counter() - t0)
+                i += 1
+            med = float(np.median(ts))
+            isa = L.lb_effective_isa(kind_id[fmt], -1)
+            legs[f"{fmt}_{nt}t"] = {"us": round(med * 1e6, 1), "weight_gbps": round(W.nbytes / med / 1e9, 2),
+                                    "reps": len(ts), "threads": nt,
+                                    "isa": isa_names.get(isa, isa) + ("-vnni" if fmt == "w4a8" and isa == 2 else ""),
+                                    "pool_copies": copies}
+    return {"legs": legs, "threads": threads, "host": info, "llc_bytes": llc,
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND"), "omp_places": os.environ.get("OMP_PLACES")}
+
+
+def cpu_baseline(budget_s: float) -> dict | None:
+    """The CPU baseline of the JSON line, measured by cpu_baseline_run in a child
+    process (OpenMP reads its binding from the environment at start-up)."""
+    env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
+    r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-only",
+                        "--cpu-seconds", str(budget_s)], capture_output=True, text=True, env=env,
+                       timeout=600)
+    if r.returncode != 0:
+        log(f"cpu baseline child failed (rc {r.returncode}): {r.stderr[-2000:]}")
+        return None
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    if res is None:
+        return None
+    nt = res["threads"]
+    head = res["legs"][f"w4a8_{nt}t"]
+    one = res["legs"]["w4a8_1t"]
+    h = res["host"]
     return {
-        "value": round(W.nbytes / res[nt]["s"] / 1e9, 2),
+        "value": head["weight_gbps"],
         "unit": "weight GB/s",
         "cores": nt,
         "kind": "reference",
-        "sample": (f"reference C lb_gemm_w4a8 (oracle/_ref, {res[nt]['isa']} path), M=1 N={W.n} K={W.k} "
-                   f"int4 g128 asym, {copies} rotating weight copies (> 2x {llc >> 20} MiB LLC), "
-                   f"median of {res[nt]['reps']} calls: {res[nt]['s'] * 1e6:.0f} us at {nt} threads, "
-                   f"{res[1]['s'] * 1e6:.0f} us at 1 thread ({W.nbytes / res[1]['s'] / 1e9:.2f} GB/s); "
-                   f"host {cpu_model()}"),
+        "sample": (f"reference C lb_gemm_w4a8 (oracle/_ref, {head['isa']} path), M=1 N=11008 K=4096 int4 g128 "
+                   f"asym, {head['pool_copies']} rotating weight copies (> 2x the {res['llc_bytes'] >> 20} MiB "
+                   f"LLC), median of {head['reps']} calls: {head['us']:.0f} us at {nt} threads "
+                   f"(OMP_PROC_BIND=close), {one['us']:.0f} us at 1 thread ({one['weight_gbps']:.2f} GB/s); host "
+                   f"{h['model']}, {h['sockets']} socket(s) x {h['cores_per_socket']} cores, nproc "
+                   f"{h['nproc']}, {h['affinity']} CPUs usable, threads capped at one socket and the job's "
+                   f"{CPU_SHARE}-CPU share"),
+        "legs": res["legs"],
+        "host": h,
     }
 
 
@@ -387,7 +553,15 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the plain 16-byte copy kernel 5 times over MIB MiB (the reference "
                          "point that scales the FETCH_SIZE / WRITE_SIZE counters), then exit")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only sweep the plain streaming read of the headline weight bytes (cold and hot) "
+                         "and print its JSON")
+    ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor sweep")
+    ap.add_argument("--cpu-baseline-only", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_baseline_only:
+        print(json.dumps(cpu_baseline_run(args.cpu_seconds)), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the hot path has no "
               "multi-GPU part in this build; run with --gpus 1.", file=sys.stderr)
@@ -410,6 +584,11 @@ def main() -> int:
     info = dev.K.cpu_info()
     log(f"device {info.get('arch')} with {info.get('compute_units')} CUs")
     graph = not args.no_graph
+    headline_bytes = 11008 * (4096 // 2 + (4096 // 128) * 5)  # int4 g128 asym weights of the headline
+    if args.read_floor:
+        print(json.dumps({"read_floor": read_floor(dev, headline_bytes, args.steps, args.warmup, graph)}),
+              flush=True)
+        return 0
     if args.only_decoder:
         print(json.dumps({"decoder": measure_decoder(["w4a8", "mxfp4"], graph=graph)}), flush=True)
         return 0
@@ -430,7 +609,9 @@ def main() -> int:
         r["hbm_frac"] = round(r["weight_gbps"] / HBM_PEAK_GBS, 4)
         results[f"{fmt}_decode"] = r
         log(f"{fmt:6s} M=1 cold: {r['us_per_call']:8.2f} us  {r['weight_gbps']:7.1f} GB/s "
-            f"({100 * r['hbm_frac']:.1f}% HBM)  path {r['path']}  rel err {r['max_rel_err']}")
+            f"({100 * r['hbm_frac']:.1f}% HBM)  path {r['path']}  rel err {r['max_rel_err']}  "
+            f"call through ctypes {r['call_us']:.1f} us  ({r['timed_launches']} launches, "
+            f"{r['bytes_rotated'] >> 20} MiB rotated)")
 
     # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167)
     if not args.only_headline:
@@ -438,7 +619,7 @@ def main() -> int:
         xb = rng.standard_normal((mb, kb)).astype(np.float32)
         for fmt in ["w4a8", "w4a16", "mxfp4"]:
             W = mx if fmt == "mxfp4" else w4
-            r = measure(dev, fmt, BATCH, W, xb, cold=False, steps=max(20, args.steps // 4),
+            r = measure(dev, fmt, BATCH, W, xb, cold=False, steps=args.steps,
                         warmup=max(2, args.warmup // 4), graph=graph)
             r["max_rel_err"] = float(f"{rel_err(fmt, W, xb, r.pop('y')):.3g}")
             if fmt == "w4a8":
@@ -454,7 +635,15 @@ def main() -> int:
                 r["mfma_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
             results[f"{fmt}_m64"] = r
             log(f"{fmt:6s} M=64 hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
-                f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}")
+                f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}  "
+                f"call through ctypes {r['call_us']:.1f} us")
+
+    floor = None
+    if not args.no_floor:
+        floor = read_floor(dev, headline_bytes, args.steps, args.warmup, graph)
+        for kk, r in results.items():
+            if r["M"] == 1:
+                r["frac_of_read_floor"] = round(floor["cold"]["us"] / r["us_per_call"], 4)
 
     decoder = None
     if not (args.only_headline or args.no_decoder):
@@ -468,7 +657,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline(w4, x, args.cpu_seconds)
+            cpu = cpu_baseline(args.cpu_seconds)
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline failed: {e}")
     line = {
@@ -492,7 +681,16 @@ def main() -> int:
         "hbm_frac": head["hbm_frac"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
-                     "algorithmic_bytes": int(algo_bytes)},
+                     "algorithmic_bytes": int(algo_bytes),
+                     # the fastest plain read of the same weight bytes, timed the same way
+                     "read_floor": None if floor is None else {
+                         "cold_us": floor["cold"]["us"], "cold_gbps": floor["cold"]["gbps"],
+                         "hot_us": floor["hot"]["us"], "hot_gbps": floor["hot"]["gbps"],
+                         "config": floor["cold"]["config"],
+                         "frac_of_floor": round(floor["cold"]["us"] / head["us_per_call"], 4)}},
+        "timed_launches": head["timed_launches"],
+        "bytes_rotated": head["bytes_rotated"],
+        "call_us": head["call_us"],
         "cpu_baseline": cpu,
         "per_format": {kk: {f: v for f, v in vv.items() if f not in ("N", "K")} for kk, vv in results.items()},
         "decoder": decoder,

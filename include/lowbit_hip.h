@@ -160,6 +160,20 @@ int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp,
  * 1 = MXFP4, 2 = W4A8 with this shape and lb_params runs in (no reference
  * counterpart; the reference's effective ISA does not depend on the shape) */
 int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p);
+/* The regime and, on the small-M (VALU) path, the kernel configuration an lbd_gemm_*
+ * of kind 0 = W4A16, 1 = MXFP4, 2 = W4A8 with this shape takes on the current device
+ * (a test and measurement hook, no reference counterpart: the reference's GEMMs
+ * report only their ISA). Fields past `path` are 0 on the matrix-core path. */
+typedef struct {
+  int path;              /* LB_ISA_GFX950 or LB_ISA_GFX950_MFMA */
+  int workgroups;        /* grid of the small-M launch */
+  int rows_per_wave;     /* weight rows each wave owns */
+  int rows_held;         /* weight rows each wave has in flight at once */
+  int chunks_per_lane;   /* 16-byte chunks per lane per weight row */
+  int two_rows_per_load; /* 1 where each wave load covers two short rows */
+  int act_rows;          /* activation rows per launch */
+} lbd_plan;
+int lbd_gemm_plan(int kind, int M, int N, int Kp, const lb_params *p, lbd_plan *out);
 
 /* ---- MFMA tile layout ("t16") of int4 g128 weights (no reference counterpart:
  *      a device-private copy of an Int4Weights matrix, src/lowbit/formats.py:56-87,
@@ -368,6 +382,10 @@ int lb_dev_free(void *ptr);
 int lb_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int lb_memcpy_d2h(void *dst, const void *src, size_t bytes);
 int lb_memcpy_d2d(void *dst, const void *src, size_t bytes);
+/* the same copies enqueued on `stream` (host memory may be pageable: the runtime
+ * stages it, so the host buffer must stay valid until the stream is synchronised) */
+int lb_memcpy_h2d_async(void *dst, const void *src, size_t bytes, void *stream);
+int lb_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream);
 int lb_memset_d(void *dst, int value, size_t bytes);
 int lb_dev_synchronize(void);
 int lb_stream_create(void **stream);
@@ -389,6 +407,13 @@ int lb_graph_destroy(void *graph_exec);
 /* plain streaming copy kernel of `bytes` (multiple of 16) on `stream`: the known-size
  * reference for scaling HBM traffic counters */
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
+/* plain streaming read of `bytes` (multiple of 16, below 4 GiB, 16-byte aligned) by
+ * `workgroups` workgroups of `threads` (256 or 512) threads, `loads` (1, 2, 4 or 8)
+ * 16-byte loads in flight per thread; each workgroup reads one contiguous range.
+ * `sink` is one device dword (written only if the XOR of the data hits a fixed
+ * value). The HBM read floor the decode GEMVs are measured against. */
+int lbd_read_kernel(const void *src, size_t bytes, int workgroups, int threads, int loads, uint32_t *sink,
+                    void *stream);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,7 @@ CSRC = PKG / "csrc"
 INCLUDE = PKG.parent / "include"
 LIBDIR = PKG / "_lib"
 LIBNAME = "liblowbit_hip.so"
-SOURCES = ["lb_api.hip", "lb_kernels.hip", "lb_gemv_g32.hip", "lb_model.hip", "lb_wquant.hip"]
+SOURCES = ["lb_api.hip", "lb_kernels.hip", "lb_gemv_g32.hip", "lb_model.hip", "lb_wquant.hip", "lb_probe.hip"]
 
 # -packed-fp32-ops off: the compiler must not emit packed fp32 VALU ops.
 # Denormals are kept (the E8M0 scale 2^-127 is a float32 subnormal) and no

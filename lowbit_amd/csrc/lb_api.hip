@@ -187,11 +187,15 @@ int env_cap() {
   return cap;
 }
 
-// The regime a GEMM runs in. A VALU request the shape cannot use is clamped to
-// the matrix-core kernels, the way the reference clamps an ISA request.
+// The regime a GEMM runs in. The request is first clamped to the LOWBIT_ISA cap
+// (a matrix-core request under LOWBIT_ISA=gfx950 becomes a VALU request), as the
+// reference clamps every request to its cap (src/lowbit/csrc/dispatch.c:77-80,151).
+// A VALU request the shape cannot use then falls to the matrix-core kernels: they
+// are the only ones that run it.
 int choose_path(int fmt, int M, int Kp, const lb_params *p) {
   const bool valu_ok = lbk::gemv_eligible(fmt, M, Kp);
-  const int req = p ? p->isa : -1;
+  int req = p ? p->isa : -1;
+  if (req == LB_ISA_GFX950_MFMA && env_cap() < LB_ISA_GFX950_MFMA) req = env_cap();
   if (req == LB_ISA_GFX950_MFMA) return LB_ISA_GFX950_MFMA;
   return valu_ok ? LB_ISA_GFX950 : LB_ISA_GFX950_MFMA;
 }
@@ -435,6 +439,31 @@ int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p) {
   if (kind < 0 || kind > 2) return fail(LB_ERR_ARG, "unknown GEMM kind");
   if (M <= 0 || Kp <= 0) return fail(LB_ERR_SHAPE, "bad shape");
   return ok(choose_path(fmts[kind], M, Kp, p));
+}
+
+int lbd_gemm_plan(int kind, int M, int N, int Kp, const lb_params *p, lbd_plan *out) {
+  static const int fmts[] = {lbk::F_W4A16, lbk::F_MXFP4, lbk::F_W4A8};
+  if (kind < 0 || kind > 2 || !out) return fail(LB_ERR_ARG, "unknown GEMM kind or null plan");
+  int rc = check_shape(M, Kp, N, kind == 1 ? LB_MXBLOCK : LB_GROUP);
+  if (rc < 0) return rc;
+  std::memset(out, 0, sizeof *out);
+  out->path = choose_path(fmts[kind], M, Kp, p);
+  if (out->path != LB_ISA_GFX950) return ok(out->path);
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  lbk::GemmArgs a;
+  a.M = M; a.Kp = Kp; a.N = N;
+  lbk::GemvPlan g;
+  hipError_t e = lbk::launch_gemv(fmts[kind], a, cus, nullptr, &g);
+  if (e != hipSuccess) return fail_hip(e, "small-M plan");
+  out->workgroups = g.workgroups;
+  out->rows_per_wave = g.rows_per_wave;
+  out->rows_held = g.rows_held;
+  out->chunks_per_lane = g.chunks_per_lane;
+  out->two_rows_per_load = g.two_rows_per_load;
+  out->act_rows = g.act_rows;
+  return ok(out->path);
 }
 
 int lbd_quantize_int4(const float *w, int N, int K, int asym, int signed_max, uint8_t *qw, float *scales,
@@ -1104,6 +1133,16 @@ int lb_memcpy_d2h(void *dst, const void *src, size_t bytes) {
   LB_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
   return ok(0);
 }
+int lb_memcpy_h2d_async(void *dst, const void *src, size_t bytes, void *stream) {
+  LB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream)),
+         "hipMemcpyAsync H2D");
+  return ok(0);
+}
+int lb_memcpy_d2h_async(void *dst, const void *src, size_t bytes, void *stream) {
+  LB_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)),
+         "hipMemcpyAsync D2H");
+  return ok(0);
+}
 int lb_memcpy_d2d(void *dst, const void *src, size_t bytes) {
   LB_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice), "hipMemcpy D2D");
   return ok(0);
@@ -1179,6 +1218,18 @@ int lb_graph_launch(void *graph_exec, void *stream) {
 }
 int lb_graph_destroy(void *graph_exec) {
   LB_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+  return ok(0);
+}
+int lbd_read_kernel(const void *src, size_t bytes, int workgroups, int threads, int loads, uint32_t *sink,
+                    void *stream) {
+  if (!src || !sink || !aligned16(src)) return fail(LB_ERR_ARG, "read needs a 16-byte aligned source and a sink");
+  if (bytes == 0 || bytes % 16 || bytes > 0xFFFFFFF0u || workgroups <= 0 || workgroups > 65536 ||
+      (threads != 256 && threads != 512) || (loads != 1 && loads != 2 && loads != 4 && loads != 8))
+    return fail(LB_ERR_ARG, "read: bytes a multiple of 16 below 4 GiB, 1..65536 workgroups of 256 or 512 "
+                            "threads, 1/2/4/8 loads");
+  hipError_t e = lbk::launch_stream_read(src, bytes, workgroups, threads, loads, sink,
+                                         static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "read kernel launch");
   return ok(0);
 }
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {

@@ -537,48 +537,66 @@ using GemvFn = void (*)(GemmArgs);
 
 // Rows held at once (R) from the share of rows each wave gets under the
 // persistent grid, for NIT register-held chunks per lane.
+// A chosen instantiation: the kernel, its weight rows held per batch (R slots; two
+// rows each under HW) and its 16-byte chunks per lane per row.
+struct GemvPick {
+  GemvFn fn = nullptr;
+  int R = 0, nit = 0;
+  bool hw = false;
+};
+
+template <int F, int MB, int R, int NIT, int PRO, bool HW = false>
+static GemvPick gemv_pick() {
+  GemvPick p;
+  p.fn = gemv_kernel<F, MB, R, NIT, PRO, HW>;
+  p.R = R;
+  p.nit = NIT;
+  p.hw = HW;
+  return p;
+}
+
 template <int F, int MB, int NIT, int PRO>
-static GemvFn pick_gemv_nit(int rpw) {
+static GemvPick pick_gemv_nit(int rpw) {
   // rows held at once: R * NIT chunks of weights must stay in registers next to the
   // activations (larger shares are processed R rows at a time)
   constexpr int RMAX = MB == 1 ? (NIT >= 8 ? 1 : NIT >= 4 ? 2 : 4) : MB == 2 ? (NIT >= 4 ? 1 : 2) : 1;
   if constexpr (RMAX == 1) {
-    return gemv_kernel<F, MB, 1, NIT, PRO>;
+    return gemv_pick<F, MB, 1, NIT, PRO>();
   } else if constexpr (RMAX == 2) {
-    return rpw <= 1 ? gemv_kernel<F, MB, 1, NIT, PRO> : gemv_kernel<F, MB, 2, NIT, PRO>;
+    return rpw <= 1 ? gemv_pick<F, MB, 1, NIT, PRO>() : gemv_pick<F, MB, 2, NIT, PRO>();
   } else {
-    if (rpw <= 1) return gemv_kernel<F, MB, 1, NIT, PRO>;
-    if (rpw <= 2) return gemv_kernel<F, MB, 2, NIT, PRO>;
-    if (rpw <= 3) return gemv_kernel<F, MB, 3, NIT, PRO>;
-    return gemv_kernel<F, MB, 4, NIT, PRO>;
+    if (rpw <= 1) return gemv_pick<F, MB, 1, NIT, PRO>();
+    if (rpw <= 2) return gemv_pick<F, MB, 2, NIT, PRO>();
+    if (rpw <= 3) return gemv_pick<F, MB, 3, NIT, PRO>();
+    return gemv_pick<F, MB, 4, NIT, PRO>();
   }
 }
 
 // Two rows per wave load (HW) for rows of at most 32 chunks: R slots of two rows.
 template <int F, int PRO>
-static GemvFn pick_gemv_hw(int rpw) {
+static GemvPick pick_gemv_hw(int rpw) {
   const int slots = (rpw + 1) / 2;
-  if (slots <= 1) return gemv_kernel<F, 1, 1, 1, PRO, true>;
-  if (slots <= 2) return gemv_kernel<F, 1, 2, 1, PRO, true>;
-  if (slots <= 3) return gemv_kernel<F, 1, 3, 1, PRO, true>;
-  return gemv_kernel<F, 1, 4, 1, PRO, true>;
+  if (slots <= 1) return gemv_pick<F, 1, 1, 1, PRO, true>();
+  if (slots <= 2) return gemv_pick<F, 1, 2, 1, PRO, true>();
+  if (slots <= 3) return gemv_pick<F, 1, 3, 1, PRO, true>();
+  return gemv_pick<F, 1, 4, 1, PRO, true>();
 }
 
-// The kernel for rows of nit register-held chunks per lane (nch chunks); null where
-// the activations exceed the LDS budget.
+// The kernel for rows of nit register-held chunks per lane (nch chunks); no kernel
+// (fn null) where the activations exceed the LDS budget.
 template <int F, int MB, int PRO>
-static GemvFn pick_gemv(int nit, int nch, int rpw) {
+static GemvPick pick_gemv(int nit, int nch, int rpw) {
   if constexpr (MB == 1 && !fmt_g32(F)) {
     if (nch <= kWave / 2 && rpw >= 2) return pick_gemv_hw<F, PRO>(rpw);
   }
   if constexpr (PRO == 3) {
-    return nit <= 1 ? pick_gemv_nit<F, MB, 1, PRO>(rpw) : nullptr;
+    return nit <= 1 ? pick_gemv_nit<F, MB, 1, PRO>(rpw) : GemvPick();
   } else {
     if (nit <= 1) return pick_gemv_nit<F, MB, 1, PRO>(rpw);
     if (nit <= 2) return pick_gemv_nit<F, MB, 2, PRO>(rpw);
     if (nit <= 4) return pick_gemv_nit<F, MB, 4, PRO>(rpw);
     // fp32 activations of two or more rows longer than 8192 exceed the LDS budget
-    if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return nullptr;
+    if constexpr ((F == F_W4A16 || F == F_MXFP4 || F == F_W4A16G32) && MB >= 2) return GemvPick();
     else return pick_gemv_nit<F, MB, 8, PRO>(rpw);
   }
 }
@@ -591,7 +609,7 @@ static GemvFn pick_gemv(int nit, int nch, int rpw) {
 // it takes one workgroup per CU as well (3-9 % at N = 3072 .. 6144), and so does a
 // W4A8 GEMV with a prologue whose workgroups would get under 32 KB of weights.
 template <int F, int MB, int PRO>
-static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
+static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s, GemvPlan *plan) {
   constexpr bool kQuant = (F == F_W4A8 || F == F_W4A8G32);
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
   const int cus = num_cus > 0 ? num_cus : 256;
@@ -605,11 +623,21 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
     grid = grid < per_cu * cus ? grid : per_cu * cus;
     const int waves = grid * kGemvWaves;
     const int rpw = a.glu ? 2 * ((a.N / 2 + waves - 1) / waves) : (a.N + waves - 1) / waves;
-    const GemvFn k = pick_gemv<F, MB, PRO>(nit, a.Kp >> 5, rpw);
+    const GemvPick pk = pick_gemv<F, MB, PRO>(nit, a.Kp >> 5, rpw);
+    const GemvFn k = pk.fn;
     if (!k) return hipErrorInvalidValue;
     if (per_cu == 2 && grid > cus && gemv_wg_per_cu(reinterpret_cast<const void *>(k), lds) < 2) {
       per_cu = 1;
       continue;
+    }
+    if (plan) {
+      plan->workgroups = grid;
+      plan->rows_per_wave = rpw;
+      plan->rows_held = pk.hw ? 2 * pk.R : pk.R;
+      plan->chunks_per_lane = pk.nit;
+      plan->two_rows_per_load = pk.hw ? 1 : 0;
+      plan->act_rows = MB;
+      return hipSuccess;
     }
     GemmArgs arg = a;
     void *args[] = {&arg};
@@ -620,22 +648,22 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
 }
 
 template <int F>
-static hipError_t launch_gemv_f(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
+static hipError_t launch_gemv_f(const GemmArgs &a, int num_cus, size_t lds, hipStream_t s, GemvPlan *plan) {
   const int pro = gemv_prologue(a);
   if (pro != 0) {
     if (a.M != 1 || (a.norm_w && a.swiglu)) return hipErrorInvalidValue;
     // the prologues act on fp32 rows, and the group-32 formats have none
     if constexpr (F == F_W4A8Q || fmt_g32(F)) return hipErrorInvalidValue;
-    else if (pro == 1) return launch_gemv_mb<F, 1, 1>(a, num_cus, lds, s);
-    else if (pro == 2) return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s);
+    else if (pro == 1) return launch_gemv_mb<F, 1, 1>(a, num_cus, lds, s, plan);
+    else if (pro == 2) return launch_gemv_mb<F, 1, 2>(a, num_cus, lds, s, plan);
     else if (a.Kp > kWave * 32) return hipErrorInvalidValue;  // one chunk per lane
-    else return launch_gemv_mb<F, 1, 3>(a, num_cus, lds, s);
+    else return launch_gemv_mb<F, 1, 3>(a, num_cus, lds, s, plan);
   }
   switch (a.M) {
-    case 1: return launch_gemv_mb<F, 1, 0>(a, num_cus, lds, s);
-    case 2: return launch_gemv_mb<F, 2, 0>(a, num_cus, lds, s);
-    case 3: return launch_gemv_mb<F, 3, 0>(a, num_cus, lds, s);
-    case 4: return launch_gemv_mb<F, 4, 0>(a, num_cus, lds, s);
+    case 1: return launch_gemv_mb<F, 1, 0>(a, num_cus, lds, s, plan);
+    case 2: return launch_gemv_mb<F, 2, 0>(a, num_cus, lds, s, plan);
+    case 3: return launch_gemv_mb<F, 3, 0>(a, num_cus, lds, s, plan);
+    case 4: return launch_gemv_mb<F, 4, 0>(a, num_cus, lds, s, plan);
   }
   return hipErrorInvalidValue;
 }

@@ -5,9 +5,9 @@
 
 namespace lbk {
 
-hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s) {
-  if (fmt == F_W4A16G32) return launch_gemv_f<F_W4A16G32>(a, num_cus, lds, s);
-  if (fmt == F_W4A8G32) return launch_gemv_f<F_W4A8G32>(a, num_cus, lds, s);
+hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s, GemvPlan *plan) {
+  if (fmt == F_W4A16G32) return launch_gemv_f<F_W4A16G32>(a, num_cus, lds, s, plan);
+  if (fmt == F_W4A8G32) return launch_gemv_f<F_W4A8G32>(a, num_cus, lds, s, plan);
   return hipErrorInvalidValue;
 }
 

@@ -90,12 +90,17 @@ constexpr size_t kGemvLdsLimit = 60 * 1024;  // dynamic LDS, leaving room for st
 size_t gemv_lds_bytes(int fmt, int M, int Kp);
 bool gemv_eligible(int fmt, int M, int Kp);
 
-hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
+// The instantiation and grid a small-M launch takes for a shape (the test hook behind
+// lbd_gemm_plan); with a non-null plan, launch_gemv fills it and launches nothing.
+struct GemvPlan {
+  int workgroups = 0, rows_per_wave = 0, rows_held = 0, chunks_per_lane = 0, two_rows_per_load = 0, act_rows = 0;
+};
+hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, GemvPlan *plan = nullptr);
 // Workgroups of a small-M kernel (512 threads, `lds` bytes of dynamic LDS) that fit
 // on one CU at once; asked of the runtime once per kernel and size.
 int gemv_wg_per_cu(const void *kern, size_t lds);
 // the group-32 instantiations of the small-M kernels (lb_gemv_g32.hip)
-hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s);
+hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s, GemvPlan *plan);
 // Per-token int8 quantizer: xq, xs, asum as lb_quant_act_int8, or (tiled) xq and asum
 // in the MFMA path's tiled layout over ceil(M/16)*16 rows, padding rows zero.
 hipError_t launch_quant(const float *x, int M, int Kp, int8_t *xq, float *xs, int32_t *asum, bool tiled,
@@ -113,6 +118,11 @@ hipError_t launch_groupacc_dot4(const int8_t *xq, const int32_t *asum, int M, in
                                 const uint8_t *qw, const uint8_t *zeros, int N,
                                 int32_t *out, hipStream_t s);
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+// Plain streaming read of `bytes` (multiple of 16, below 4 GiB) by `workgroups` groups
+// of `threads` (256 or 512) threads with `loads` (1, 2, 4, 8) 16-byte loads in flight
+// per thread (lb_probe.hip); `sink` is one device dword it almost never writes.
+hipError_t launch_stream_read(const void *src, size_t bytes, int workgroups, int threads, int loads, uint32_t *sink,
+                              hipStream_t s);
 
 // Decoder-layer kernels (lb_model.hip).
 hipError_t launch_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, hipStream_t s);

@@ -157,16 +157,16 @@ int gemv_wg_per_cu(const void *kern, size_t lds) {
   return n;
 }
 
-hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
+hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, GemvPlan *plan) {
   if (!gemv_eligible(fmt, a.M, a.Kp)) return hipErrorInvalidValue;
   const size_t lds = gemv_lds_bytes(fmt, a.M, a.Kp);
   switch (fmt) {
-    case F_W4A16: return launch_gemv_f<F_W4A16>(a, num_cus, lds, s);
-    case F_MXFP4: return launch_gemv_f<F_MXFP4>(a, num_cus, lds, s);
-    case F_W4A8: return launch_gemv_f<F_W4A8>(a, num_cus, lds, s);
-    case F_W4A8Q: return launch_gemv_f<F_W4A8Q>(a, num_cus, lds, s);
+    case F_W4A16: return launch_gemv_f<F_W4A16>(a, num_cus, lds, s, plan);
+    case F_MXFP4: return launch_gemv_f<F_MXFP4>(a, num_cus, lds, s, plan);
+    case F_W4A8: return launch_gemv_f<F_W4A8>(a, num_cus, lds, s, plan);
+    case F_W4A8Q: return launch_gemv_f<F_W4A8Q>(a, num_cus, lds, s, plan);
     case F_W4A16G32:
-    case F_W4A8G32: return launch_gemv_g32(fmt, a, num_cus, lds, s);
+    case F_W4A8G32: return launch_gemv_g32(fmt, a, num_cus, lds, s, plan);
   }
   return hipErrorInvalidValue;
 }

@@ -96,6 +96,8 @@ SIGNATURES = {
     "lb_dev_free": ([_vp], _int),
     "lb_memcpy_h2d": ([_vp, _vp, _sz], _int),
     "lb_memcpy_d2h": ([_vp, _vp, _sz], _int),
+    "lb_memcpy_h2d_async": ([_vp, _vp, _sz, _vp], _int),
+    "lb_memcpy_d2h_async": ([_vp, _vp, _sz, _vp], _int),
     "lb_memcpy_d2d": ([_vp, _vp, _sz], _int),
     "lb_memset_d": ([_vp, _int, _sz], _int),
     "lb_dev_synchronize": ([], _int),
@@ -112,7 +114,9 @@ SIGNATURES = {
     "lb_graph_launch": ([_vp, _vp], _int),
     "lb_graph_destroy": ([_vp], _int),
     "lbd_copy_kernel": ([_vp, _vp, _sz, _vp], _int),
+    "lbd_read_kernel": ([_vp, _sz, _int, _int, _int, _vp, _vp], _int),
     "lbd_gemm_path": ([_int, _int, _int, _pp], _int),
+    "lbd_gemm_plan": ([_int, _int, _int, _int, _pp, C.c_void_p], _int),
     "lbd_int4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_int4_t16": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _vp], _int),
     "lbd_gemm_w4a8_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
@@ -145,6 +149,23 @@ SIGNATURES = {
     "lbd_gemm_w4a8_g32": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp], _int),
     "lbd_quantize_int4_g32": ([_vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp], _int),
 }
+
+
+class LbdPlan(C.Structure):
+    """lbd_plan of include/lowbit_hip.h: the regime and small-M kernel configuration a
+    GEMM shape takes."""
+    _fields_ = [(f, C.c_int) for f in ("path", "workgroups", "rows_per_wave", "rows_held", "chunks_per_lane",
+                                       "two_rows_per_load", "act_rows")]
+
+
+def gemm_plan(kind: str, m: int, n: int, kp: int, isa=None) -> dict:
+    """The path and small-M kernel configuration (lbd_gemm_plan) a GEMM of this shape takes."""
+    p = LbdPlan()
+    prm = _Params(_isa_id(isa), 0, 0, 0, 0, 0, 0)
+    _check(lib().lbd_gemm_plan(KIND_IDS[kind], m, n, kp, C.byref(prm), C.byref(p)), "lbd_gemm_plan", False)
+    out = {f: getattr(p, f) for f, _ in LbdPlan._fields_}
+    out["path"] = ISA_NAMES.get(p.path, "none")
+    return out
 
 
 class LbdFusion(C.Structure):
@@ -305,6 +326,9 @@ class DeviceBuffer:
             pass
 
 
+_TILE_LOCK = threading.Lock()
+
+
 @dataclass
 class DeviceInt4Weights:
     """int4 g128 weights resident in HBM (same layout as Int4Weights).
@@ -325,9 +349,14 @@ class DeviceInt4Weights:
     t16: tuple | None = None
 
     def tiles(self) -> tuple:
-        """(qwt, st, zt or None) in the t16 layout, repacked on first use."""
+        """(qwt, st, zt or None) in the t16 layout, repacked on first use (once, under a
+        lock, and finished before it is returned: calls run on per-thread streams)."""
         if self.group != GROUP:
             raise ValueError("the t16 matrix-core layout holds groups of 128 only")
+        with _TILE_LOCK:
+            return self._tiles()
+
+    def _tiles(self) -> tuple:
         if self.t16 is None:
             L = lib()
             bq, bs, bz = _sz(0), _sz(0), _sz(0)
@@ -339,6 +368,7 @@ class DeviceInt4Weights:
                                          None if self.zeros is None else self.zeros.ptr, self.n, self.kp,
                                          qwt.ptr, st.ptr, None if zt is None else zt.ptr, None),
                    "lbd_repack_int4_t16", False)
+            _check(L.lb_stream_synchronize(None), "lb_stream_synchronize", False)
             self.t16 = (qwt, st, zt)
         return self.t16
 
@@ -356,7 +386,11 @@ class DeviceMXFP4Weights:
     t16: tuple | None = None
 
     def tiles(self) -> tuple:
-        """(qwt, et) in the t16 layout, repacked on first use."""
+        """(qwt, et) in the t16 layout, repacked on first use (as DeviceInt4Weights.tiles)."""
+        with _TILE_LOCK:
+            return self._tiles()
+
+    def _tiles(self) -> tuple:
         if self.t16 is None:
             L = lib()
             bq, be = _sz(0), _sz(0)
@@ -364,6 +398,7 @@ class DeviceMXFP4Weights:
             qwt, et = DeviceBuffer(bq.value), DeviceBuffer(be.value)
             _check(L.lbd_repack_mxfp4_t16(self.qw.ptr, self.e8m0.ptr, self.n, self.kp, qwt.ptr, et.ptr, None),
                    "lbd_repack_mxfp4_t16", False)
+            _check(L.lb_stream_synchronize(None), "lb_stream_synchronize", False)
             self.t16 = (qwt, et)
         return self.t16
 
@@ -421,8 +456,9 @@ def quantize_int4_device(w, asym: bool = False, scale: str = "absmax", shape=Non
     fn = lib().lbd_quantize_int4 if group == GROUP else lib().lbd_quantize_int4_g32
     _check(fn(src.ptr, n, k, int(asym), int(scale == "signed-max"), qw.ptr, sc.ptr, None if z is None else z.ptr,
               stream), "lbd_quantize_int4", False)
-    if stream is not None:
-        _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)  # src may be freed next
+    # finished before the handle is returned: src may be freed next, and GEMMs on
+    # other streams read the result
+    _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)
     nbytes = n * kp // 2 + n * g * 4 + (n * g if asym else 0)
     return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes, group)
 
@@ -435,44 +471,79 @@ def quantize_mxfp4_device(w, shape=None, stream=None) -> "DeviceMXFP4Weights":
     kp = pad_to(k, MXBLOCK)
     qw, e = DeviceBuffer(n * kp // 2), DeviceBuffer(n * kp // MXBLOCK)
     _check(lib().lbd_quantize_mxfp4(src.ptr, n, k, qw.ptr, e.ptr, stream), "lbd_quantize_mxfp4", False)
-    if stream is not None:
-        _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)
+    _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)
     return DeviceMXFP4Weights(qw, e, n, kp, k, n * kp // 2 + n * kp // MXBLOCK)
 
 
-def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
+class _Staging(threading.local):
+    """Per-thread device staging for calls on resident weights: a stream and device
+    buffers for X, Y and the matrix-core workspace, grown on demand and reused by
+    every later call of the thread (so a call allocates nothing once warm)."""
+
+    def __init__(self):
+        self.stream = None
+        self.bufs: dict[str, DeviceBuffer] = {}
+
+    def get_stream(self):
+        if self.stream is None:
+            s = _vp()
+            _check(lib().lb_stream_create(C.byref(s)), "lb_stream_create", False)
+            self.stream = s.value
+        return self.stream
+
+    def buffer(self, name: str, nbytes: int) -> DeviceBuffer:
+        b = self.bufs.get(name)
+        if b is None or b.nbytes < nbytes:
+            if b is not None:
+                _check(lib().lb_stream_synchronize(self.get_stream()), "lb_stream_synchronize", False)
+            b = DeviceBuffer(max(nbytes, 1 << 16))
+            self.bufs[name] = b
+        return b
+
+
+_STAGE = _Staging()
+
+
+def _run_dev(kind: str, w, m: int, dx: int, dy: int, prm: _Params, stream) -> int:
+    """Launch one GEMM on resident weights `w` (device pointers dx / dy) on `stream`;
+    the matrix-core regime reads the t16 tile layout, repacked on first use."""
     L = lib()
-    m = pr.x.shape[0]
-    dx = DeviceBuffer.from_array(pr.x)
-    dy = DeviceBuffer(pr.y.nbytes)
     zp = None if getattr(w, "zeros", None) is None else w.zeros.ptr
-    # the matrix-core regime reads the t16 tile layout of the resident matrix
     mfma = _check(L.lbd_gemm_path(KIND_IDS[kind], m, w.kp, C.byref(prm)), "lbd_gemm_path", False) == ISA_GFX950_MFMA
     if kind in ("w4a16", "mxfp4") and mfma:
-        ws = DeviceBuffer(L.lbd_bf16x3_workspace_bytes(m, w.kp))
+        ws = _STAGE.buffer("ws", L.lbd_bf16x3_workspace_bytes(m, w.kp))
         if kind == "w4a16":
             qwt, st, zt = w.tiles()
-            rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n,
-                                      dy.ptr, C.byref(prm), ws.ptr, ws.nbytes, None)
-        else:
-            qwt, et = w.tiles()
-            rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, w.kp, qwt.ptr, et.ptr, w.n, dy.ptr, C.byref(prm), ws.ptr,
-                                      ws.nbytes, None)
-    elif kind == "w4a16":
-        rc = L.lbd_gemm_w4a16(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm), None)
-    elif kind == "mxfp4":
-        rc = L.lbd_gemm_mxfp4(dx.ptr, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, dy.ptr, C.byref(prm), None)
-    else:
-        ws = DeviceBuffer(L.lbd_w4a8_workspace_bytes(m, w.kp))
-        if mfma:
-            qwt, st, zt = w.tiles()
-            rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n,
-                                     dy.ptr, C.byref(prm), ws.ptr, ws.nbytes, None)
-        else:
-            rc = L.lbd_gemm_w4a8(dx.ptr, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy.ptr, C.byref(prm),
-                                 ws.ptr, ws.nbytes, None)
-    _check(rc, f"lbd_gemm_{kind}")
-    pr.y[...] = dy.to_array(pr.y.shape, np.float32)  # synchronous copy on the null stream
+            return L.lbd_gemm_w4a16_t16(dx, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n, dy,
+                                        C.byref(prm), ws.ptr, ws.nbytes, stream)
+        qwt, et = w.tiles()
+        return L.lbd_gemm_mxfp4_t16(dx, m, w.kp, qwt.ptr, et.ptr, w.n, dy, C.byref(prm), ws.ptr, ws.nbytes, stream)
+    if kind == "w4a16":
+        return L.lbd_gemm_w4a16(dx, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy, C.byref(prm), stream)
+    if kind == "mxfp4":
+        return L.lbd_gemm_mxfp4(dx, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, dy, C.byref(prm), stream)
+    ws = _STAGE.buffer("ws", L.lbd_w4a8_workspace_bytes(m, w.kp))
+    if mfma:
+        qwt, st, zt = w.tiles()
+        return L.lbd_gemm_w4a8_t16(dx, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n, dy,
+                                   C.byref(prm), ws.ptr, ws.nbytes, stream)
+    return L.lbd_gemm_w4a8(dx, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, dy, C.byref(prm), ws.ptr, ws.nbytes,
+                           stream)
+
+
+def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
+    """One call on resident weights: X up, the GEMM, Y down, all on the calling thread's
+    stream and staging buffers, then a synchronisation (the reference's calls are
+    synchronous, src/lowbit/kernels.py:127-135)."""
+    L = lib()
+    m = pr.x.shape[0]
+    s = _STAGE.get_stream()
+    dx = _STAGE.buffer("x", pr.x.nbytes)
+    dy = _STAGE.buffer("y", pr.y.nbytes)
+    _check(L.lb_memcpy_h2d_async(dx.ptr, pr.x.ctypes.data, pr.x.nbytes, s), "lb_memcpy_h2d_async", False)
+    _check(_run_dev(kind, w, m, dx.ptr, dy.ptr, prm, s), f"lbd_gemm_{kind}")
+    _check(L.lb_memcpy_d2h_async(pr.y.ctypes.data, dy.ptr, pr.y.nbytes, s), "lb_memcpy_d2h_async", False)
+    _check(L.lb_stream_synchronize(s), "lb_stream_synchronize", False)
     return pr.y
 
 
@@ -482,11 +553,15 @@ def _g32_gemm(kind: str, pr: _Prepared, w) -> np.ndarray:
     d = w if isinstance(w, DeviceInt4Weights) else to_device(w)
     L = lib()
     m = pr.x.shape[0]
-    dx, dy = DeviceBuffer.from_array(pr.x), DeviceBuffer(pr.y.nbytes)
+    s = _STAGE.get_stream()
+    dx = _STAGE.buffer("x", pr.x.nbytes)
+    dy = _STAGE.buffer("y", pr.y.nbytes)
+    _check(L.lb_memcpy_h2d_async(dx.ptr, pr.x.ctypes.data, pr.x.nbytes, s), "lb_memcpy_h2d_async", False)
     fn = L.lbd_gemm_w4a16_g32 if kind == "w4a16" else L.lbd_gemm_w4a8_g32
-    _check(fn(dx.ptr, m, d.kp, d.qw.ptr, d.scales.ptr, None if d.zeros is None else d.zeros.ptr, d.n, dy.ptr, None),
+    _check(fn(dx.ptr, m, d.kp, d.qw.ptr, d.scales.ptr, None if d.zeros is None else d.zeros.ptr, d.n, dy.ptr, s),
            f"lbd_gemm_{kind}_g32")
-    pr.y[...] = dy.to_array(pr.y.shape, np.float32)  # synchronous copy on the null stream
+    _check(L.lb_memcpy_d2h_async(pr.y.ctypes.data, dy.ptr, pr.y.nbytes, s), "lb_memcpy_d2h_async", False)
+    _check(L.lb_stream_synchronize(s), "lb_stream_synchronize", False)
     return pr.y
 
 

@@ -144,3 +144,35 @@ def test_argmax_slot_count_matches_header():
     from lowbit_amd import model as DM
     m = re.search(r"#define LBD_ARGMAX_SLOTS (\d+)", HEADER.read_text())
     assert m and int(m.group(1)) == DM.ARGMAX_SLOTS
+
+
+_CAP_PROBE = """
+import ctypes as C, json
+from lowbit_amd import kernels as K
+L = K.lib()
+def path(isa, m):
+    return L.lbd_gemm_path(2, m, 4096, C.byref(K._Params(isa, 0, 0, 0, 0, 0, 0)))
+print(json.dumps({"mfma_m1": path(K.ISA_GFX950_MFMA, 1), "auto_m1": path(-1, 1),
+                  "valu_m1": path(K.ISA_GFX950, 1), "mfma_m64": path(K.ISA_GFX950_MFMA, 64),
+                  "valu_m64": path(K.ISA_GFX950, 64)}))
+"""
+
+
+@pytest.mark.parametrize("cap,mfma_m1", [(None, K.ISA_GFX950_MFMA), ("gfx950", K.ISA_GFX950)])
+def test_isa_cap_clamps_requests(cap, mfma_m1):
+    """LOWBIT_ISA=gfx950 clamps a matrix-core request to the VALU kernels where the
+    shape allows, as the reference clamps requests to its cap
+    (src/lowbit/csrc/dispatch.c:77-80,151); shapes the VALU kernels cannot run stay
+    on the matrix cores. Run in a fresh process: the cap is read once."""
+    import json
+    import os
+    import sys
+    env = {k: v for k, v in os.environ.items() if k != "LOWBIT_ISA"}
+    if cap:
+        env["LOWBIT_ISA"] = cap
+    out = subprocess.run([sys.executable, "-c", _CAP_PROBE], capture_output=True, text=True, check=True,
+                         cwd=ROOT, env=env).stdout
+    got = json.loads(out.strip().splitlines()[-1])
+    assert got["mfma_m1"] == mfma_m1
+    assert got["auto_m1"] == got["valu_m1"] == K.ISA_GFX950
+    assert got["mfma_m64"] == got["valu_m64"] == K.ISA_GFX950_MFMA

@@ -1,8 +1,14 @@
-"""Known-answer tests of the packed formats and host quantizers (CPU).
+"""Packed formats and host quantizers of lowbit_amd (CPU only).
 
-Mirrors the reference's format tests (tests/test_formats.py) against lowbit_amd,
-plus cross-checks of the product's packers against the oracle's independent
-unpacker.
+Two kinds of checks:
+
+* known answers, held as data tables below. Each table cites where its values
+  come from: the reference's format definitions (src/lowbit/formats.py) and the
+  values its format tests pin (tests/test_formats.py of the reference);
+* properties of the quantizers over seeded random inputs. These are the
+  half-step error bound, padding that decodes to zero, and the shared-exponent
+  rule. The packers are also checked against the oracle's independent unpacker
+  and quantizer.
 """
 import numpy as np
 import pytest
@@ -10,156 +16,218 @@ import pytest
 from lowbit_amd import formats as F
 from oracle import reference as O
 
+ROWS = 6
 
-@pytest.mark.parametrize("block", [32, 128])
-def test_nibble_pack_roundtrip(rng, block):
-    codes = rng.integers(0, 16, size=(5, 3 * block), dtype=np.uint8)
+
+def _codes_of(index_map, packed):
+    """Codes read back from `packed` through an explicit (byte, shift) map."""
+    byte, shift = index_map
+    return (packed[:, byte] >> shift) & 15
+
+
+def _nibble_map(kp, block):
+    """Closed form of the packed layout: element e of a row sits in byte
+    (e // block) * block/2 + (e % block) % (block/2), low nibble for the first
+    half of its block and high nibble for the second (src/lowbit/csrc/lowbit.h:9-19)."""
+    e = np.arange(kp)
+    half = block // 2
+    byte = (e // block) * half + (e % block) % half
+    shift = np.where((e % block) >= half, 4, 0)
+    return byte, shift
+
+
+# ------------------------------------------------------------------ nibble layout
+
+@pytest.mark.parametrize("block,nblocks", [(32, 1), (32, 5), (128, 1), (128, 3)])
+def test_packed_layout_follows_closed_form(rng, block, nblocks):
+    kp = block * nblocks
+    codes = rng.integers(0, 16, size=(ROWS, kp), dtype=np.uint8)
     packed = F.pack_nibbles(codes, block)
-    assert packed.shape == (5, 3 * block // 2)
+    assert packed.shape == (ROWS, kp // 2) and packed.dtype == np.uint8
+    np.testing.assert_array_equal(_codes_of(_nibble_map(kp, block), packed), codes)
+    # inverse, and the oracle's own unpacker
     np.testing.assert_array_equal(F.unpack_nibbles(packed, block), codes)
-    # documented layout: byte j = elem j (low) | elem j + block/2 (high)
-    assert packed[0, 0] == codes[0, 0] | (codes[0, block // 2] << 4)
-    # the oracle's unpacker (an explicit index map) agrees
     np.testing.assert_array_equal(O.unpack_codes(packed, block), codes)
 
 
-def test_nibble_layout_byte_positions():
-    # element 128g+j -> low nibble of byte 64g+j, element 128g+64+j -> high nibble
-    codes = np.zeros((1, 256), np.uint8)
-    codes[0, 128 + 5] = 3
-    codes[0, 128 + 64 + 5] = 12
-    packed = F.pack_nibbles(codes, 128)
-    assert packed[0, 64 + 5] == (3 | (12 << 4))
-    assert np.count_nonzero(packed) == 1
+def test_single_code_lands_in_one_nibble():
+    for block, elem, byte, high in [(128, 133, 69, False), (128, 197, 69, True), (32, 50, 18, True)]:
+        codes = np.zeros((1, 2 * block), np.uint8)
+        codes[0, elem] = 9
+        packed = F.pack_nibbles(codes, block)
+        assert np.flatnonzero(packed[0]).tolist() == [byte]
+        assert packed[0, byte] == (9 << 4 if high else 9)
 
 
-@pytest.mark.parametrize("asym", [False, True])
-@pytest.mark.parametrize("k", [128, 300, 1, 257])
-def test_int4_roundtrip_error_bound(rng, asym, k):
-    w = rng.standard_normal((7, k)).astype(np.float32) * 3
-    q = F.quantize_int4(w, asym=asym)
-    assert q.kp % 128 == 0 and q.kp >= k
-    wd = q.dequantize()
-    assert wd.shape == w.shape
-    s = np.repeat(q.scales, 128, axis=1)[:, :k]
-    assert np.all(np.abs(wd - w) <= 0.5 * s * (1 + 1e-5) + 1e-7)
-    codes = q.codes()
-    assert codes.max() <= 15
-    zeros = 8 if q.zeros is None else q.zeros[:, -1:]
-    np.testing.assert_array_equal(codes[:, k:], np.broadcast_to(zeros, codes[:, k:].shape))
+# ------------------------------------------------------------------ int4 group 128: known answers
+
+# (name, weights of one 128-element group, asym, scale rule, expected scale, expected zero,
+#  expected codes or None). Values follow the quantizer's closed form
+# (src/lowbit/formats.py:90-142): sym s = max|w| / 7 and q = rint(w / s) + 8;
+# asym s = (max - min) / 15, z = rint(-min / s); a zero scale becomes 1.
+_G = 128
+INT4_KATS = [
+    ("zero group, sym", np.zeros(_G), False, "absmax", 1.0, 8, np.full(_G, 8)),
+    ("zero group, asym", np.zeros(_G), True, "absmax", 1.0, 0, np.zeros(_G)),
+    ("constant 5, sym", np.full(_G, 5.0), False, "absmax", np.float32(5.0) / np.float32(7.0), 8, np.full(_G, 15)),
+    ("constant 5, asym", np.full(_G, 5.0), True, "absmax", np.float32(5.0) / np.float32(15.0), 0, np.full(_G, 15)),
+    ("ramp -1.5..3, asym", np.linspace(-1.5, 3.0, _G), True, "absmax",
+     np.float32(4.5) / np.float32(15.0), 5, None),
+    ("on-grid step 0.25, sym", np.resize(np.arange(-7, 8), _G) * 0.25, False, "absmax", 0.25, 8,
+     np.resize(np.arange(-7, 8), _G) + 8),
+    ("signed max -4, sym", np.resize([-4.0, 1.0, 2.0, -1.0], _G), False, "signed-max", 0.5, 8,
+     np.resize([0, 10, 12, 6], _G)),
+]
 
 
-@pytest.mark.parametrize("k", [128, 300, 1])
-def test_int4_signed_max_scale(rng, k):
-    w = rng.standard_normal((9, k)).astype(np.float32) * 3
-    q = F.quantize_int4(w, scale="signed-max")
-    wd = q.dequantize()
-    s = np.abs(np.repeat(q.scales, 128, axis=1)[:, :k])
-    err = np.abs(wd - w)
-    g = w[:, :128] if k >= 128 else w
-    i = np.abs(g).argmax(axis=1)
-    np.testing.assert_allclose(wd[np.arange(9), i], g[np.arange(9), i], rtol=1e-6)
-    assert np.all(q.codes()[np.arange(9), i] == 0)
-    assert np.all(err <= s * (1 + 1e-5) + 1e-7)
-    assert np.mean(err <= 0.5 * s * (1 + 1e-5) + 1e-7) > 0.95
-    e0 = np.abs(F.quantize_int4(w).dequantize() - w)
-    assert np.mean(err ** 2) <= np.mean(e0 ** 2)
-    with pytest.raises(ValueError):
-        F.quantize_int4(w, asym=True, scale="signed-max")
-    with pytest.raises(ValueError):
-        F.quantize_int4(w, scale="bogus")
+@pytest.mark.parametrize("name,w,asym,rule,scale,zero,codes", INT4_KATS, ids=[k[0] for k in INT4_KATS])
+def test_int4_known_answers(name, w, asym, rule, scale, zero, codes):
+    q = F.quantize_int4(np.asarray(w, np.float32)[None], asym=asym, scale=rule)
+    assert q.scales[0, 0] == np.float32(scale)
+    assert (8 if q.zeros is None else int(q.zeros[0, 0])) == zero
+    if codes is not None:
+        np.testing.assert_array_equal(q.codes()[0], codes)
+    if name.startswith("ramp"):
+        c = q.codes()[0]
+        assert (c[0], c[-1]) == (0, 15)  # min and max land on the ends of the code range
 
 
-def test_int4_exact_on_grid(rng):
-    s = np.float32(0.25)
-    codes = rng.integers(-7, 8, size=(4, 256))
-    codes[:, 0] = 7
-    codes[:, 128] = -7
-    w = (codes * s).astype(np.float32)
+def test_int4_on_grid_weights_are_reproduced_exactly(rng):
+    # every group holds +-7 steps, so max|w| / 7 is exactly the step (reference pins
+    # the same fact, tests/test_formats.py:55-64)
+    steps = rng.integers(-7, 8, size=(4, 2 * _G))
+    steps[:, [0, _G]] = [7, -7]
+    w = (steps * np.float32(0.25)).astype(np.float32)
     q = F.quantize_int4(w)
+    np.testing.assert_array_equal(q.scales, np.float32(0.25))
     np.testing.assert_array_equal(q.dequantize(), w)
-    np.testing.assert_array_equal(q.scales, s)
 
 
-def test_int4_constant_and_zero_groups():
-    w = np.zeros((2, 128), np.float32)
-    w[1] = 5.0
-    for asym in (False, True):
-        q = F.quantize_int4(w, asym=asym)
-        np.testing.assert_allclose(q.dequantize(), w, rtol=0, atol=1e-6)
-    # the documented special cases: zero rows get s = 1 and code z
-    q = F.quantize_int4(w)
-    assert q.scales[0, 0] == 1.0 and np.all(q.codes()[0] == 8)
-    qa = F.quantize_int4(w, asym=True)
-    assert qa.scales[0, 0] == 1.0 and qa.zeros[0, 0] == 0 and np.all(qa.codes()[0] == 0)
+def test_int4_rejects_unknown_rules():
+    w = np.ones((1, 8), np.float32)
+    for kwargs in ({"asym": True, "scale": "signed-max"}, {"scale": "bogus"}):
+        with pytest.raises(ValueError):
+            F.quantize_int4(w, **kwargs)
 
 
-def test_int4_asym_closed_form():
-    # one group with min -1.5 and max 3: s = 4.5/15 = 0.3, z = rint(1.5/0.3) = 5
-    w = np.linspace(-1.5, 3.0, 128, dtype=np.float32)[None]
-    q = F.quantize_int4(w, asym=True)
-    assert q.scales[0, 0] == np.float32(np.float32(4.5) / np.float32(15))
-    assert q.zeros[0, 0] == 5
-    c = q.codes()[0]
-    assert c[0] == 0 and c[-1] == 15
+# ------------------------------------------------------------------ int4: properties
+
+@pytest.mark.parametrize("k", [1, 127, 128, 257, 300])
+@pytest.mark.parametrize("asym", [False, True])
+def test_int4_properties(rng, k, asym):
+    w = (rng.standard_normal((ROWS, k)) * 3).astype(np.float32)
+    q = F.quantize_int4(w, asym=asym)
+    kp = q.kp
+    assert kp % _G == 0 and kp - _G < k <= kp
+    codes = q.codes()
+    assert codes.shape == (ROWS, kp) and codes.max() <= 15
+    step = np.repeat(q.scales, _G, axis=1)[:, :k]
+    err = np.abs(q.dequantize() - w)
+    assert np.all(err <= 0.5 * step * (1 + 1e-5) + 1e-7)  # round to nearest: half a step
+    # the padding decodes to exactly 0: its code is the group's zero-point
+    z = np.full((ROWS, 1), 8) if q.zeros is None else q.zeros[:, -1:]
+    assert np.all(codes[:, k:] == z)
+    # byte-identical with the oracle's decode of the same arrays
+    np.testing.assert_array_equal(O.dequant_int4(q.qw, q.scales, q.zeros, k).astype(np.float32), q.dequantize())
 
 
-def test_e2m1_table_and_rounding():
-    vals = F.E2M1_VALUES
-    c = F.fp32_to_e2m1(vals)
-    np.testing.assert_array_equal(vals[c], vals)
-    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
-    expect = np.array([0.0, 1.0, 1.0, 2.0, 2.0, 4.0, 4.0], np.float32)
-    np.testing.assert_array_equal(vals[F.fp32_to_e2m1(ties)], expect)
-    np.testing.assert_array_equal(vals[F.fp32_to_e2m1(-ties)], -expect)
-    np.testing.assert_array_equal(vals[F.fp32_to_e2m1(np.array([7.9, -100.0], np.float32))], [6.0, -6.0])
-    # canonical +0: tiny negatives round to code 0, never 8
-    assert F.fp32_to_e2m1(np.array([-0.1, -0.0], np.float32)).tolist() == [0, 0]
+@pytest.mark.parametrize("k", [1, 128, 300])
+def test_int4_signed_max_properties(rng, k):
+    w = (rng.standard_normal((9, k)) * 3).astype(np.float32)
+    q = F.quantize_int4(w, scale="signed-max")
+    err = np.abs(q.dequantize() - w)
+    step = np.abs(np.repeat(q.scales, _G, axis=1)[:, :k])
+    # the element of largest magnitude in the first group is code 0 and exact
+    g0 = w[:, :min(k, _G)]
+    i = np.argmax(np.abs(g0), axis=1)
+    r = np.arange(9)
+    assert np.all(q.codes()[r, i] == 0)
+    np.testing.assert_allclose(q.dequantize()[r, i], g0[r, i], rtol=1e-6)
+    # at most one step everywhere (values near -m clip from +8 to +7), half a step
+    # nearly everywhere, and no worse on average than the absmax rule
+    assert np.all(err <= step * (1 + 1e-5) + 1e-7)
+    assert np.mean(err <= 0.5 * step * (1 + 1e-5) + 1e-7) > 0.95
+    assert np.mean(err ** 2) <= np.mean((F.quantize_int4(w).dequantize() - w) ** 2)
 
 
-def test_e8m0_decode():
-    e = np.array([0, 1, 126, 127, 128, 254, 255], np.uint8)
+# ------------------------------------------------------------------ E2M1 / E8M0: known answers
+
+# (input, decoded value): the E2M1 grid maps to itself; ties go to the even code; the
+# range saturates at +-6; -0 and tiny negatives give the canonical +0 code
+# (src/lowbit/formats.py:23-24,182-194; the reference pins the ties and the
+# saturation in tests/test_formats.py:75-91).
+E2M1_KATS = ([(v, v) for v in F.E2M1_VALUES.tolist()] +
+             [(0.25, 0.0), (0.75, 1.0), (1.25, 1.0), (1.75, 2.0), (2.5, 2.0), (3.5, 4.0), (5.0, 4.0),
+              (-0.25, 0.0), (-0.75, -1.0), (-1.25, -1.0), (-1.75, -2.0), (-2.5, -2.0), (-3.5, -4.0),
+              (-5.0, -4.0), (7.9, 6.0), (-100.0, -6.0), (0.3, 0.5), (2.6, 3.0)])
+
+
+def test_e2m1_encode_known_answers():
+    x = np.array([a for a, _ in E2M1_KATS], np.float32)
+    want = np.array([b for _, b in E2M1_KATS], np.float32)
+    np.testing.assert_array_equal(F.E2M1_VALUES[F.fp32_to_e2m1(x)], want)
+    np.testing.assert_array_equal(F.fp32_to_e2m1(np.array([-0.0, -0.1], np.float32)), [0, 0])
+
+
+# (byte, value) of the E8M0 decode: 2^(e - 127), 0 -> the float32 subnormal 2^-127,
+# 255 -> NaN (src/lowbit/formats.py:175-179, src/lowbit/csrc/lowbit.h:84-92; the
+# reference pins these bytes in tests/test_formats.py:94-99)
+E8M0_KATS = [(0, 2.0 ** -127), (1, 2.0 ** -126), (126, 0.5), (127, 1.0), (128, 2.0), (200, 2.0 ** 73),
+             (254, 2.0 ** 127)]
+
+
+def test_e8m0_decode_known_answers():
+    e = np.array([b for b, _ in E8M0_KATS] + [255], np.uint8)
     f = F.e8m0_to_float(e)
-    np.testing.assert_array_equal(f[:6], np.array([2.0**-127, 2.0**-126, 0.5, 1.0, 2.0, 2.0**127], np.float32))
-    assert np.isnan(f[6])
-    assert f[0].view(np.uint32) == 0x00400000  # the float32 subnormal 2^-127
+    np.testing.assert_array_equal(f[:-1], np.array([v for _, v in E8M0_KATS], np.float32))
+    assert np.isnan(f[-1])
+    assert int(f[0].view(np.uint32)) == 0x00400000
 
+
+# ------------------------------------------------------------------ MXFP4: properties and grid
 
 @pytest.mark.parametrize("k", [32, 100, 4096])
-def test_mxfp4_roundtrip(rng, k):
-    w = rng.standard_normal((6, k)).astype(np.float32)
+def test_mxfp4_properties(rng, k):
+    w = rng.standard_normal((ROWS, k)).astype(np.float32)
     q = F.quantize_mxfp4(w)
-    assert q.kp % 32 == 0
-    wd = q.dequantize()
+    assert q.kp % 32 == 0 and q.kp - 32 < k <= q.kp
+    # shared exponent of every block: floor(log2(amax)) - 2
+    blocks = np.zeros((ROWS, q.kp), np.float32)
+    blocks[:, :k] = w
+    amax = np.abs(blocks.reshape(ROWS, -1, 32)).max(axis=2)
+    np.testing.assert_array_equal(q.e8m0.astype(np.int64) - 127, np.floor(np.log2(amax)).astype(np.int64) - 2)
+    # the widest E2M1 step is 2 (4 -> 6), so no value is off by more than 2 scales
     scale = np.repeat(F.e8m0_to_float(q.e8m0), 32, axis=1)[:, :k]
-    assert np.all(np.abs(wd - w) <= 2.0 * scale)
-    blk = np.pad(w, ((0, 0), (0, q.kp - k))).reshape(6, -1, 32)
-    amax = np.abs(blk).max(axis=2)
-    np.testing.assert_array_equal(q.e8m0.astype(int) - 127, np.floor(np.log2(amax)) - 2)
+    assert np.all(np.abs(q.dequantize() - w) <= 2.0 * scale)
+    np.testing.assert_array_equal(O.dequant_mxfp4(q.qw, q.e8m0, k).astype(np.float32), q.dequantize())
 
 
-def test_mxfp4_exact_on_grid(rng):
+def test_mxfp4_grid_values_times_four_are_exact(rng):
+    # block maximum 6 * 4 = 24: floor(log2 24) - 2 = 2, E8M0 byte 129 (the reference pins
+    # the same case, tests/test_formats.py:115-123)
     codes = rng.integers(0, 16, size=(3, 64)).astype(np.uint8)
-    codes[:, 0] = 7
-    codes[:, 32] = 7
-    w = F.E2M1_VALUES[codes] * np.float32(4.0)
+    codes[:, [0, 32]] = 7
+    w = (F.E2M1_VALUES[codes] * np.float32(4.0)).astype(np.float32)
     q = F.quantize_mxfp4(w)
+    assert np.all(q.e8m0 == 129)
     np.testing.assert_array_equal(q.dequantize(), w)
-    np.testing.assert_array_equal(q.e8m0, 129)
 
 
-def test_act_quant(rng):
-    x = rng.standard_normal((4, 200)).astype(np.float32)
+# ------------------------------------------------------------------ per-token int8 activations
+
+@pytest.mark.parametrize("m,k", [(1, 1), (4, 200), (3, 1000)])
+def test_act_quant_properties(rng, m, k):
+    x = rng.standard_normal((m, k)).astype(np.float32)
     a = F.quantize_act_int8(x)
-    assert a.xq.shape == (4, 256) and a.gsum.shape == (4, 2)
-    assert np.all(np.abs(a.xq) <= 127)
-    np.testing.assert_array_equal(a.xq[:, 200:], 0)
-    np.testing.assert_array_equal(a.gsum, a.xq.astype(np.int32).reshape(4, 2, 128).sum(-1))
-    assert np.all(np.abs(a.dequantize()[:, :200] - x) <= 0.5 * a.scale[:, None] * (1 + 1e-6))
+    kp = F.pad_to(k, _G)
+    assert a.xq.shape == (m, kp) and a.gsum.shape == (m, kp // _G)
+    assert np.all(a.xq[:, k:] == 0) and np.abs(a.xq.astype(np.int32)).max() <= 127
+    np.testing.assert_array_equal(a.gsum, a.xq.astype(np.int32).reshape(m, -1, _G).sum(axis=2))
+    assert np.all(np.abs(a.dequantize()[:, :k] - x) <= 0.5 * a.scale[:, None] * (1 + 1e-6))
 
 
 def test_act_quant_matches_oracle(rng):
-    x = rng.standard_normal((5, 1000)).astype(np.float32) * 3
+    x = (rng.standard_normal((5, 1000)) * 3).astype(np.float32)
     x[2] = 0
     a = F.quantize_act_int8(x)
     xq, xs, asum = O.quant_act_int8(x)
@@ -168,10 +236,13 @@ def test_act_quant_matches_oracle(rng):
     np.testing.assert_array_equal(a.gsum, asum)
 
 
-def test_containers_nbytes():
-    w = np.ones((8, 4096), np.float32)
-    assert F.quantize_int4(w, asym=True).nbytes == 8 * (2048 + 32 * 4 + 32)
-    # the metric's effective weight bytes at the BASELINE shape
+# ------------------------------------------------------------------ effective weight bytes
+
+def test_nbytes_is_the_metric_byte_count():
+    # packed codes + fp32 scales (+ uint8 zero-points) or + E8M0 (src/lowbit/formats.py:76-77,163-164)
     n, k = 11008, 4096
-    assert n * k // 2 + n * (k // 128) * 4 + n * (k // 128) == 24_305_664
-    assert n * k // 2 + n * (k // 32) == 23_953_408
+    assert F.quantize_int4(np.ones((8, k), np.float32), asym=True).nbytes == 8 * (k // 2 + (k // 128) * 5)
+    assert F.quantize_int4(np.ones((8, k), np.float32)).nbytes == 8 * (k // 2 + (k // 128) * 4)
+    assert F.quantize_mxfp4(np.ones((8, k), np.float32)).nbytes == 8 * (k // 2 + k // 32)
+    assert n * (k // 2 + (k // 128) * 5) == 24_305_664
+    assert n * (k // 2 + k // 32) == 23_953_408

@@ -1,0 +1,170 @@
+"""GPU parity at the BASELINE configurations' own shapes, against the CPU oracle.
+
+Every shape the benchmark configurations name runs here through the C ABI:
+  C1  W4A16 decode, M=1 N=4096 K=4096, asym and sym weights;
+  C2  all three formats at M=1 N=11008 K=4096 (the headline shape), through the
+      host-pointer ABI (lb_gemm_*) and through resident device handles (lbd_gemm_*),
+      on the small-M kernel configuration bench.py times (asserted via lbd_gemm_plan);
+  C3  W4A8 at M=16 and 64, N=11008 and 4096, K=4096, sym and asym, on both weight
+      layouts of the matrix-core path, plus worst-case operand tiles (codes 0/15,
+      zero-points 0/7/8/15, activations +-127/-128) at 4096 x 4096;
+  C4  W4A16 and MXFP4 at M=1, 16, 64, N=4096 K=11008, rows scaled by LogNormal(0, 0.5)
+      (which spreads the E8M0 block exponents).
+Inputs follow the configurations: X, W ~ N(0, 1) fp32 from a seeded generator.
+
+The bar is the reference's: |y - ref| <= 1e-5 * (|X| @ |W|^T) against float64 for
+W4A16 / MXFP4 (tests/conftest.py:22-27), and 1e-5 times the lane magnitudes
+sum_k q|a| + z|sum a| for W4A8 (tests/test_kernels.py:108-119); the int32 group
+accumulators are compared bit for bit (src/lowbit/reference.py:18-26).
+"""
+from functools import lru_cache
+
+import numpy as np
+import pytest
+
+import lowbit_amd as lb
+from lowbit_amd import kernels as K
+from oracle import cref
+from oracle import reference as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+
+
+@lru_cache(maxsize=None)
+def _weights(n, k, seed, lognormal=False):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    if lognormal:
+        w = (w * rng.lognormal(0.0, 0.5, (n, 1))).astype(np.float32)
+    return w
+
+
+@lru_cache(maxsize=None)
+def _packed(fmt, n, k, seed, asym=False, lognormal=False):
+    w = _weights(n, k, seed, lognormal)
+    return lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=asym)
+
+
+def _x(m, k, seed):
+    return np.random.default_rng(seed + 1).standard_normal((m, k)).astype(np.float32)
+
+
+def _check(fmt, x, W, y):
+    xp = lb.formats.pad_acts(x, W.kp)
+    if fmt == "w4a16":
+        ref = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros)
+        bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
+    elif fmt == "mxfp4":
+        ref = cref.c_gemm_mxfp4(xp, W.qw, W.e8m0)
+        bound = cref.c_gemm_mxfp4(xp, W.qw, W.e8m0, absval=True)
+    else:
+        a = lb.quantize_act_int8(x)
+        ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+    assert y.shape == ref.shape
+    return O.assert_fp_close(y, ref, bound, RTOL)
+
+
+# ------------------------------------------------------------------ C1
+
+@pytest.mark.parametrize("asym", [True, False])
+@pytest.mark.parametrize("resident", [False, True])
+def test_c1_w4a16_decode_4096(asym, resident):
+    W = _packed("w4a16", 4096, 4096, 0, asym)
+    x = _x(1, 4096, 0)
+    y = K.gemm_w4a16(x, lb.to_device(W) if resident else W)
+    assert K.last_path() == "gfx950"
+    _check("w4a16", x, W, y)
+
+
+# ------------------------------------------------------------------ C2 (headline shape)
+
+C2 = [("w4a8", True), ("w4a8", False), ("w4a16", True), ("w4a16", False), ("mxfp4", False)]
+
+
+@pytest.mark.parametrize("fmt,asym", C2)
+def test_c2_plan_is_the_benchmarked_kernel(fmt, asym):
+    """The small-M configuration at 1 x 11008 x 4096: several weight rows in flight per
+    wave, two 16-byte chunks per lane (a row of 4096 is 128 chunks), one activation row."""
+    plan = K.gemm_plan(fmt, 1, 11008, 4096)
+    assert plan["path"] == "gfx950"
+    assert plan["act_rows"] == 1 and plan["chunks_per_lane"] == 2 and plan["two_rows_per_load"] == 0
+    assert plan["rows_held"] >= 2 and plan["rows_held"] >= plan["rows_per_wave"]
+    assert plan["workgroups"] * 8 * plan["rows_per_wave"] >= 11008
+
+
+@pytest.mark.parametrize("resident", [False, True])
+@pytest.mark.parametrize("fmt,asym", C2)
+def test_c2_decode_11008x4096(fmt, asym, resident):
+    W = _packed(fmt, 11008, 4096, 0, asym)
+    x = _x(1, 4096, 0)
+    fn = K.GEMMS[fmt]
+    y = fn(x, lb.to_device(W) if resident else W)
+    assert K.last_path() == "gfx950"
+    _check(fmt, x, W, y)
+    if fmt == "w4a8":
+        a = lb.quantize_act_int8(x)
+        ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+        O.assert_fp_close(K.gemm_w4a8_q(a, W), ref, bound, RTOL)
+
+
+# ------------------------------------------------------------------ C3 (W4A8 batches)
+
+C3 = [(m, n, asym) for m in (16, 64) for n in (11008, 4096) for asym in (True, False)]
+
+
+@pytest.mark.parametrize("resident", [True, False])
+@pytest.mark.parametrize("m,n,asym", C3)
+def test_c3_w4a8_batches(m, n, asym, resident):
+    """Resident handles run on the t16 tile layout, the pointer ABI on the row-major
+    layout; both are the int8 matrix-core path."""
+    W = _packed("w4a8", n, 4096, 1, asym)
+    x = _x(m, 4096, 1)
+    y = K.gemm_w4a8(x, lb.to_device(W) if resident else W)
+    assert K.last_path() == "gfx950-mfma"
+    _check("w4a8", x, W, y)
+
+
+def _adversarial_4096(rng, asym):
+    n = k = 4096
+    g = k // 128
+    codes = rng.choice(np.array([0, 15], np.uint8), size=(n, k))
+    codes[: n // 4] = 15  # whole rows at the top code
+    zeros = rng.choice(np.array([0, 7, 8, 15], np.uint8), size=(n, g)) if asym else None
+    W = lb.Int4Weights(lb.formats.pack_nibbles(codes, 128),
+                       (rng.standard_normal((n, g)) * 0.01).astype(np.float32), zeros, k)
+    xq = rng.choice(np.array([127, -128, -127], np.int8), size=(64, k))
+    xq[0] = -128
+    xq[1] = 127
+    a = lb.Int8Acts(xq, np.abs(rng.standard_normal(64)).astype(np.float32) + 0.01,
+                    xq.astype(np.int32).reshape(64, g, 128).sum(axis=2).astype(np.int32))
+    return W, a
+
+
+@pytest.mark.parametrize("isa", ["gfx950", "gfx950-mfma"])
+@pytest.mark.parametrize("asym", [True, False])
+def test_c3_worst_case_tiles_bit_exact(rng, isa, asym):
+    """64 x 4096 x 4096 of worst-case operands: exact int32 group accumulators on both
+    integer paths, and the fp32 rescale within the bound."""
+    W, a = _adversarial_4096(rng, asym)
+    want = cref.c_group_acc(a.xq, W.qw, W.zeros)
+    assert np.abs(want).max() < 2 ** 31
+    np.testing.assert_array_equal(K.w4a8_group_acc(a, W, isa=isa), want)
+    ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+    O.assert_fp_close(K.gemm_w4a8_q(a, W, isa=isa), ref, bound, RTOL)
+
+
+# ------------------------------------------------------------------ C4 (down-projection shape)
+
+@pytest.mark.parametrize("resident", [True, False])
+@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("fmt,asym", [("mxfp4", False), ("w4a16", True), ("w4a16", False)])
+def test_c4_down_projection_lognormal_rows(fmt, asym, m, resident):
+    W = _packed(fmt, 4096, 11008, 2, asym, lognormal=True)
+    if fmt == "mxfp4":
+        assert len(np.unique(W.e8m0)) > 8  # the row scaling spreads the block exponents
+    x = _x(m, 11008, 2)
+    y = K.GEMMS[fmt](x, lb.to_device(W) if resident else W)
+    assert K.last_path() == ("gfx950" if m == 1 else "gfx950-mfma")
+    _check(fmt, x, W, y)

@@ -242,6 +242,94 @@ def test_gemms_match_reference_c(rng, shape):
     O.assert_fp_close(y, O.gemm_mxfp4_ref(xp, Wm.qw, Wm.e8m0), O.fp_bound(xp, O.dequant_mxfp4(Wm.qw, Wm.e8m0)))
 
 
+# ------------------------------------------------------------------ W4A8 bound pins
+#
+# Every W4A8 GPU test is judged by the `bound` output of the C oracle's
+# orc_gemm_w4a8. The reference defines that scale in tests/test_kernels.py:108-116:
+# per group the lane magnitude sum_k q|a| + z|sum_k a|, weighted by the group scale
+# and multiplied by the token scale. The oracle takes |s| and |xs|, so the bound is
+# a magnitude for signed-max weights too (their scales are negative); for positive
+# scales the two are the same number.
+
+def _bound_operands(rng, m, n, k, asym, rule="absmax"):
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    W = F.quantize_int4(rng.standard_normal((n, k)).astype(np.float32), asym=asym, scale=rule)
+    xq, xs, asum = O.quant_act_int8(F.pad_acts(x, W.kp))
+    return xq, xs, asum, W
+
+
+@pytest.mark.parametrize("tag", ["sym", "asym"])
+def test_w4a8_bound_matches_numpy_restatement_on_golden_vectors(tag):
+    zeros = GOLD[f"ga_{tag}_zeros"] if f"ga_{tag}_zeros" in GOLD.files else None
+    qw, s = GOLD[f"ga_{tag}_qw"], GOLD[f"ga_{tag}_scales"]
+    _, bound = cref.c_gemm_w4a8(GOLD["q_xq"], GOLD["q_xs"], GOLD["q_asum"], qw, s, zeros)
+    np.testing.assert_allclose(bound, O.w4a8_lane_bound(GOLD["q_xq"], GOLD["q_xs"], GOLD["q_asum"], qw, s, zeros),
+                               rtol=1e-13, atol=0)
+
+
+@pytest.mark.parametrize("m,n,k,asym,rule", [(1, 7, 128, True, "absmax"), (3, 5, 300, False, "absmax"),
+                                             (4, 33, 1000, True, "absmax"), (5, 37, 300, False, "signed-max")])
+def test_w4a8_bound_matches_numpy_restatement(rng, m, n, k, asym, rule):
+    xq, xs, asum, W = _bound_operands(rng, m, n, k, asym, rule)
+    y, bound = cref.c_gemm_w4a8(xq, xs, asum, W.qw, W.scales, W.zeros)
+    np.testing.assert_allclose(bound, O.w4a8_lane_bound(xq, xs, asum, W.qw, W.scales, W.zeros), rtol=1e-13, atol=0)
+    # |acc_g| = |sum (q - z) a| <= sum q|a| + z|sum a| for every group, so the bound
+    # dominates the exact result itself
+    assert np.all(np.abs(y) <= bound * (1 + 1e-12))
+    if rule == "absmax":
+        # positive scales: equal to the reference's expression with signed scales
+        # (tests/test_kernels.py:115)
+        q = O.unpack_codes(W.qw, 128).astype(np.float64).reshape(n, -1, 128)
+        z = np.full(W.scales.shape, 8.0) if W.zeros is None else W.zeros.astype(np.float64)
+        mag = (np.einsum("mgk,ngk->mng", np.abs(xq.astype(np.float64)).reshape(m, -1, 128), q)
+               + z[None] * np.abs(asum.astype(np.float64))[:, None, :])
+        refb = np.einsum("mng,ng->mn", mag, W.scales.astype(np.float64)) * xs.astype(np.float64)[:, None]
+        np.testing.assert_allclose(bound, refb, rtol=1e-13, atol=0)
+
+
+def test_w4a8_bound_closed_forms():
+    # one row, one group. Case 1: every code 15, z = 0, every activation -128:
+    #   sum q|a| = 128 * 15 * 128, z|sum a| = 0  ->  245760 * |s| * xs
+    qw = np.full((1, 64), 0xFF, np.uint8)
+    xq = np.full((1, 128), -128, np.int8)
+    asum = np.array([[-128 * 128]], np.int32)
+    _, b = cref.c_gemm_w4a8(xq, np.array([2.0], np.float32), asum, qw, np.array([[0.5]], np.float32),
+                            np.array([[0]], np.uint8))
+    assert b[0, 0] == 245760.0
+    # Case 2: code 3 everywhere, z = 7, activations alternating +1 / -1 (sum 0):
+    #   sum q|a| = 3 * 128 = 384, z|sum a| = 0; a negative scale counts by magnitude
+    qw = np.full((1, 64), 0x33, np.uint8)
+    xq = np.resize(np.array([1, -1], np.int8), (1, 128))
+    y, b = cref.c_gemm_w4a8(xq, np.array([1.0], np.float32), np.array([[0]], np.int32), qw,
+                            np.array([[-0.25]], np.float32), np.array([[7]], np.uint8))
+    assert b[0, 0] == 384 * 0.25 and y[0, 0] == 0.0
+    # Case 3: code 8 = z (symmetric zero row), activations all 5: the exact result is 0
+    #   but the magnitude is sum q|a| + z|sum a| = 8 * 640 + 8 * 640
+    qw = np.full((1, 64), 0x88, np.uint8)
+    xq = np.full((1, 128), 5, np.int8)
+    y, b = cref.c_gemm_w4a8(xq, np.array([1.0], np.float32), np.array([[640]], np.int32), qw,
+                            np.array([[1.0]], np.float32), None)
+    assert y[0, 0] == 0.0 and b[0, 0] == 2 * 8 * 640
+
+
+def test_w4a8_bound_planted_mistakes(rng):
+    """A bound without the zero-point term, or one that measures |acc| instead of the
+    lane magnitudes, must fail the pins above."""
+    xq, xs, asum, W = _bound_operands(rng, 3, 20, 512, True)
+    _, bound = cref.c_gemm_w4a8(xq, xs, asum, W.qw, W.scales, W.zeros)
+    s = np.abs(W.scales.astype(np.float64))
+    q = O.unpack_codes(W.qw, 128).astype(np.float64).reshape(W.n, -1, 128)
+    no_z = np.einsum("mng,ng->mn", np.einsum("mgk,ngk->mng", np.abs(xq.astype(np.float64)).reshape(3, -1, 128), q),
+                     s) * xs[:, None]
+    assert not np.allclose(no_z, bound, rtol=1e-6)
+    acc = O.w4a8_group_acc_ref(xq, W.qw, W.zeros).astype(np.float64)
+    abs_acc = np.einsum("mng,ng->mn", np.abs(acc), s) * xs[:, None]
+    assert not np.allclose(abs_acc, bound, rtol=1e-6)
+    # the |acc| form is never larger: it shrinks wherever a group's sum cancels, the
+    # case the reference's lane magnitudes exist for (tests/test_kernels.py:108-110)
+    assert np.all(abs_acc <= bound * (1 + 1e-12))
+
+
 # ------------------------------------------------------------------ planted mistakes
 
 _UNPACK = O.unpack_codes
