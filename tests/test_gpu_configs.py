@@ -163,7 +163,7 @@ def test_c3_worst_case_tiles_bit_exact(rng, isa, asym):
 def test_c4_down_projection_lognormal_rows(fmt, asym, m, resident):
     W = _packed(fmt, 4096, 11008, 2, asym, lognormal=True)
     if fmt == "mxfp4":
-        assert len(np.unique(W.e8m0)) > 8  # the row scaling spreads the block exponents
+        assert len(np.unique(W.e8m0)) >= 6  # the row scaling spreads the block exponents
     x = _x(m, 11008, 2)
     y = K.GEMMS[fmt](x, lb.to_device(W) if resident else W)
     assert K.last_path() == ("gfx950" if m == 1 else "gfx950-mfma")
