@@ -199,6 +199,17 @@ int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                       const float *st, const uint8_t *zt, int N, float *y,
                       const lb_params *p, void *workspace,
                       size_t workspace_bytes, void *stream);
+/* lbd_gemm_w4a8_t16 without allocation (no reference counterpart: for callers that
+ * cannot allocate device memory, such as code under HIP graph capture and serving
+ * loops that forbid hipMalloc). The quantized activations live in a scratch array of
+ * lbd_noalloc_scratch_bytes() = 8 MiB that the library keeps on each device for the
+ * life of the process, so lbd_w4a8_workspace_bytes(M, Kp) must not exceed it (else
+ * LB_ERR_SHAPE; M * Kp up to about 8 million). Every call on one device shares that
+ * array: calls that overlap on one device (other streams, other threads) race and
+ * must be ordered by the caller. Same results as lbd_gemm_w4a8_t16, bit for bit. */
+size_t lbd_noalloc_scratch_bytes(void);
+int lbd_gemm_w4a8_t16_noalloc(const float *x, int M, int Kp, const uint8_t *qwt, const float *st,
+                              const uint8_t *zt, int N, float *y, const lb_params *p, void *stream);
 /* y = x . w^T as lbd_gemm_w4a16, weights in the t16 layout, on bf16 matrix cores
  * with the float32 semantics of the reference's kernels (src/lowbit/csrc/
  * kern_scalar.c:10-47): x is split exactly into three bf16 terms (in `workspace`,

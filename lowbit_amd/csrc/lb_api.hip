@@ -582,9 +582,12 @@ int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt, const 
   return run_bf3(lbk::F_MXFP4, a, ws, s);
 }
 
-int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
-                      int N, float *y, const lb_params *p, void *workspace, size_t workspace_bytes,
-                      void *stream) {
+}  // extern "C"
+
+namespace {
+
+int check_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt, int N,
+                   float *y, const lb_params *p) {
   int rc = check_shape(M, Kp, N, LB_GROUP);
   if (rc < 0) return rc;
   if ((rc = check_params(p, M)) < 0) return rc;
@@ -593,14 +596,31 @@ int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const f
     return fail(LB_ERR_ARG, "x, qwt and st must be 16-byte aligned");
   if (zt && (reinterpret_cast<uintptr_t>(zt) & 3)) return fail(LB_ERR_ARG, "zt must be 4-byte aligned");
   if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return 0;
+}
+
+lbk::GemmArgs w4a8_t16_args(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
+                            int N, float *y) {
   lbk::GemmArgs a;
   a.x = x; a.qw = qwt; a.scales = st; a.zeros = zt; a.y = y;
   a.M = M; a.Kp = Kp; a.N = N;
   a.wt16 = true;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
+                      int N, float *y, const lb_params *p, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+  int rc = check_w4a8_t16(x, M, Kp, qwt, st, zt, N, y, p);
+  if (rc < 0) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
   char *ws = static_cast<char *>(workspace);
   if ((rc = w4a8_workspace(M, Kp, workspace_bytes, s, &ws)) < 0) return rc;
-  return run_w4a8(a, p, ws, s);
+  return run_w4a8(w4a8_t16_args(x, M, Kp, qwt, st, zt, N, y), p, ws, s);
 }
 
 int lbd_gemm_w4a8_q(const int8_t *xq, const float *xs, const int32_t *asum, int M, int Kp,
@@ -1112,6 +1132,67 @@ int lb_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp, cons
   LB_HIP(hipMemcpyAsync(out, b + oo, bo, hipMemcpyDeviceToHost, s), "copy out");
   LB_HIP(hipStreamSynchronize(s), "synchronize");
   return ok(rc);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free W4A8 (t16)
+//
+// lbd_gemm_w4a8_t16_noalloc keeps the quantized activations in `scratch`, a
+// file-scope device array each GPU holds until the process ends, so the call
+// allocates nothing. Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): the first call on each device takes
+// that device's address of it with hipGetSymbolAddress and every later call uses
+// the address kept for the device.
+
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+
+}  // namespace
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::unordered_map<int, char *> g_scratch;  // device -> that device's address of `scratch`
+
+int scratch_address(char **out) {
+  int dev = 0;
+  int rc = current_device(&dev);
+  if (rc < 0) return rc;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(dev);
+  if (it == g_scratch.end()) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress of the scratch array");
+    if (!p) return fail(LB_ERR_HIP, "hipGetSymbolAddress gave no address for the scratch array");
+    it = g_scratch.emplace(dev, static_cast<char *>(p)).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t lbd_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int lbd_gemm_w4a8_t16_noalloc(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
+                              int N, float *y, const lb_params *p, void *stream) {
+  int rc = check_w4a8_t16(x, M, Kp, qwt, st, zt, N, y, p);
+  if (rc < 0) return rc;
+  const size_t need = w4a8_ws_bytes(M, Kp);
+  if (need > kNoAllocScratchBytes)
+    return fail(LB_ERR_SHAPE, "lbd_gemm_w4a8_t16_noalloc: the quantized activations of this M x Kp need more "
+                              "than its 8 MiB scratch (lbd_w4a8_workspace_bytes(M, Kp) must be at most "
+                              "lbd_noalloc_scratch_bytes())");
+  char *ws = nullptr;
+  if ((rc = scratch_address(&ws)) < 0) return rc;
+  return run_w4a8(w4a8_t16_args(x, M, Kp, qwt, st, zt, N, y), p, ws, static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------- plumbing

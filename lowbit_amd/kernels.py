@@ -121,6 +121,8 @@ SIGNATURES = {
     "lbd_repack_int4_t16": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _vp], _int),
     "lbd_gemm_w4a8_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
     "lbd_gemm_w4a16_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_noalloc_scratch_bytes": ([], _sz),
+    "lbd_gemm_w4a8_t16_noalloc": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp], _int),
     "lbd_bf16x3_workspace_bytes": ([_int, _int], _sz),
     "lbd_mxfp4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_mxfp4_t16": ([_vp, _vp, _int, _int, _vp, _vp, _vp], _int),
