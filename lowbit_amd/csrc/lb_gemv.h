@@ -119,6 +119,87 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
   }
 }
 
+// ---- per-chunk arithmetic, shared by gemv_kernel and gemv_paced_kernel so that the
+//      two give the same bits
+
+// Sum of one chunk's 32 fp32 activations (low-nibble half, then high-nibble half), in
+// the order the W4A16 products are summed, so that sum(q*x) - z*sum(x) is exactly 0
+// when every q == z and z is a power of two (z = 8: symmetric zero rows and padding).
+__device__ __forceinline__ float chunk_xsum(const float4 (&xv)[8]) {
+  float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    sl += xv[p].x; sl += xv[p].y; sl += xv[p].z; sl += xv[p].w;
+    sh += xv[4 + p].x; sh += xv[4 + p].y; sh += xv[4 + p].z; sh += xv[4 + p].w;
+  }
+  return sl + sh;
+}
+
+// W4A16: sum_k (q_k - z) x_k of one 16-byte chunk, as sum q x - z * sum x.
+__device__ __forceinline__ float w4a16_chunk(uint4 w, const float4 (&xv)[8], int z, float xsum) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  float pl = 0.0f, ph = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const uint32_t lo = opaque(lo_nibbles(wd[d])), hi = opaque(hi_nibbles(wd[d]));
+    pl = __builtin_fmaf((float)(lo & 0xFF), xv[d].x, pl);
+    pl = __builtin_fmaf((float)((lo >> 8) & 0xFF), xv[d].y, pl);
+    pl = __builtin_fmaf((float)((lo >> 16) & 0xFF), xv[d].z, pl);
+    pl = __builtin_fmaf((float)(lo >> 24), xv[d].w, pl);
+    ph = __builtin_fmaf((float)(hi & 0xFF), xv[4 + d].x, ph);
+    ph = __builtin_fmaf((float)((hi >> 8) & 0xFF), xv[4 + d].y, ph);
+    ph = __builtin_fmaf((float)((hi >> 16) & 0xFF), xv[4 + d].z, ph);
+    ph = __builtin_fmaf((float)(hi >> 24), xv[4 + d].w, ph);
+  }
+  return __builtin_fmaf(-(float)z, xsum, pl + ph);
+}
+
+// MXFP4: the E2M1 pairs (low nibble, high nibble) of each byte of a chunk, exact in fp32.
+__device__ __forceinline__ void mxfp4_decode(uint4 w, float (&wl)[16], float (&wh)[16]) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const v2f p0 = e2m1_pair<0>(wd[d], 1.0f), p1 = e2m1_pair<1>(wd[d], 1.0f);
+    const v2f p2 = e2m1_pair<2>(wd[d], 1.0f), p3 = e2m1_pair<3>(wd[d], 1.0f);
+    wl[4 * d + 0] = p0.x; wh[4 * d + 0] = p0.y;
+    wl[4 * d + 1] = p1.x; wh[4 * d + 1] = p1.y;
+    wl[4 * d + 2] = p2.x; wh[4 * d + 2] = p2.y;
+    wl[4 * d + 3] = p3.x; wh[4 * d + 3] = p3.y;
+  }
+}
+
+// MXFP4: sum_k e2m1(q_k) x_k of one chunk (before the block scale).
+__device__ __forceinline__ float mxfp4_dot(const float (&wl)[16], const float (&wh)[16], const float4 (&xv)[8]) {
+  float pl = 0.0f, ph = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    pl = __builtin_fmaf(wl[4 * d + 0], xv[d].x, pl);
+    pl = __builtin_fmaf(wl[4 * d + 1], xv[d].y, pl);
+    pl = __builtin_fmaf(wl[4 * d + 2], xv[d].z, pl);
+    pl = __builtin_fmaf(wl[4 * d + 3], xv[d].w, pl);
+    ph = __builtin_fmaf(wh[4 * d + 0], xv[4 + d].x, ph);
+    ph = __builtin_fmaf(wh[4 * d + 1], xv[4 + d].y, ph);
+    ph = __builtin_fmaf(wh[4 * d + 2], xv[4 + d].z, ph);
+    ph = __builtin_fmaf(wh[4 * d + 3], xv[4 + d].w, ph);
+  }
+  return pl + ph;
+}
+
+// W4A8: the exact int32 sum_k q_k a_k of one chunk (int8 dot4 on the unsigned codes,
+// 0..15 being non-negative int8, against the low- and high-half activation codes).
+__device__ __forceinline__ int w4a8_chunk(uint4 w, uint4 al, uint4 ah) {
+  int d = 0;
+  d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.x), (int)al.x, d, false);
+  d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.x), (int)ah.x, d, false);
+  d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.y), (int)al.y, d, false);
+  d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.y), (int)ah.y, d, false);
+  d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.z), (int)al.z, d, false);
+  d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.z), (int)ah.z, d, false);
+  d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.w), (int)al.w, d, false);
+  d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.w), (int)ah.w, d, false);
+  return d;
+}
+
 // acc[m][r] += this lane's share of slot r (r < nr) against activation row m (HW:
 // each half-wave its own row of the slot). Chunks past the row end hold zero
 // weights, zero scales and zero activations.
@@ -137,34 +218,11 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
         for (int p = 0; p < 8; p++)
           xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-        // sum of the 32 activations in the same order as the products below, so
-        // that sum(q*x) - z*sum(x) is exactly 0 when every q == z and z is a power
-        // of two (z = 8: symmetric zero rows and padding)
-        float sl = 0.0f, sh = 0.0f;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-          sl += xv[p].x; sl += xv[p].y; sl += xv[p].z; sl += xv[p].w;
-          sh += xv[4 + p].x; sh += xv[4 + p].y; sh += xv[4 + p].z; sh += xv[4 + p].w;
-        }
-        const float xsum = sl + sh;
+        const float xsum = chunk_xsum(xv);
 #pragma unroll
         for (int r = 0; r < R; r++) {
           if (r >= nr) break;
-          const uint32_t wd[4] = {g.w[r][it].x, g.w[r][it].y, g.w[r][it].z, g.w[r][it].w};
-          float pl = 0.0f, ph = 0.0f;
-#pragma unroll
-          for (int d = 0; d < 4; d++) {
-            const uint32_t lo = opaque(lo_nibbles(wd[d])), hi = opaque(hi_nibbles(wd[d]));
-            pl = __builtin_fmaf((float)(lo & 0xFF), xv[d].x, pl);
-            pl = __builtin_fmaf((float)((lo >> 8) & 0xFF), xv[d].y, pl);
-            pl = __builtin_fmaf((float)((lo >> 16) & 0xFF), xv[d].z, pl);
-            pl = __builtin_fmaf((float)(lo >> 24), xv[d].w, pl);
-            ph = __builtin_fmaf((float)(hi & 0xFF), xv[4 + d].x, ph);
-            ph = __builtin_fmaf((float)((hi >> 8) & 0xFF), xv[4 + d].y, ph);
-            ph = __builtin_fmaf((float)((hi >> 16) & 0xFF), xv[4 + d].z, ph);
-            ph = __builtin_fmaf((float)(hi >> 24), xv[4 + d].w, ph);
-          }
-          const float part = __builtin_fmaf(-(float)g.zi[r][it], xsum, pl + ph);
+          const float part = w4a16_chunk(g.w[r][it], xv, g.zi[r][it], xsum);
           acc[m][r] = __builtin_fmaf(g.sc[r][it], part, acc[m][r]);
         }
       }
@@ -172,44 +230,21 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (r >= nr) break;
-        // E2M1 pairs (low nibble, high nibble) of each byte, exact in fp32
         float wl[16], wh[16];
-        const uint32_t wd[4] = {g.w[r][it].x, g.w[r][it].y, g.w[r][it].z, g.w[r][it].w};
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const v2f p0 = e2m1_pair<0>(wd[d], 1.0f), p1 = e2m1_pair<1>(wd[d], 1.0f);
-          const v2f p2 = e2m1_pair<2>(wd[d], 1.0f), p3 = e2m1_pair<3>(wd[d], 1.0f);
-          wl[4 * d + 0] = p0.x; wh[4 * d + 0] = p0.y;
-          wl[4 * d + 1] = p1.x; wh[4 * d + 1] = p1.y;
-          wl[4 * d + 2] = p2.x; wh[4 * d + 2] = p2.y;
-          wl[4 * d + 3] = p3.x; wh[4 * d + 3] = p3.y;
-        }
+        mxfp4_decode(g.w[r][it], wl, wh);
 #pragma unroll
         for (int m = 0; m < MB; m++) {
           float4 xv[8];
 #pragma unroll
           for (int p = 0; p < 8; p++)
             xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-          float pl = 0.0f, ph = 0.0f;
-#pragma unroll
-          for (int d = 0; d < 4; d++) {
-            pl = __builtin_fmaf(wl[4 * d + 0], xv[d].x, pl);
-            pl = __builtin_fmaf(wl[4 * d + 1], xv[d].y, pl);
-            pl = __builtin_fmaf(wl[4 * d + 2], xv[d].z, pl);
-            pl = __builtin_fmaf(wl[4 * d + 3], xv[d].w, pl);
-            ph = __builtin_fmaf(wh[4 * d + 0], xv[4 + d].x, ph);
-            ph = __builtin_fmaf(wh[4 * d + 1], xv[4 + d].y, ph);
-            ph = __builtin_fmaf(wh[4 * d + 2], xv[4 + d].z, ph);
-            ph = __builtin_fmaf(wh[4 * d + 3], xv[4 + d].w, ph);
-          }
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], pl + ph, acc[m][r]);
+          acc[m][r] = __builtin_fmaf(g.sc[r][it], mxfp4_dot(wl, wh, xv), acc[m][r]);
         }
       }
     } else {
-      // W4A8: int8 dot4 on unsigned codes (0..15 are non-negative int8) and the
-      // int8 activations; the group's zero-point term z * sum(a) is taken once,
-      // by the lane holding the group's first 16 bytes. Each lane's integer is
-      // exact and below 2^24, so its conversion to fp32 is exact.
+      // W4A8: the group's zero-point term z * sum(a) is taken once, by the lane
+      // holding the group's first 16 bytes. Each lane's integer is exact and below
+      // 2^24, so its conversion to fp32 is exact.
       const int gi = fmt_g32(F) ? ci : ci >> 2;
       const bool first = fmt_g32(F) || (ci & 3) == 0;
 #pragma unroll
@@ -220,16 +255,7 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
         for (int r = 0; r < R; r++) {
           if (r >= nr) break;
-          const uint4 w = g.w[r][it];
-          int d = 0;
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.x), (int)al.x, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.x), (int)ah.x, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.y), (int)al.y, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.y), (int)ah.y, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.z), (int)al.z, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.z), (int)ah.z, d, false);
-          d = __builtin_amdgcn_sdot4((int)lo_nibbles(w.w), (int)al.w, d, false);
-          d = __builtin_amdgcn_sdot4((int)hi_nibbles(w.w), (int)ah.w, d, false);
+          int d = w4a8_chunk(g.w[r][it], al, ah);
           d -= g.zi[r][it] * as;
           acc[m][r] = __builtin_fmaf(g.sc[r][it], (float)d, acc[m][r]);
         }
@@ -535,6 +561,259 @@ void gemv_kernel(GemmArgs a) {
 
 using GemvFn = void (*)(GemmArgs);
 
+// ============================================================ paced decode GEMV (M = 1)
+//
+// The plain decode GEMV (one activation row, no fused prologue or epilogue) on rows
+// of more than 1024 elements. A CU accepts only a limited number of outstanding
+// vector-memory instructions: a wave that issues all its weight loads up front stalls
+// at the issue of the later ones until the queue drains, and everything behind them
+// in program order (the activation prologue, then the compute) waits too, so compute
+// ran only after most of the stream had arrived. Here each wave issues the loads of
+// one row, runs the prologue (activations staged in LDS; for W4A8 the per-token
+// quantizer), then per row issues the next row's loads before it waits for and
+// computes the current one (two register stages, the next row always in flight).
+// Loads are unconditional (rows past the wave's share read zero-length ranges), so
+// every wait counts exactly the loads it needs. Weight, scale, zero-point and E8M0
+// loads are non-temporal: each byte is read once per call.
+//
+// The per-lane arithmetic and the wave reduction are those of gemv_kernel
+// (gemv_compute), so the outputs equal that kernel's bit for bit.
+
+constexpr int kPacedAux = 2;  // cache-policy bits of the weight loads: non-temporal
+
+// One weight row in flight: NIT 16-byte chunks per lane and, per chunk, the raw scale
+// bits (int4: fp32 of the chunk's group; MXFP4: the E8M0 byte of its block) and the
+// zero-point byte (int4); bytes are converted where they are used.
+template <int NIT>
+struct PacedStage {
+  uint4 w[NIT];
+  uint32_t s[NIT];
+  uint32_t z[NIT];
+};
+
+template <int F, int NIT>
+__device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &st, int row, int r1, int lane,
+                                           int nch, int G) {
+  const uint32_t rowbytes = (uint32_t)(a.Kp >> 1);
+  const bool in = row < r1;
+  const size_t rr = in ? (size_t)row : 0;
+  const Rsrc rw = make_rsrc(a.qw + rr * rowbytes, in ? rowbytes : 0u);
+  if constexpr (F == F_MXFP4) {
+    const Rsrc re = make_rsrc(a.e8m0 + rr * nch, in ? (uint32_t)nch : 0u);
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+      const uint32_t ci = (uint32_t)lane + kWave * it;
+      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
+      st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
+      st.s[it] = __builtin_amdgcn_raw_buffer_load_b8(re, (int)ci, 0, kPacedAux);
+      st.z[it] = 0;
+    }
+  } else {
+    const Rsrc rs = make_rsrc(a.scales + rr * G, in ? (uint32_t)G * 4 : 0u);
+    const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (in && a.zeros) ? (uint32_t)G : 0u);
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+      const uint32_t ci = (uint32_t)lane + kWave * it, gi = ci >> 2;
+      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
+      st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
+      st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gi * 4), 0, kPacedAux);
+      st.z[it] = __builtin_amdgcn_raw_buffer_load_b8(rz, (int)gi, 0, kPacedAux);
+    }
+  }
+}
+
+// fl(a / 127) for a >= 0: one multiply and two fused multiply-adds instead of the IEEE
+// division sequence. q0 = fl(a * fl(1/127)), r = a - 127 q0 (exact), q0 + r fl(1/127)
+// rounded once; equal to the IEEE quotient for every finite float32 a >= 0 (checked
+// exhaustively against a / 127.0f on the host). +inf takes the division.
+__device__ __forceinline__ float div127(float a) {
+  constexpr float kR = 1.0f / 127.0f;
+  const float q0 = a * kR;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kR, q0);
+  return a <= 3.4028234663852886e38f ? q1 : a / 127.0f;
+}
+
+// Rows up to 8192 elements fit in 128 VGPRs, so two workgroups share a CU; longer rows
+// hold more registers per stage and run one workgroup per CU.
+template <int NIT>
+struct PacedMinWaves {
+  static constexpr int value = NIT <= 4 ? 4 : 1;
+};
+
+template <int F, int NIT>
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(PacedMinWaves<NIT>::value)))
+void gemv_paced_kernel(GemmArgs a) {
+  constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
+  constexpr int T = kGemvThreads;
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ float red[kGemvWaves];
+  const int Kp = a.Kp, N = a.N;
+  const int nch = Kp >> 5;
+  const int nit = (nch + kWave - 1) / kWave;
+  const int nchp = nit * kWave;
+  const int G = Kp / fmt_group(F), Gp = nchp / 4;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  // rows of this workgroup (an even share, 32-bit arithmetic), then of this wave
+  const unsigned nwg = gridDim.x, bx = blockIdx.x;
+  const unsigned base = (unsigned)N / nwg, rem = (unsigned)N - base * nwg;
+  const int wr0 = (int)(bx * base + min(bx, rem)), wn = (int)(base + (bx < rem ? 1u : 0u));
+  const int r0 = wr0 + (wave * wn) / kGemvWaves, r1 = wr0 + ((wave + 1) * wn) / kGemvWaves;
+
+  float *xl = reinterpret_cast<float *>(lds);
+  uint8_t *ql = lds;
+  int32_t *asl = reinterpret_cast<int32_t *>(lds + (size_t)nchp * 32);
+  float *xsl = reinterpret_cast<float *>(asl + Gp);
+
+  // ---- 1. the activation row into registers (its loads first), the first row's weights
+  constexpr int S = NIT;
+  float4 xr[F == F_W4A8Q ? 1 : S];
+  if constexpr (F != F_W4A8Q) {
+    const Rsrc rx = make_rsrc(a.x, (uint32_t)Kp * 4);
+#pragma unroll
+    for (int i = 0; i < S; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  PacedStage<NIT> st0, st1;
+  paced_load<F, NIT>(a, st0, r0, r1, lane, nch, G);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. the prologue: stage (or quantize) the activations into the LDS planes
+  if constexpr (F == F_W4A16 || F == F_MXFP4) {
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      if (i >= nit) continue;
+      int ci, half, within;
+      chunk_pos(F, threadIdx.x * 4 + i * T * 4, ci, half, within);
+      *reinterpret_cast<float4 *>(xl + ((size_t)(half * 4 + (within >> 2)) * nchp + ci) * 4) = xr[i];
+    }
+  } else if constexpr (F == F_W4A8) {
+    float amax = 0.0f;  // padding reads +0 and cannot raise it
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      amax = fmaxf(fmaxf(amax, fabsf(xr[i].x)), fabsf(xr[i].y));
+      amax = fmaxf(fmaxf(amax, fabsf(xr[i].z)), fabsf(xr[i].w));
+    }
+    amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    float rmax = red[0];
+#pragma unroll
+    for (int w = 1; w < kGemvWaves; w++) rmax = fmaxf(rmax, red[w]);
+    const float sc = rmax > 0.0f ? div127(rmax) : 1.0f;  // row_scale, bit for bit
+    const float inv = 1.0f / sc;
+    if (threadIdx.x == 0) xsl[0] = sc;
+#pragma unroll
+    for (int i = 0; i < S; i++) {
+      if (i >= nit) continue;
+      const int e = threadIdx.x * 4 + i * T * 4;
+      int ci, half, within;
+      chunk_pos(F, e, ci, half, within);
+      const uint32_t qv = quant4_fast(xr[i], sc, inv);
+      *reinterpret_cast<uint32_t *>(ql + ((size_t)half * nchp + ci) * 16 + within) = qv;
+      const int gs = half_wave_sum(sum_i8x4(qv));
+      if ((threadIdx.x & 31) == 31) asl[e >> 7] = gs;
+    }
+  } else {  // F_W4A8Q: codes, group sums and the token scale as given
+    const Rsrc rq = make_rsrc(a.xq, (uint32_t)Kp);
+    for (int e = threadIdx.x * 4; e < nchp * 32; e += T * 4) {
+      int ci, half, within;
+      chunk_pos(F, e, ci, half, within);
+      *reinterpret_cast<uint32_t *>(ql + ((size_t)half * nchp + ci) * 16 + within) = ld_u32(rq, e);
+    }
+    for (int gg = threadIdx.x; gg < Gp; gg += T) asl[gg] = gg < G ? a.asum[gg] : 0;
+    if (threadIdx.x == 0) xsl[0] = a.xs[0];
+  }
+  __syncthreads();
+
+  // ---- 3. this lane's activation operands into registers (rows up to 4096 elements:
+  //         fp32, 64 VGPRs, or int8 codes, 16), read from the LDS planes once
+  constexpr bool kXReg = NIT <= 2;
+  constexpr bool kF32 = (F == F_W4A16 || F == F_MXFP4);
+  float4 xv[kXReg && kF32 ? NIT : 1][8];
+  float xsm[kXReg && F == F_W4A16 ? NIT : 1];
+  uint4 al[kXReg && kInt8 ? NIT : 1], ah[kXReg && kInt8 ? NIT : 1];
+  int as[kXReg && kInt8 ? NIT : 1];
+  if constexpr (kXReg) {
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+      const int ci = lane + kWave * it;  // NIT == nit: the planes hold every chunk
+      if constexpr (kF32) {
+#pragma unroll
+        for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
+        if constexpr (F == F_W4A16) xsm[it] = chunk_xsum(xv[it]);
+      } else {
+        al[it] = *reinterpret_cast<const uint4 *>(ql + (size_t)ci * 16);
+        ah[it] = *reinterpret_cast<const uint4 *>(ql + ((size_t)nchp + ci) * 16);
+        as[it] = (ci & 3) == 0 ? asl[ci >> 2] : 0;
+      }
+    }
+  }
+
+  // ---- 4. rows: the next one's loads out, then this one's compute, reduction and store
+  const int zadd = a.zeros ? 0 : 8;
+  auto row_out = [&](const PacedStage<NIT> &st, int row) {
+    float acc = 0.0f;
+    if constexpr (kXReg) {
+#pragma unroll
+      for (int it = 0; it < NIT; it++) {
+        if constexpr (F == F_W4A16) {
+          const float part = w4a16_chunk(st.w[it], xv[it], (int)(st.z[it] & 0xFFu) + zadd, xsm[it]);
+          acc = __builtin_fmaf(__uint_as_float(st.s[it]), part, acc);
+        } else if constexpr (F == F_MXFP4) {
+          float wl[16], wh[16];
+          mxfp4_decode(st.w[it], wl, wh);
+          acc = __builtin_fmaf(e8m0_to_f32(st.s[it] & 0xFFu), mxfp4_dot(wl, wh, xv[it]), acc);
+        } else {
+          int d = w4a8_chunk(st.w[it], al[it], ah[it]);
+          d -= ((int)(st.z[it] & 0xFFu) + zadd) * as[it];
+          acc = __builtin_fmaf(__uint_as_float(st.s[it]), (float)d, acc);
+        }
+      }
+    } else {
+      GemvRegs<F, 1, NIT> g;
+#pragma unroll
+      for (int it = 0; it < NIT; it++) {
+        g.w[0][it] = st.w[it];
+        if constexpr (F == F_MXFP4) {
+          g.sc[0][it] = e8m0_to_f32(st.s[it] & 0xFFu);
+          g.zi[0][it] = 0;
+        } else {
+          g.sc[0][it] = __uint_as_float(st.s[it]);
+          g.zi[0][it] = (int)(st.z[it] & 0xFFu) + zadd;
+        }
+      }
+      float ac[1][1] = {{0.0f}};
+      gemv_compute<F, 1, 1, NIT, false>(g, ac, 1, lane, nchp, Gp, xl, ql, asl);
+      acc = ac[0][0];
+    }
+    float t = wave_sum(acc);
+    if constexpr (kInt8) {
+#pragma clang fp contract(off)
+      t *= xsl[0];
+    }
+    if (lane == 0) a.y[row] = t;
+  };
+  for (int r = r0; r < r1; r += 2) {
+    paced_load<F, NIT>(a, st1, r + 1, r1, lane, nch, G);
+    __builtin_amdgcn_sched_barrier(0);
+    row_out(st0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    paced_load<F, NIT>(a, st0, r + 2, r1, lane, nch, G);
+    __builtin_amdgcn_sched_barrier(0);
+    if (r + 1 < r1) row_out(st1, r + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Whether the paced kernel runs this launch: one activation row, no fused prologue or
+// epilogue, rows longer than 1024 elements (shorter ones load two rows per wave load
+// in gemv_kernel), group-128 int4 or MXFP4.
+inline bool gemv_paced_eligible(int fmt, const GemmArgs &a) {
+  return a.M == 1 && !fmt_g32(fmt) && gemv_prologue(a) == 0 && !a.bias && !a.res && !a.amax_key && !a.glu &&
+         (a.Kp >> 5) > kWave / 2;
+}
+
 // Rows held at once (R) from the share of rows each wave gets under the
 // persistent grid, for NIT register-held chunks per lane.
 // A chosen instantiation: the kernel, its weight rows held per batch (R slots; two
@@ -601,6 +880,36 @@ static GemvPick pick_gemv(int nit, int nch, int rpw) {
   }
 }
 
+// The paced kernel: two workgroups per CU where two fit at once, otherwise one.
+template <int F>
+static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipStream_t s, GemvPlan *plan) {
+  const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
+  GemvFn k = nullptr;
+  int nk = 0;
+  if (nit <= 1) k = gemv_paced_kernel<F, 1>, nk = 1;
+  else if (nit <= 2) k = gemv_paced_kernel<F, 2>, nk = 2;
+  else if (nit <= 4) k = gemv_paced_kernel<F, 4>, nk = 4;
+  else k = gemv_paced_kernel<F, 8>, nk = 8;
+  int per_cu = 2;
+  if (gemv_wg_per_cu(reinterpret_cast<const void *>(k), lds) < 2) per_cu = 1;
+  int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
+  grid = grid < per_cu * cus ? grid : per_cu * cus;
+  if (plan) {
+    const int waves = grid * kGemvWaves;
+    plan->workgroups = grid;
+    plan->rows_per_wave = (a.N + waves - 1) / waves;
+    plan->rows_held = 2;  // the row being computed and the next one in flight
+    plan->chunks_per_lane = nk;
+    plan->two_rows_per_load = 0;
+    plan->act_rows = 1;
+    return hipSuccess;
+  }
+  GemmArgs arg = a;
+  void *args[] = {&arg};
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(kGemvThreads), args, lds, s);
+  return e != hipSuccess ? e : hipGetLastError();
+}
+
 // Persistent grid of at most two workgroups per CU, fewer when there are few rows.
 // Two only when two fit on a CU at once (at most 128 VGPRs per lane, and the LDS of
 // both): otherwise the second waits for the first to finish, and one workgroup per
@@ -618,6 +927,9 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
   // it runs faster with the CU to itself (gate/up 9728 x 896: 5.1 -> 4.5 us)
   const double wg_bytes = (double)a.N * (a.Kp / 2) / (2.0 * cus);
   int per_cu = (kQuant && (a.N < 2 * 2 * cus * kGemvWaves || (PRO != 0 && wg_bytes < 32768.0))) ? 1 : 2;
+  if constexpr (MB == 1 && PRO == 0 && !fmt_g32(F)) {
+    if (gemv_paced_eligible(F, a)) return launch_gemv_paced<F>(a, cus, lds, s, plan);
+  }
   for (;;) {
     int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
     grid = grid < per_cu * cus ? grid : per_cu * cus;
