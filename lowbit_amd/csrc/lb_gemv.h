@@ -591,7 +591,13 @@ struct PacedStage {
   uint32_t z[NIT];
 };
 
-template <int F, int NIT>
+// DW: the zero-point (int4) and E8M0 (MXFP4) bytes come as the aligned dword that
+// holds them, extracted where they are used. A byte load's value carried across the
+// row loop is masked at the loop edge, which waits for the whole stage and stalls the
+// next row's issue; dword values are carried as they are. Taken where every row's
+// bytes fill whole dwords (G or the block count a multiple of 4), so no dword reaches
+// past a row: every byte is in bounds.
+template <int F, int NIT, bool DW>
 __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &st, int row, int r1, int lane,
                                            int nch, int G) {
   const uint32_t rowbytes = (uint32_t)(a.Kp >> 1);
@@ -605,8 +611,10 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
       const uint32_t ci = (uint32_t)lane + kWave * it;
       const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
       st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
-      st.s[it] = __builtin_amdgcn_raw_buffer_load_b8(re, (int)ci, 0, kPacedAux);
+      if constexpr (DW) st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(re, (int)(ci & ~3u), 0, kPacedAux);
+      else st.s[it] = __builtin_amdgcn_raw_buffer_load_b8(re, (int)ci, 0, kPacedAux);
       st.z[it] = 0;
+      __builtin_amdgcn_sched_barrier(0);  // a chunk's loads together: its compute waits for them alone
     }
   } else {
     const Rsrc rs = make_rsrc(a.scales + rr * G, in ? (uint32_t)G * 4 : 0u);
@@ -617,9 +625,19 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
       const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
       st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
       st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gi * 4), 0, kPacedAux);
-      st.z[it] = __builtin_amdgcn_raw_buffer_load_b8(rz, (int)gi, 0, kPacedAux);
+      if constexpr (DW) st.z[it] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)(gi & ~3u), 0, kPacedAux);
+      else st.z[it] = __builtin_amdgcn_raw_buffer_load_b8(rz, (int)gi, 0, kPacedAux);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+}
+
+// The byte of chunk `ci` in a stage's metadata word (DW: the dword holding it).
+template <int F, bool DW>
+__device__ __forceinline__ uint32_t paced_byte(uint32_t word, uint32_t ci) {
+  if constexpr (!DW) return word & 0xFFu;
+  const uint32_t idx = F == F_MXFP4 ? ci : ci >> 2;  // block or group index
+  return (word >> (8 * (idx & 3u))) & 0xFFu;
 }
 
 // fl(a / 127) for a >= 0: one multiply and two fused multiply-adds instead of the IEEE
@@ -633,16 +651,8 @@ __device__ __forceinline__ float div127(float a) {
   return a <= 3.4028234663852886e38f ? q1 : a / 127.0f;
 }
 
-// Rows up to 8192 elements fit in 128 VGPRs, so two workgroups share a CU; longer rows
-// hold more registers per stage and run one workgroup per CU.
-template <int NIT>
-struct PacedMinWaves {
-  static constexpr int value = NIT <= 4 ? 4 : 1;
-};
-
-template <int F, int NIT>
-__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(PacedMinWaves<NIT>::value)))
-void gemv_paced_kernel(GemmArgs a) {
+template <int F, int NIT, bool DW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
   constexpr int T = kGemvThreads;
   extern __shared__ __align__(16) unsigned char lds[];
@@ -652,6 +662,16 @@ void gemv_paced_kernel(GemmArgs a) {
   const int nit = (nch + kWave - 1) / kWave;
   const int nchp = nit * kWave;
   const int G = Kp / fmt_group(F), Gp = nchp / 4;
+  // ---- 1. the activation row into registers (the kernel's first loads), then the
+  //         row shares and the first row's weights
+  constexpr int S = NIT;
+  float4 xr[F == F_W4A8Q ? 1 : S];
+  if constexpr (F != F_W4A8Q) {
+    const Rsrc rx = make_rsrc(a.x, (uint32_t)Kp * 4);
+#pragma unroll
+    for (int i = 0; i < S; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   // rows of this workgroup (an even share, 32-bit arithmetic), then of this wave
@@ -664,18 +684,8 @@ void gemv_paced_kernel(GemmArgs a) {
   uint8_t *ql = lds;
   int32_t *asl = reinterpret_cast<int32_t *>(lds + (size_t)nchp * 32);
   float *xsl = reinterpret_cast<float *>(asl + Gp);
-
-  // ---- 1. the activation row into registers (its loads first), the first row's weights
-  constexpr int S = NIT;
-  float4 xr[F == F_W4A8Q ? 1 : S];
-  if constexpr (F != F_W4A8Q) {
-    const Rsrc rx = make_rsrc(a.x, (uint32_t)Kp * 4);
-#pragma unroll
-    for (int i = 0; i < S; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
-  }
-  __builtin_amdgcn_sched_barrier(0);
   PacedStage<NIT> st0, st1;
-  paced_load<F, NIT>(a, st0, r0, r1, lane, nch, G);
+  paced_load<F, NIT, DW>(a, st0, r0, r1, lane, nch, G);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. the prologue: stage (or quantize) the activations into the LDS planes
@@ -752,21 +762,23 @@ void gemv_paced_kernel(GemmArgs a) {
 
   // ---- 4. rows: the next one's loads out, then this one's compute, reduction and store
   const int zadd = a.zeros ? 0 : 8;
+  const float xs = kInt8 ? xsl[0] : 1.0f;  // the token scale (W4A8)
   auto row_out = [&](const PacedStage<NIT> &st, int row) {
     float acc = 0.0f;
     if constexpr (kXReg) {
 #pragma unroll
       for (int it = 0; it < NIT; it++) {
+        const uint32_t ci = (uint32_t)lane + kWave * it;
         if constexpr (F == F_W4A16) {
-          const float part = w4a16_chunk(st.w[it], xv[it], (int)(st.z[it] & 0xFFu) + zadd, xsm[it]);
-          acc = __builtin_fmaf(__uint_as_float(st.s[it]), part, acc);
+          const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
+          acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
         } else if constexpr (F == F_MXFP4) {
           float wl[16], wh[16];
           mxfp4_decode(st.w[it], wl, wh);
-          acc = __builtin_fmaf(e8m0_to_f32(st.s[it] & 0xFFu), mxfp4_dot(wl, wh, xv[it]), acc);
+          acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), mxfp4_dot(wl, wh, xv[it]), acc);
         } else {
           int d = w4a8_chunk(st.w[it], al[it], ah[it]);
-          d -= ((int)(st.z[it] & 0xFFu) + zadd) * as[it];
+          d -= ((int)paced_byte<F, DW>(st.z[it], ci) + zadd) * as[it];
           acc = __builtin_fmaf(__uint_as_float(st.s[it]), (float)d, acc);
         }
       }
@@ -774,13 +786,14 @@ void gemv_paced_kernel(GemmArgs a) {
       GemvRegs<F, 1, NIT> g;
 #pragma unroll
       for (int it = 0; it < NIT; it++) {
+        const uint32_t ci = (uint32_t)lane + kWave * it;
         g.w[0][it] = st.w[it];
         if constexpr (F == F_MXFP4) {
-          g.sc[0][it] = e8m0_to_f32(st.s[it] & 0xFFu);
+          g.sc[0][it] = e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci));
           g.zi[0][it] = 0;
         } else {
           g.sc[0][it] = __uint_as_float(st.s[it]);
-          g.zi[0][it] = (int)(st.z[it] & 0xFFu) + zadd;
+          g.zi[0][it] = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
         }
       }
       float ac[1][1] = {{0.0f}};
@@ -790,19 +803,31 @@ void gemv_paced_kernel(GemmArgs a) {
     float t = wave_sum(acc);
     if constexpr (kInt8) {
 #pragma clang fp contract(off)
-      t *= xsl[0];
+      t *= xs;
     }
     if (lane == 0) a.y[row] = t;
   };
-  for (int r = r0; r < r1; r += 2) {
-    paced_load<F, NIT>(a, st1, r + 1, r1, lane, nch, G);
+  // steady state: two rows per iteration, the next row always in flight (stage 0 holds
+  // row r on entry); then the last one or two rows, whose loads are all out already
+  int r = r0;
+  for (; r + 2 < r1; r += 2) {
+    paced_load<F, NIT, DW>(a, st1, r + 1, r1, lane, nch, G);
     __builtin_amdgcn_sched_barrier(0);
     row_out(st0, r);
     __builtin_amdgcn_sched_barrier(0);
-    paced_load<F, NIT>(a, st0, r + 2, r1, lane, nch, G);
+    paced_load<F, NIT, DW>(a, st0, r + 2, r1, lane, nch, G);
     __builtin_amdgcn_sched_barrier(0);
-    if (r + 1 < r1) row_out(st1, r + 1);
+    row_out(st1, r + 1);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if (r + 1 < r1) {
+    paced_load<F, NIT, DW>(a, st1, r + 1, r1, lane, nch, G);
+    __builtin_amdgcn_sched_barrier(0);
+    row_out(st0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    row_out(st1, r + 1);
+  } else if (r < r1) {
+    row_out(st0, r);
   }
 }
 
@@ -884,12 +909,14 @@ static GemvPick pick_gemv(int nit, int nch, int rpw) {
 template <int F>
 static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipStream_t s, GemvPlan *plan) {
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
+  // metadata bytes per row: E8M0 one per 32 elements, zero-points one per 128
+  const bool dw = ((F == F_MXFP4 ? a.Kp / 32 : a.Kp / 128) % 4) == 0;
   GemvFn k = nullptr;
   int nk = 0;
-  if (nit <= 1) k = gemv_paced_kernel<F, 1>, nk = 1;
-  else if (nit <= 2) k = gemv_paced_kernel<F, 2>, nk = 2;
-  else if (nit <= 4) k = gemv_paced_kernel<F, 4>, nk = 4;
-  else k = gemv_paced_kernel<F, 8>, nk = 8;
+  if (nit <= 1) k = dw ? gemv_paced_kernel<F, 1, true> : gemv_paced_kernel<F, 1, false>, nk = 1;
+  else if (nit <= 2) k = dw ? gemv_paced_kernel<F, 2, true> : gemv_paced_kernel<F, 2, false>, nk = 2;
+  else if (nit <= 4) k = dw ? gemv_paced_kernel<F, 4, true> : gemv_paced_kernel<F, 4, false>, nk = 4;
+  else k = dw ? gemv_paced_kernel<F, 8, true> : gemv_paced_kernel<F, 8, false>, nk = 8;
   int per_cu = 2;
   if (gemv_wg_per_cu(reinterpret_cast<const void *>(k), lds) < 2) per_cu = 1;
   int grid = (a.N + kGemvWaves - 1) / kGemvWaves;
