@@ -657,7 +657,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   constexpr int T = kGemvThreads;
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[kGemvWaves];
-  const int Kp = a.Kp, N = a.N;
+  const int Kp = a.Kp;
   const int nch = Kp >> 5;
   const int nit = (nch + kWave - 1) / kWave;
   const int nchp = nit * kWave;
@@ -674,9 +674,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  // rows of this workgroup (an even share, 32-bit arithmetic), then of this wave
-  const unsigned nwg = gridDim.x, bx = blockIdx.x;
-  const unsigned base = (unsigned)N / nwg, rem = (unsigned)N - base * nwg;
+  // rows of this workgroup (an even share: N / grid and N % grid come from the host),
+  // then of this wave; the empty asm keeps the scalar work of the split behind the
+  // activation loads (the instruction selector would otherwise place it first)
+  unsigned bx = blockIdx.x;
+  asm volatile("" : "+s"(bx));
+  const unsigned base = (unsigned)a.split_base, rem = (unsigned)a.split_rem;
   const int wr0 = (int)(bx * base + min(bx, rem)), wn = (int)(base + (bx < rem ? 1u : 0u));
   const int r0 = wr0 + (wave * wn) / kGemvWaves, r1 = wr0 + ((wave + 1) * wn) / kGemvWaves;
 
@@ -932,6 +935,8 @@ static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipS
     return hipSuccess;
   }
   GemmArgs arg = a;
+  arg.split_base = a.N / grid;
+  arg.split_rem = a.N % grid;
   void *args[] = {&arg};
   const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(kGemvThreads), args, lds, s);
   return e != hipSuccess ? e : hipGetLastError();

@@ -28,6 +28,9 @@ struct GemmArgs {
   const uint8_t *e8m0 = nullptr;  // [N, Kp/32]
   float *y = nullptr;             // [M, N]
   int M = 0, Kp = 0, N = 0;
+  // one-row (paced) GEMV: rows per workgroup N / grid and N % grid, divided on the host so
+  // that no division runs ahead of the kernel's first loads
+  int split_base = 0, split_rem = 0;
   const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path)
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
   bool wt16 = false;              // qw / scales / zeros / e8m0 in the MFMA tile layout (t16)

@@ -110,6 +110,32 @@ def test_c2_decode_11008x4096(fmt, asym, resident):
         O.assert_fp_close(K.gemm_w4a8_q(a, W), ref, bound, RTOL)
 
 
+@pytest.mark.parametrize("case", ["subnormal", "huge", "max", "under"])
+@pytest.mark.parametrize("asym", [True, False])
+def test_c2_w4a16_activation_range(case, asym):
+    """The one-row W4A16 kernel multiplies codes by activations scaled by 2^24 unless some
+    |x| >= 2^96; both sides of that switch, and float32 subnormal activations, stay
+    within the bound at the headline shape."""
+    W = _packed("w4a16", 11008, 4096, 0, asym)
+    x = _x(1, 4096, 3)
+    if case == "subnormal":
+        x = (x * np.float32(1e-39)).astype(np.float32)  # every x a float32 subnormal
+        # scales times 2^100 (exact) keep the products and outputs normal, so that the
+        # relative bound applies
+        W = lb.Int4Weights(W.qw, (W.scales * np.float32(2.0 ** 100)).astype(np.float32), W.zeros, W.k)
+    elif case == "huge":
+        x = (x * np.float32(2.0 ** 97)).astype(np.float32)
+    elif case == "max":
+        x = (x / np.abs(x).max() * np.float32(2.0 ** 96)).astype(np.float32)
+        assert np.abs(x).max() == 2.0 ** 96  # exactly the switch point
+    else:
+        x = (x * np.float32(2.0 ** 93)).astype(np.float32)  # large, just under it
+    y = K.gemm_w4a16(x, lb.to_device(W))
+    assert K.last_path() == "gfx950"
+    assert np.isfinite(y).all()
+    _check("w4a16", x, W, y)
+
+
 # ------------------------------------------------------------------ C3 (W4A8 batches)
 
 C3 = [(m, n, asym) for m in (16, 64) for n in (11008, 4096) for asym in (True, False)]
