@@ -381,11 +381,13 @@ def cpu_threads(info: dict) -> int:
     return max(1, min(one_socket, info["affinity"], CPU_SHARE))
 
 
-def cpu_baseline_run(budget_s: float) -> dict | None:
+def cpu_baseline_run(budget_s: float, info: dict) -> dict | None:
     """Every decode format of the reference's own C library (oracle/_ref) at M=1
-    11008x4096, at 1 thread and at cpu_threads() threads, weights rotated past 2x the
-    host LLC, median of >= 3 calls after a warm-up (src/lowbit/bench.py:116-124).
-    Runs in a child process started with OMP_PROC_BIND=close, OMP_PLACES=cores."""
+    11008x4096, at 1 thread and at cpu_threads(info) threads, weights rotated past 2x
+    the host LLC, median of >= 3 calls after a warm-up (src/lowbit/bench.py:116-124).
+    Runs in a child process started with OMP_PROC_BIND=close, OMP_PLACES=cores;
+    `info` is the parent's host_cpu(): once the OpenMP runtime has bound the child's
+    first thread to one core, the child's own affinity mask holds that core alone."""
     from dataclasses import replace
 
     import lowbit_amd as lb
@@ -394,7 +396,6 @@ def cpu_baseline_run(budget_s: float) -> dict | None:
     L = cref.ref_lib()
     if L is None:
         return None
-    info = host_cpu()
     threads = cpu_threads(info)
     rng = np.random.default_rng(0)
     m, n, k = DECODE
@@ -450,8 +451,8 @@ def cpu_baseline(budget_s: float) -> dict | None:
     process (OpenMP reads its binding from the environment at start-up)."""
     env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
     r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-only",
-                        "--cpu-seconds", str(budget_s)], capture_output=True, text=True, env=env,
-                       timeout=600)
+                        "--cpu-seconds", str(budget_s), "--cpu-host", json.dumps(host_cpu())],
+                       capture_output=True, text=True, env=env, timeout=600)
     if r.returncode != 0:
         log(f"cpu baseline child failed (rc {r.returncode}): {r.stderr[-2000:]}")
         return None
@@ -558,9 +559,11 @@ def main() -> int:
                          "and print its JSON")
     ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor sweep")
     ap.add_argument("--cpu-baseline-only", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-host", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_baseline_only:
-        print(json.dumps(cpu_baseline_run(args.cpu_seconds)), flush=True)
+        print(json.dumps(cpu_baseline_run(args.cpu_seconds, json.loads(args.cpu_host) if args.cpu_host
+                                          else host_cpu())), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the hot path has no "
