@@ -672,6 +672,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
     for (int i = 0; i < S; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // W4A8 and W4A16: about 256 clocks between the activation loads and the first
+  // weight loads, so that the activations, whose prologue (the int8 quantizer, the
+  // W4A16 chunk sums) gates every row, queue ahead of the weight stream (1 x 11008 x
+  // 4096 cold: W4A8 6.23 -> 5.77 us, W4A16 6.49 -> 6.40; 64 and 128 clocks gain
+  // less, 320 and more lose again; MXFP4 gains nothing)
+  if constexpr (F == F_W4A8 || F == F_W4A16) __builtin_amdgcn_s_sleep(4);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   // rows of this workgroup (an even share: N / grid and N % grid come from the host),
