@@ -2,8 +2,9 @@
 host packers, byte for byte.
 
 The host packers restate the reference's quantize_int4 / quantize_mxfp4
-(src/lowbit/formats.py:90-142, 197-212) and are pinned to its golden vectors in
-tests/test_formats.py, so equality here carries that parity to the device. Inputs
+(src/lowbit/formats.py:90-142, 197-212) and are pinned by the known-answer and
+property tests of tests/test_formats.py, so equality here carries that parity to
+the device. Inputs
 cover what changes a byte: ragged K (padding), all three int4 scale rules, exact
 rounding ties, zero / subnormal / huge groups, repeated maxima of both signs
 (signed-max takes the first), E2M1 decision points, and MXFP4 block maxima just
