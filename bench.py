@@ -276,6 +276,38 @@ def read_floor(dev: Dev, nbytes: int, steps: int, warmup: int, graph: bool = Tru
     return out
 
 
+PROBE_FORMS = ["v_fmac_f32", "v_fma_f32", "v_add_f32", "v_mul_f32", "v_and_b32", "v_lshrrev_b32",
+               "v_cvt_f32_ubyte1", "v_cvt_f32_u32", "v_bfe_u32", "v_perm_b32", "v_and_or_b32", "v_fma_mix_f32",
+               "v_dot4_i32_i8", "v_pk_add_f16", "v_cvt_scalef32_pk_f32_fp4"]
+
+
+def machine_facts(dev: Dev, warmup: int) -> dict:
+    """The device facts the kernel designs rest on, measured by the library's probe
+    kernels (lb_probe.hip): the issue cost of single VALU instruction forms (16 waves
+    per CU, eight independent registers, 32 instructions per loop iteration) and the
+    fixed cost of a launch (an
+    empty kernel over the same grid, graph replay)."""
+    K, L = dev.K, dev.L
+    cus = K.device_info()["compute_units"]
+    wgs, iters, waves_per_cu = 2 * cus, 1024, 16  # 32 instructions per iteration
+    assert L.lbd_probe_forms() == len(PROBE_FORMS)
+    out = K.DeviceBuffer(wgs * 512 * 4)
+    rates = {}
+    for op, name in enumerate(PROBE_FORMS):
+        ms = dev.time_launches(lambda i, op=op: dev.check(L.lbd_probe_valu(op, iters, wgs, out.ptr, dev.stream),
+                                                          "probe"), 5, max(2, warmup // 10))
+        rates[name] = round(ms * 1e6 / (waves_per_cu * iters * 32), 4)
+        log(f"{name:28s} {rates[name]:.3f} ns per wave64 instruction per CU")
+    empty = {}
+    for g in (cus, 2 * cus):
+        ms = dev.time_launches(lambda i, g=g: dev.check(L.lbd_empty_kernel(g, dev.stream), "empty"), 200, warmup)
+        empty[f"{g}x512"] = round(ms * 1e3, 3)
+        log(f"empty kernel {g} x 512 threads: {empty[f'{g}x512']:.2f} us per graph-replayed launch")
+    return {"valu_ns_per_wave_instruction_per_cu": rates, "empty_launch_us": empty,
+            "probe": {"workgroups": wgs, "threads": 512, "iters": iters, "instructions_per_iter": 32,
+                      "independent_registers": 8}}
+
+
 def call_time(dev: Dev, fmt: str, W, x: np.ndarray, pool, layout: str, n_calls: int, warmup: int) -> float:
     """Median wall time (us) of one Python call lowbit_amd.gemm_<fmt>(x, handle) on
     resident weights, rotating over the same pool of copies as the kernel timing: the
@@ -562,6 +594,9 @@ def main() -> int:
                     help="only sweep the plain streaming read of the headline weight bytes (cold and hot) "
                          "and print its JSON")
     ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor sweep")
+    ap.add_argument("--machine-facts", action="store_true",
+                    help="only measure the device facts the kernels are designed around (VALU issue cost per "
+                         "instruction form, launch cost, the plain-read floor) and print their JSON")
     ap.add_argument("--cpu-baseline-only", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-host", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -595,6 +630,11 @@ def main() -> int:
     if args.read_floor:
         print(json.dumps({"read_floor": read_floor(dev, headline_bytes, args.steps, args.warmup, graph)}),
               flush=True)
+        return 0
+    if args.machine_facts:
+        facts = machine_facts(dev, args.warmup)
+        facts["read_floor"] = read_floor(dev, headline_bytes, args.steps, args.warmup, graph)
+        print(json.dumps({"machine_facts": facts}), flush=True)
         return 0
     if args.only_decoder:
         print(json.dumps({"decoder": measure_decoder(["w4a8", "mxfp4"], graph=graph)}), flush=True)

@@ -425,6 +425,18 @@ int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
  * value). The HBM read floor the decode GEMVs are measured against. */
 int lbd_read_kernel(const void *src, size_t bytes, int workgroups, int threads, int loads, uint32_t *sink,
                     void *stream);
+/* VALU issue-rate probe (no reference counterpart; the measurement behind the
+ * instruction costs a kernel design relies on): form `op` (0 .. lbd_probe_forms() - 1,
+ * in order v_fmac_f32, v_fma_f32, v_add_f32, v_mul_f32, v_and_b32, v_lshrrev_b32,
+ * v_cvt_f32_ubyte1, v_cvt_f32_u32, v_bfe_u32, v_perm_b32, v_and_or_b32, v_fma_mix_f32,
+ * v_dot4_i32_i8, v_pk_add_f16, v_cvt_scalef32_pk_f32_fp4), `iters` iterations of 32
+ * instructions per thread (eight independent registers, four steps), `workgroups`
+ * workgroups of 512 threads; `out`
+ * receives workgroups * 512 floats of no meaning (they keep the work alive). */
+int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream);
+int lbd_probe_forms(void);
+/* a kernel of `workgroups` x 512 threads that does nothing: the fixed cost of a launch */
+int lbd_empty_kernel(int workgroups, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1313,6 +1313,21 @@ int lbd_read_kernel(const void *src, size_t bytes, int workgroups, int threads, 
   if (e != hipSuccess) return fail_hip(e, "read kernel launch");
   return ok(0);
 }
+int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream) {
+  if (!out) return fail(LB_ERR_ARG, "probe needs an output buffer");
+  if (op < 0 || op >= lbk::valu_probe_forms() || iters <= 0 || workgroups <= 0 || workgroups > 65536)
+    return fail(LB_ERR_ARG, "probe: op 0 .. lbd_probe_forms() - 1, iters > 0, 1..65536 workgroups");
+  hipError_t e = lbk::launch_valu_probe(op, iters, workgroups, out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "probe launch");
+  return ok(0);
+}
+int lbd_probe_forms(void) { return lbk::valu_probe_forms(); }
+int lbd_empty_kernel(int workgroups, void *stream) {
+  if (workgroups <= 0 || workgroups > 65536) return fail(LB_ERR_ARG, "empty kernel: 1..65536 workgroups");
+  hipError_t e = lbk::launch_empty(workgroups, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "empty kernel launch");
+  return ok(0);
+}
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {
   if (!dst || !src || bytes % 16 || !aligned16(dst) || !aligned16(src))
     return fail(LB_ERR_ARG, "copy needs 16-byte aligned pointers and a multiple of 16 bytes");

@@ -126,6 +126,13 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 // per thread (lb_probe.hip); `sink` is one device dword it almost never writes.
 hipError_t launch_stream_read(const void *src, size_t bytes, int workgroups, int threads, int loads, uint32_t *sink,
                               hipStream_t s);
+// VALU issue-rate probe `op` (0 .. valu_probe_forms() - 1), `iters` iterations of 32
+// instructions per thread (eight independent registers, four steps), workgroups of 512
+// threads; out[workgroups * 512].
+hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipStream_t s);
+int valu_probe_forms();
+// a kernel that does nothing, workgroups of 512 threads
+hipError_t launch_empty(int workgroups, hipStream_t s);
 
 // Decoder-layer kernels (lb_model.hip).
 hipError_t launch_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, hipStream_t s);

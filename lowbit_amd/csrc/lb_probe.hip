@@ -1,7 +1,10 @@
 // Measurement kernels: a plain streaming read of a buffer, the reference point the
 // decode GEMVs are measured against (the fastest a launch of that many bytes can
-// read them), in the configurations the sweep in bench.py tries.
+// read them), in the configurations the sweep in bench.py tries; VALU issue-rate
+// probes of single instruction forms; an empty kernel (the fixed cost of a launch).
 #include <hip/hip_runtime.h>
+
+#include <utility>
 
 #include "lb_device.h"
 #include "lb_internal.h"
@@ -49,6 +52,99 @@ static hipError_t launch_read_t(const void *src, uint32_t bytes, int wgs, int lo
     case 8: hipLaunchKernelGGL((stream_read_kernel<T, 8>), dim3(wgs), dim3(T), 0, s, p, bytes, per_wg, sink); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+// ---- issue-rate probes: one VALU instruction form, eight independent registers per
+//      step, four steps per loop iteration (so the loop's own scalar instructions are
+//      a small share), `iters` iterations; the host times the launch over a grid of 16
+//      waves per CU and reports time per wave instruction per CU
+
+// Instruction forms, in probe order (operands: r the register stepped, a and b two
+// lane values; outputs of the pair-producing forms land in a 64-bit register pair).
+#define LB_PROBE_FORMS(X)                                                   \
+  X(0, "v_fmac_f32_e32 %0, %1, %2")                                         \
+  X(1, "v_fma_f32 %0, %1, %2, %0")                                          \
+  X(2, "v_add_f32_e32 %0, %1, %0")                                          \
+  X(3, "v_mul_f32_e32 %0, %1, %0")                                          \
+  X(4, "v_and_b32_e32 %0, %1, %0")                                          \
+  X(5, "v_lshrrev_b32_e32 %0, 4, %0")                                       \
+  X(6, "v_cvt_f32_ubyte1_e32 %0, %0")                                       \
+  X(7, "v_cvt_f32_u32_e32 %0, %0")                                          \
+  X(8, "v_bfe_u32 %0, %0, 4, 4")                                            \
+  X(9, "v_perm_b32 %0, %1, %2, %0")                                         \
+  X(10, "v_and_or_b32 %0, %1, %2, %0")                                      \
+  X(11, "v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]")                   \
+  X(12, "v_dot4_i32_i8 %0, %1, %2, %0")                                     \
+  X(13, "v_pk_add_f16 %0, %1, %0")
+
+constexpr int kProbeForms = 15;  // the 14 forms above and v_cvt_scalef32_pk_f32_fp4
+
+template <int OP>
+__global__ __launch_bounds__(512) void valu_probe_kernel(int iters, float *out) {
+  // finite, normal float operands (1 + t/1024 and 0.5): the float forms never meet a
+  // NaN, infinity or subnormal; the integer forms take the same bits
+  uint32_t a = __float_as_uint(1.0f + (float)threadIdx.x * 0.0009765625f), b = 0x3F000000u;
+  uint32_t r0 = a, r1 = a + 1, r2 = a + 2, r3 = a + 3, r4 = a + 4, r5 = a + 5, r6 = a + 6, r7 = a + 7;
+  v2f p[8] = {};
+  for (int i = 0; i < iters; i++) {
+    if constexpr (OP == 14) {
+      // the pair conversion: eight independent sources and destination pairs
+#define LB_PK(J, R) asm volatile("v_cvt_scalef32_pk_f32_fp4 %0, %1, %2" : "=v"(p[J]) : "v"(R), "v"(b));
+#define LB_PK8 LB_PK(0, r0) LB_PK(1, r1) LB_PK(2, r2) LB_PK(3, r3) LB_PK(4, r4) LB_PK(5, r5) LB_PK(6, r6) LB_PK(7, r7)
+      LB_PK8 LB_PK8 LB_PK8 LB_PK8
+#undef LB_PK8
+#undef LB_PK
+    } else {
+#define LB_STEP(ID, INS)                                                    \
+  if constexpr (OP == ID) {                                                 \
+    asm volatile(INS : "+v"(r0) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r1) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r2) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r3) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r4) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r5) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r6) : "v"(a), "v"(b));                          \
+    asm volatile(INS : "+v"(r7) : "v"(a), "v"(b));                          \
+  }
+      LB_PROBE_FORMS(LB_STEP)
+      LB_PROBE_FORMS(LB_STEP)
+      LB_PROBE_FORMS(LB_STEP)
+      LB_PROBE_FORMS(LB_STEP)
+#undef LB_STEP
+    }
+  }
+  float f = __uint_as_float(r0 ^ r1 ^ r2 ^ r3 ^ r4 ^ r5 ^ r6 ^ r7);
+#pragma unroll
+  for (int j = 0; j < 8; j++) f += p[j].x + p[j].y;
+  out[(size_t)blockIdx.x * 512 + threadIdx.x] = f;
+}
+
+template <int OP>
+static void launch_probe_op(int iters, int workgroups, float *out, hipStream_t s) {
+  hipLaunchKernelGGL((valu_probe_kernel<OP>), dim3(workgroups), dim3(512), 0, s, iters, out);
+}
+
+template <int... OPS>
+static hipError_t launch_probe_sel(int op, int iters, int workgroups, float *out, hipStream_t s,
+                                   std::integer_sequence<int, OPS...>) {
+  bool found = false;
+  ((op == OPS ? (launch_probe_op<OPS>(iters, workgroups, out, s), found = true) : false), ...);
+  return found ? hipGetLastError() : hipErrorInvalidValue;
+}
+
+hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipStream_t s) {
+  if (iters <= 0 || workgroups <= 0 || workgroups > 65536) return hipErrorInvalidValue;
+  return launch_probe_sel(op, iters, workgroups, out, s, std::make_integer_sequence<int, kProbeForms>{});
+}
+
+int valu_probe_forms() { return kProbeForms; }
+
+__global__ __launch_bounds__(512) void empty_kernel() {}
+
+hipError_t launch_empty(int workgroups, hipStream_t s) {
+  if (workgroups <= 0 || workgroups > 65536) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(empty_kernel, dim3(workgroups), dim3(512), 0, s);
   return hipGetLastError();
 }
 

@@ -138,6 +138,27 @@ def test_t16_sizes_and_argument_checks():
     assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6
 
 
+def test_probe_argument_checks():
+    """The measurement probes (lbd_probe_valu, lbd_empty_kernel, lbd_read_kernel) reject
+    bad arguments before any device work, and the probe count matches the instruction
+    forms bench.py names."""
+    import bench
+    L = K.lib()
+    assert L.lbd_probe_forms() == len(bench.PROBE_FORMS) == 15
+    assert L.lbd_probe_valu(0, 16, 1, None, None) == -6            # no output buffer
+    out = C.c_void_p(16)                                            # never dereferenced
+    assert L.lbd_probe_valu(15, 16, 1, out, None) == -6             # past the last form
+    assert L.lbd_probe_valu(-1, 16, 1, out, None) == -6
+    assert L.lbd_probe_valu(0, 0, 1, out, None) == -6               # no iterations
+    assert L.lbd_probe_valu(0, 16, 0, out, None) == -6              # no workgroups
+    assert L.lbd_empty_kernel(0, None) == -6
+    assert L.lbd_empty_kernel(70000, None) == -6
+    assert L.lbd_read_kernel(None, 1024, 1, 256, 1, None, None) == -6
+    assert L.lbd_read_kernel(out, 1000, 1, 256, 1, out, None) == -6   # not a multiple of 16
+    assert L.lbd_read_kernel(out, 1024, 1, 128, 1, out, None) == -6   # 128 threads
+    assert L.lbd_read_kernel(out, 1024, 1, 256, 3, out, None) == -6   # 3 loads
+
+
 def test_argmax_slot_count_matches_header():
     import re
 
