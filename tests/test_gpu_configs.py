@@ -113,9 +113,9 @@ def test_c2_decode_11008x4096(fmt, asym, resident):
 @pytest.mark.parametrize("case", ["subnormal", "huge", "max", "under"])
 @pytest.mark.parametrize("asym", [True, False])
 def test_c2_w4a16_activation_range(case, asym):
-    """The one-row W4A16 kernel multiplies codes by activations scaled by 2^24 unless some
-    |x| >= 2^96; both sides of that switch, and float32 subnormal activations, stay
-    within the bound at the headline shape."""
+    """Activations across the float32 range at the headline shape: all subnormal (scales
+    raised so that the products and outputs stay normal), and rows scaled to 2^93..2^97
+    times N(0, 1). The one-row kernel's sum q x - z sum x stays within the bound."""
     W = _packed("w4a16", 11008, 4096, 0, asym)
     x = _x(1, 4096, 3)
     if case == "subnormal":
@@ -127,9 +127,9 @@ def test_c2_w4a16_activation_range(case, asym):
         x = (x * np.float32(2.0 ** 97)).astype(np.float32)
     elif case == "max":
         x = (x / np.abs(x).max() * np.float32(2.0 ** 96)).astype(np.float32)
-        assert np.abs(x).max() == 2.0 ** 96  # exactly the switch point
+        assert np.abs(x).max() == 2.0 ** 96
     else:
-        x = (x * np.float32(2.0 ** 93)).astype(np.float32)  # large, just under it
+        x = (x * np.float32(2.0 ** 93)).astype(np.float32)
     y = K.gemm_w4a16(x, lb.to_device(W))
     assert K.last_path() == "gfx950"
     assert np.isfinite(y).all()
