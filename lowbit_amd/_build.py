@@ -28,9 +28,14 @@ SOURCES = ["lb_api.hip", "lb_kernels.hip", "lb_gemv_g32.hip", "lb_model.hip", "l
 # -packed-fp32-ops off: the compiler must not emit packed fp32 VALU ops.
 # Denormals are kept (the E8M0 scale 2^-127 is a float32 subnormal) and no
 # fast-math: the int8 quantizer relies on IEEE float32 division and rounding.
+# Device functions start on 4 KiB boundaries, so a kernel's first page holds its
+# first 4 KiB of code: the same W4A16 decode kernel took 6.56-7.05 us per launch at
+# 1 x 11008 x 4096 cold when the linker placed it 3.5 KiB into a page (its first
+# page boundary 512 bytes in, inside the prologue), 6.30-6.40 us page-aligned.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "-fno-gpu-flush-denormals-to-zero", "-fno-fast-math"]
+         "-fno-gpu-flush-denormals-to-zero", "-fno-fast-math",
+         "-Xarch_device", "-falign-functions=4096"]
 
 
 def _hipcc() -> str:
