@@ -172,6 +172,7 @@ typedef struct {
   int chunks_per_lane;   /* 16-byte chunks per lane per weight row */
   int two_rows_per_load; /* 1 where each wave load covers two short rows */
   int act_rows;          /* activation rows per launch */
+  int k_slices;          /* slices of 4096 elements each row is cut into, one wave each */
 } lbd_plan;
 int lbd_gemm_plan(int kind, int M, int N, int Kp, const lb_params *p, lbd_plan *out);
 

@@ -463,6 +463,7 @@ int lbd_gemm_plan(int kind, int M, int N, int Kp, const lb_params *p, lbd_plan *
   out->chunks_per_lane = g.chunks_per_lane;
   out->two_rows_per_load = g.two_rows_per_load;
   out->act_rows = g.act_rows;
+  out->k_slices = g.k_slices;
   return ok(out->path);
 }
 

@@ -420,7 +420,9 @@ void gemv_kernel(GemmArgs a) {
       }
     }
   } else if constexpr (F == F_W4A8 || F == F_W4A8G32) {
-    // fused per-token quantizer: bit-identical to quant_rows_kernel
+    // fused per-token quantizer: bit-identical to quant_rows_kernel (unrolled over
+    // the rows, so that xr is indexed by constants and stays in registers)
+#pragma unroll
     for (int m = 0; m < MB; m++) {
       const Rsrc rx = make_rsrc(a.x + (size_t)m * Kp, (uint32_t)Kp * 4);
       float amax = 0.0f;  // padding reads +0 and cannot raise it
@@ -599,7 +601,7 @@ struct PacedStage {
 // past a row: every byte is in bounds.
 template <int F, int NIT, bool DW>
 __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &st, int row, int r1, int lane,
-                                           int nch, int G) {
+                                           int nch, int G, uint32_t cbase = 0) {
   const uint32_t rowbytes = (uint32_t)(a.Kp >> 1);
   const bool in = row < r1;
   const size_t rr = in ? (size_t)row : 0;
@@ -608,7 +610,7 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
     const Rsrc re = make_rsrc(a.e8m0 + rr * nch, in ? (uint32_t)nch : 0u);
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-      const uint32_t ci = (uint32_t)lane + kWave * it;
+      const uint32_t ci = cbase + (uint32_t)lane + kWave * it;
       const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
       st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
       if constexpr (DW) st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(re, (int)(ci & ~3u), 0, kPacedAux);
@@ -621,7 +623,7 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
     const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (in && a.zeros) ? (uint32_t)G : 0u);
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-      const uint32_t ci = (uint32_t)lane + kWave * it, gi = ci >> 2;
+      const uint32_t ci = cbase + (uint32_t)lane + kWave * it, gi = ci >> 2;
       const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
       st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
       st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gi * 4), 0, kPacedAux);
@@ -840,6 +842,136 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   }
 }
 
+// ============================================================ paced decode GEMV, rows split (M = 1, K > 4096)
+//
+// W4A16 and MXFP4 rows of more than 128 chunks (4096 elements): their fp32
+// activations no longer fit a wave's registers (64 VGPRs hold two chunks per lane),
+// and reading them from LDS for every row costs more LDS bandwidth than the row's
+// weights (4096 x 11008: 44 KB per row, 16 waves per CU). Here a row's chunks are cut
+// into S slices of 128 chunks (two per lane). Wave w of a workgroup takes slice w % S,
+// the waves of one slice split the workgroup's rows evenly, and each wave holds its
+// slice's activations in registers for all its rows: LDS serves 16 KB per wave once.
+// Per row a wave sums its slice as the one-row kernel sums a row (same per-chunk
+// helpers, same two stages in flight); the slices' sums meet in LDS, and after one
+// barrier the workgroup adds them in slice order and stores the row. The activation
+// planes are padded to S * 128 chunks (zeros), so a slice past the row's end adds
+// exactly 0. (W4A8, whose int8 codes cost a quarter of the LDS bytes, measured no
+// faster this way: 8.48 -> 8.42 us cold, 7.51 -> 7.80 us hot at 1 x 4096 x 11008.)
+constexpr int kSplitChunks = 2 * kWave;  // chunks per slice
+
+template <int F, bool DW>
+__global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs a) {
+  static_assert(F == F_W4A16 || F == F_MXFP4, "fp32 activations");
+  constexpr int T = kGemvThreads, NIT = 2, SX = kGemvMaxNit;  // X staging: up to 8 float4 per thread
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int Kp = a.Kp;
+  const int nch = Kp >> 5;
+  const int S = (nch + kSplitChunks - 1) / kSplitChunks;  // 2..4 (the host checks)
+  const int nchp = S * kSplitChunks;                      // plane entries, whole slices
+  const int G = Kp / fmt_group(F);
+  // ---- 1. the activation row (whole slices; slots past Kp read 0), the kernel's
+  //         first loads
+  float4 xr[SX];
+  {
+    const Rsrc rx = make_rsrc(a.x, (uint32_t)Kp * 4);
+#pragma unroll
+    for (int i = 0; i < SX; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (F == F_W4A16) __builtin_amdgcn_s_sleep(4);  // as in the one-row kernel
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  unsigned bx = blockIdx.x;
+  asm volatile("" : "+s"(bx));
+  const unsigned base = (unsigned)a.split_base, rem = (unsigned)a.split_rem;
+  const int wr0 = (int)(bx * base + min(bx, rem)), wn = (int)(base + (bx < rem ? 1u : 0u));
+  // slice sl of this wave, its index j among the P waves of that slice, its rows
+  const int sl = wave % S, j = wave / S, P = (kGemvWaves - 1 - sl) / S + 1;
+  const int r0 = wr0 + (j * wn) / P, r1 = wr0 + ((j + 1) * wn) / P;
+  const uint32_t cb = (uint32_t)sl * kSplitChunks;
+
+  float *xl = reinterpret_cast<float *>(lds);
+  float *part = xl + (size_t)nchp * 32;  // the slices' row sums, [row of the workgroup][slice]
+  PacedStage<NIT> st0, st1;
+  paced_load<F, NIT, DW>(a, st0, r0, r1, lane, nch, G, cb);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. stage the activations of all S slices into the LDS planes
+#pragma unroll
+  for (int i = 0; i < SX; i++) {
+    if (i >= 2 * S) continue;  // block-uniform
+    int ci, half, within;
+    chunk_pos(F, threadIdx.x * 4 + i * T * 4, ci, half, within);
+    *reinterpret_cast<float4 *>(xl + ((size_t)(half * 4 + (within >> 2)) * nchp + ci) * 4) = xr[i];
+  }
+  __syncthreads();
+
+  // ---- 3. this wave's slice of the activations into registers
+  float4 xv[NIT][8];
+  float xsm[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; it++) {
+    const int ci = (int)cb + lane + kWave * it;
+#pragma unroll
+    for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
+    xsm[it] = F == F_W4A16 ? chunk_xsum(xv[it]) : 0.0f;
+  }
+
+  // ---- 4. rows: the next one's loads out, then this one's slice sum into `part`
+  const int zadd = a.zeros ? 0 : 8;
+  auto row_part = [&](const PacedStage<NIT> &st, int row) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+      const uint32_t ci = cb + (uint32_t)lane + kWave * it;
+      if constexpr (F == F_W4A16) {
+        const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
+        acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
+      } else {
+        float wl[16], wh[16];
+        mxfp4_decode(st.w[it], wl, wh);
+        acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), mxfp4_dot(wl, wh, xv[it]), acc);
+      }
+    }
+    const float t = wave_sum(acc);
+    if (lane == 0) part[(row - wr0) * S + sl] = t;
+  };
+  int r = r0;
+  for (; r + 2 < r1; r += 2) {
+    paced_load<F, NIT, DW>(a, st1, r + 1, r1, lane, nch, G, cb);
+    __builtin_amdgcn_sched_barrier(0);
+    row_part(st0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    paced_load<F, NIT, DW>(a, st0, r + 2, r1, lane, nch, G, cb);
+    __builtin_amdgcn_sched_barrier(0);
+    row_part(st1, r + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (r + 1 < r1) {
+    paced_load<F, NIT, DW>(a, st1, r + 1, r1, lane, nch, G, cb);
+    __builtin_amdgcn_sched_barrier(0);
+    row_part(st0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    row_part(st1, r + 1);
+  } else if (r < r1) {
+    row_part(st0, r);
+  }
+  // ---- 5. the workgroup's rows: slice sums added in slice order
+  __syncthreads();
+  for (int i = threadIdx.x; i < wn; i += T) {
+    float t = part[i * S];
+    for (int s2 = 1; s2 < S; s2++) t += part[i * S + s2];
+    a.y[wr0 + i] = t;
+  }
+}
+
+// LDS of the split kernel: the fp32 activation planes of S whole slices, then the
+// workgroup's row sums (rows_max rows x S slices).
+inline size_t gemv_split_lds_bytes(int Kp, int rows_max) {
+  const int S = ((Kp >> 5) + kSplitChunks - 1) / kSplitChunks;
+  return (size_t)S * kSplitChunks * 128 + (size_t)rows_max * S * sizeof(float);
+}
+
 // Whether the paced kernel runs this launch: one activation row, no fused prologue or
 // epilogue, rows longer than 1024 elements (shorter ones load two rows per wave load
 // in gemv_kernel), group-128 int4 or MXFP4.
@@ -920,6 +1052,41 @@ static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipS
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
   // metadata bytes per row: E8M0 one per 32 elements, zero-points one per 128
   const bool dw = ((F == F_MXFP4 ? a.Kp / 32 : a.Kp / 128) % 4) == 0;
+  if constexpr (F == F_W4A16 || F == F_MXFP4) {
+    // rows of more than 4096 elements: split over the waves, where the planes of
+    // whole slices stay within the GEMV's LDS budget (rows up to 12288 elements)
+    if (nit > 2 && gemv_split_lds_bytes(a.Kp, 0) <= kGemvLdsLimit) {
+      const GemvFn k = dw ? gemv_paced_split_kernel<F, true> : gemv_paced_split_kernel<F, false>;
+      const int S = ((a.Kp >> 5) + kSplitChunks - 1) / kSplitChunks;
+      int per_cu = 2, grid = 0;
+      size_t slds = 0;
+      for (;;) {
+        grid = (a.N + kGemvWaves - 1) / kGemvWaves;
+        grid = grid < per_cu * cus ? grid : per_cu * cus;
+        slds = gemv_split_lds_bytes(a.Kp, (a.N + grid - 1) / grid);
+        if (per_cu == 1 || gemv_wg_per_cu(reinterpret_cast<const void *>(k), slds) >= 2) break;
+        per_cu = 1;
+      }
+      if (plan) {
+        const int pmin = kGemvWaves / S;  // waves of the slice with the fewest
+        plan->workgroups = grid;
+        plan->rows_per_wave = ((a.N + grid - 1) / grid + pmin - 1) / pmin;
+        plan->rows_held = 2;
+        plan->chunks_per_lane = 2;
+        plan->two_rows_per_load = 0;
+        plan->act_rows = 1;
+        plan->k_slices = S;
+        return hipSuccess;
+      }
+      GemmArgs arg = a;
+      arg.split_base = a.N / grid;
+      arg.split_rem = a.N % grid;
+      void *args[] = {&arg};
+      const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(kGemvThreads), args,
+                                           slds, s);
+      return e != hipSuccess ? e : hipGetLastError();
+    }
+  }
   GemvFn k = nullptr;
   int nk = 0;
   if (nit <= 1) k = dw ? gemv_paced_kernel<F, 1, true> : gemv_paced_kernel<F, 1, false>, nk = 1;

@@ -97,6 +97,7 @@ bool gemv_eligible(int fmt, int M, int Kp);
 // lbd_gemm_plan); with a non-null plan, launch_gemv fills it and launches nothing.
 struct GemvPlan {
   int workgroups = 0, rows_per_wave = 0, rows_held = 0, chunks_per_lane = 0, two_rows_per_load = 0, act_rows = 0;
+  int k_slices = 1;  // slices each weight row is cut into across waves (rows past 4096 elements)
 };
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, GemvPlan *plan = nullptr);
 // Workgroups of a small-M kernel (512 threads, `lds` bytes of dynamic LDS) that fit

@@ -160,7 +160,7 @@ class LbdPlan(C.Structure):
     """lbd_plan of include/lowbit_hip.h: the regime and small-M kernel configuration a
     GEMM shape takes."""
     _fields_ = [(f, C.c_int) for f in ("path", "workgroups", "rows_per_wave", "rows_held", "chunks_per_lane",
-                                       "two_rows_per_load", "act_rows")]
+                                       "two_rows_per_load", "act_rows", "k_slices")]
 
 
 def gemm_plan(kind: str, m: int, n: int, kp: int, isa=None) -> dict:

@@ -195,3 +195,54 @@ def test_c4_down_projection_lognormal_rows(fmt, asym, m, resident):
     y = K.GEMMS[fmt](x, lb.to_device(W) if resident else W)
     assert K.last_path() == ("gfx950" if m == 1 else "gfx950-mfma")
     _check(fmt, x, W, y)
+
+
+# ------------------------------------------------------------------ rows past 4096 elements
+
+def test_c4_plan_splits_rows_over_waves():
+    """At M=1 the down-projection's W4A16 and MXFP4 rows (11008 elements, 344 chunks)
+    are cut into three slices of at most 128 chunks, one wave each, two chunks per
+    lane; W4A8 rows and the headline shape's rows are not split."""
+    for fmt in ("w4a16", "mxfp4"):
+        plan = K.gemm_plan(fmt, 1, 4096, 11008)
+        assert plan["path"] == "gfx950" and plan["k_slices"] == 3 and plan["chunks_per_lane"] == 2
+        assert plan["rows_held"] == 2 and plan["act_rows"] == 1
+    assert K.gemm_plan("w4a8", 1, 4096, 11008)["k_slices"] == 1
+    for fmt in ("w4a16", "mxfp4", "w4a8"):
+        assert K.gemm_plan(fmt, 1, 11008, 4096)["k_slices"] == 1
+
+
+# (format, asym, rows, row length, slices): fp32 rows split up to 12288 elements (the
+# planes of whole slices within the 60 KB LDS budget); a 13312-element row (416
+# chunks: four slices would need 64 KB) and every W4A8 row keep the unsplit kernel
+SPLIT = [("w4a16", True, 4097, 4224, 2), ("w4a16", False, 1000, 12288, 3), ("mxfp4", False, 4097, 8224, 3),
+         ("mxfp4", False, 3000, 12288, 3), ("w4a16", True, 1500, 13312, 1), ("w4a8", True, 4096, 11008, 1),
+         ("w4a8", False, 1000, 16384, 1)]
+
+
+@pytest.mark.parametrize("fmt,asym,n,k,slices", SPLIT)
+def test_split_rows_against_oracle(fmt, asym, n, k, slices):
+    """One activation row against rows of 4224..16384 elements: two or three slices,
+    the last one mostly past the row's end (4224: 4 of 128 chunks) or partial (8224:
+    257 chunks), odd row counts; the rows that stay unsplit checked alongside."""
+    W = _packed(fmt, n, k, 5, asym)
+    x = _x(1, k, 5)
+    plan = K.gemm_plan(fmt, 1, n, W.kp)
+    assert plan["path"] == "gfx950" and plan["k_slices"] == slices
+    y = K.GEMMS[fmt](x, lb.to_device(W))
+    assert K.last_path() == "gfx950"
+    _check(fmt, x, W, y)
+
+
+def test_split_rows_zero_rows_exact():
+    """Rows whose codes all equal the zero-point give exactly 0 in every slice, so
+    exactly 0 after the slices are added (symmetric int4 of zero rows: q = z = 8)."""
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((512, 12288)).astype(np.float32)
+    w[::7] = 0.0
+    W = lb.quantize_int4(w)
+    x = rng.standard_normal((1, 12288)).astype(np.float32)
+    for fn in (K.gemm_w4a16, K.gemm_w4a8):
+        y = fn(x, lb.to_device(W))
+        assert np.all(y[:, ::7] == 0)
+        _check("w4a16" if fn is K.gemm_w4a16 else "w4a8", x, W, y)

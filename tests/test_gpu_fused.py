@@ -88,9 +88,18 @@ def dense(hw):
 
 
 def run_plain(fmt, dw, act, n):
+    """The unfused GEMV of `act`. W4A16 / MXFP4 rows past 4096 elements take the
+    split one-row kernel there, which adds its slices' sums in another order than
+    the fused kernels sum a row, so for them the same small-M kernel runs without
+    the prologue (a zero bias keeps the launch off the one-row kernels; adding +0
+    changes no value)."""
     y = K.DeviceBuffer(4 * n)
     _LIVE.append(y)
-    plain(fmt, dw, up(act.astype(np.float32)).ptr, y.ptr)
+    x_dev = up(act.astype(np.float32)).ptr
+    if fmt != "w4a8" and dw.kp > 4096:
+        ok(fused(fmt, dw, x_dev, y.ptr, bias=up(np.zeros(n, np.float32)).ptr))
+    else:
+        plain(fmt, dw, x_dev, y.ptr)
     return y.to_array((n,), np.float32)
 
 
@@ -177,7 +186,11 @@ def test_glu_epilogue(rng, fmt, m, n, k):
     L = K.lib()
     yp, ref, yg = K.DeviceBuffer(4 * m * n), K.DeviceBuffer(4 * m * n // 2), K.DeviceBuffer(4 * m * n // 2)
     _LIVE.extend([yp, ref, yg])
-    cases = [dict(), dict(bias=db.ptr)]
+    # a plain one-row launch of W4A16 / MXFP4 rows past 4096 elements takes the split
+    # kernel (its slices' sums added in another order), so a zero bias stands in for
+    # "no fusion" there (see run_plain)
+    split = m == 1 and fmt != "w4a8" and dw.kp > 4096
+    cases = [dict(bias=up(np.zeros(n, np.float32)).ptr) if split else dict(), dict(bias=db.ptr)]
     if m == 1:
         nw = up((1 + 0.05 * rng.standard_normal(k)).astype(np.float32))
         cases.append(dict(norm=nw.ptr, eps=1e-6, bias=db.ptr))
