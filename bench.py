@@ -181,6 +181,17 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
                 qwt, et = K.DeviceBuffer(bq.value), K.DeviceBuffer(be.value)
                 dev.check(L.lbd_repack_mxfp4_t16(b[0].ptr, b[1].ptr, n, W.kp, qwt.ptr, et.ptr, s), "t16 repack")
                 tiled.append((qwt, et))
+        elif fmt == "w4a16" and L.lbd_w4a16_prefers_t16f8(m, n, W.kp) == 1 and \
+                (W.zeros is None or int(W.zeros.max(initial=0)) <= 15):
+            # the t16f8 copy (zero-points folded in), where lowbit_amd handles read it
+            layout = "t16f8"
+            bq, bs = C.c_size_t(0), C.c_size_t(0)
+            dev.check(L.lbd_int4_t16f8_bytes(n, W.kp, C.byref(bq), C.byref(bs)), "t16f8 sizes")
+            for b in pool:
+                qwt8, st = K.DeviceBuffer(bq.value), K.DeviceBuffer(bs.value)
+                dev.check(L.lbd_repack_int4_t16f8(b[0].ptr, b[1].ptr, b[2].ptr if len(b) > 2 else None, n, W.kp,
+                                                  qwt8.ptr, st.ptr, s), "t16f8 repack")
+                tiled.append((qwt8, st))
         else:
             bq, bs, bz = C.c_size_t(0), C.c_size_t(0), C.c_size_t(0)
             dev.check(L.lbd_int4_t16_bytes(n, W.kp, C.byref(bq), C.byref(bs), C.byref(bz)), "t16 sizes")
@@ -198,13 +209,13 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
 
     def launch(i):
         b = pool[i % len(pool)]
-        if layout == "t16":
+        if layout == "t16f8":
+            rc = L.lbd_gemm_w4a16_t16f8(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, n, dy.ptr, C.byref(prm), ws.ptr,
+                                        ws_bytes, s)
+        elif layout == "t16":
             if fmt == "w4a8":
                 rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
                                          dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
-            elif fmt == "w4a16":
-                rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
-                                          dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
             else:
                 rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, n, dy.ptr, C.byref(prm), ws.ptr,
                                           ws_bytes, s)
@@ -324,7 +335,9 @@ def call_time(dev: Dev, fmt: str, W, x: np.ndarray, pool, layout: str, n_calls: 
                 h.qw, h.e8m0 = b[0], b[1]
         else:
             h = K.DeviceInt4Weights(None, None, None, W.n, W.kp, W.k, W.nbytes)
-            if layout == "t16":
+            if layout == "t16f8":
+                h.t16f8, h.zmax = (b[0], b[1]), 8 if W.zeros is None else int(W.zeros.max(initial=0))
+            elif layout == "t16":
                 h.t16 = (b[0], b[1], b[2])
             else:
                 h.qw, h.scales, h.zeros = b[0], b[1], (b[2] if len(b) > 2 else None)
@@ -672,7 +685,7 @@ def main() -> int:
             if fmt == "w4a8":
                 r["mfma"] = "int8"
                 r["mfma_frac"] = round(r["gflops"] / 1e3 / INT8_PEAK_TOPS, 4)
-            elif r["weight_layout"] == "t16":
+            elif r["weight_layout"] in ("t16", "t16f8"):
                 # fp32 semantics on bf16 matrix cores: three bf16 products per fp32 product
                 r["mfma"] = "bf16x3"
                 r["mfma_frac"] = round(BF16X3_TERMS * r["gflops"] / 1e3 / BF16_PEAK_TFLOPS, 4)

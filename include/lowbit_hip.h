@@ -222,6 +222,32 @@ int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                        const lb_params *p, void *workspace,
                        size_t workspace_bytes, void *stream);
 size_t lbd_bf16x3_workspace_bytes(int M, int Kp);
+/* ---- "t16f8": int4 g128 weights for lbd_gemm_w4a16 on bf16 matrix cores with the
+ *      zero-point folded in (no reference counterpart: a device-private copy of an
+ *      Int4Weights matrix, src/lowbit/formats.py:56-87, that the bf16 matrix cores
+ *      convert two operands per instruction). Each code less its group's zero-point
+ *      (z = 8 when zeros is NULL) is one E4M3 byte of value (code - z) 2^-9: sign
+ *      and magnitude, exact for |code - z| <= 15, which holds for every zero-point
+ *      the reference's packer writes (0-15, src/lowbit/formats.py:122); a larger
+ *      difference is stored as NaN, so results are NaN rather than wrong.
+ *        qwt8 [S][G4][2][64][16 B]  half h, lane 16q + c of tile (s, g): byte b is
+ *                                   nibble h (0 low, 1 high) of byte 64g + 16q + b
+ *                                   of row 16s + c, less z
+ *        st   as for t16
+ *      Rows past N and groups past Kp/128 are zero bytes. ---- */
+int lbd_int4_t16f8_bytes(int N, int Kp, size_t *qwt8_bytes, size_t *st_bytes);
+int lbd_repack_int4_t16f8(const uint8_t *qw, const float *scales,
+                          const uint8_t *zeros, int N, int Kp, uint8_t *qwt8,
+                          float *st, void *stream);
+/* 1 when lbd_gemm_w4a16_t16f8 is expected to be faster than lbd_gemm_w4a16_t16 at
+ * this shape on the current device (enough weight subtiles per workgroup to hide
+ * the t16f8 layout's doubled weight bytes), else 0; or LB_ERR_SHAPE */
+int lbd_w4a16_prefers_t16f8(int M, int N, int Kp);
+/* y = x . w^T as lbd_gemm_w4a16_t16 (same workspace contract, same results bit for
+ * bit) on t16f8 weights; always the matrix-core path */
+int lbd_gemm_w4a16_t16f8(const float *x, int M, int Kp, const uint8_t *qwt8,
+                         const float *st, int N, float *y, const lb_params *p,
+                         void *workspace, size_t workspace_bytes, void *stream);
 /* MXFP4 in the t16 order: qwt as above (lane 16q + c of tile (s, g) holds block
  * 4g + q of row 16s + c), et [S][G4][64] the E8M0 byte of that block (G = ceil(Kp/128)) */
 int lbd_mxfp4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *et_bytes);

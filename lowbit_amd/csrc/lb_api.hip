@@ -248,8 +248,9 @@ int w4a8_workspace(int M, int Kp, size_t given_bytes, hipStream_t s, char **ws) 
   return take_workspace(w4a8_ws_bytes(M, Kp), given_bytes, s, ws);
 }
 
-// bf16x3 GEMM on t16 weights: split the activations into `ws`, then the GEMM.
-int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s) {
+// bf16x3 GEMM on t16 (or, f8, t16f8) weights: split the activations into `ws`,
+// then the GEMM.
+int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s, bool f8 = false) {
   int cus = 0;
   DevInfo di;
   if (device_info(&di) == 0) cus = di.cus;
@@ -257,16 +258,17 @@ int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s) {
   a.x3 = reinterpret_cast<const uint4 *>(ws);
   hipError_t e = lbk::launch_split3(fmt, a.x, a.M, a.Kp, reinterpret_cast<uint4 *>(ws), s);
   if (e != hipSuccess) return fail_hip(e, "activation split launch");
-  e = lbk::launch_bf3_gemm(fmt, a, cus, s);
+  e = lbk::launch_bf3_gemm(fmt, a, cus, s, f8);
   if (e != hipSuccess) return fail_hip(e, "bf16x3 GEMM launch");
   return ok(LB_ISA_GFX950_MFMA);
 }
 
 // Shared checks of the t16 GEMM entry points (32-bit offsets inside the kernels).
-int check_t16(int M, int Kp, int N) {
+int check_t16(int M, int Kp, int N, bool f8 = false) {
   if ((size_t)M * Kp * 4 > 0xFFFFFFF0u || lbk::x3_bytes(M, Kp) > 0xFFFFFFF0u)
     return fail(LB_ERR_SHAPE, "activations above 4 GiB");
-  if (lbk::t16_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
+  if ((f8 ? lbk::t16f8_qw_bytes(N, Kp) : lbk::t16_qw_bytes(N, Kp)) > 0xFFFFFFF0u)
+    return fail(LB_ERR_SHAPE, "t16 weights above 4 GiB");
   return 0;
 }
 
@@ -543,6 +545,53 @@ int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt, const 
   char *ws = static_cast<char *>(workspace);
   if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
   return run_bf3(lbk::F_W4A16, a, ws, s);
+}
+
+int lbd_int4_t16f8_bytes(int N, int Kp, size_t *qwt8_bytes, size_t *st_bytes) {
+  int rc = check_shape(1, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (qwt8_bytes) *qwt8_bytes = lbk::t16f8_qw_bytes(N, Kp);
+  if (st_bytes) *st_bytes = lbk::t16_group_entries(N, Kp) * 4;
+  return ok(0);
+}
+
+int lbd_repack_int4_t16f8(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                          uint8_t *qwt8, float *st, void *stream) {
+  int rc = check_shape(1, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if (!qw || !scales || !qwt8 || !st) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(qw) || !aligned16(qwt8)) return fail(LB_ERR_ARG, "qw and qwt8 must be 16-byte aligned");
+  if (lbk::t16f8_qw_bytes(N, Kp) > 0xFFFFFFF0u) return fail(LB_ERR_SHAPE, "t16f8 weights above 4 GiB");
+  hipError_t e = lbk::launch_repack_int4_t16f8(qw, scales, zeros, N, Kp, qwt8, st, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "t16f8 repack launch");
+  return ok(0);
+}
+
+int lbd_w4a16_prefers_t16f8(int M, int N, int Kp) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  int cus = 0;
+  DevInfo di;
+  if (device_info(&di) == 0) cus = di.cus;
+  return lbk::w4a16_prefers_t16f8(M, N, cus) ? 1 : 0;
+}
+
+int lbd_gemm_w4a16_t16f8(const float *x, int M, int Kp, const uint8_t *qwt8, const float *st, int N, float *y,
+                         const lb_params *p, void *workspace, size_t workspace_bytes, void *stream) {
+  int rc = check_shape(M, Kp, N, LB_GROUP);
+  if (rc < 0) return rc;
+  if ((rc = check_params(p, M)) < 0) return rc;
+  if (!x || !qwt8 || !st || !y) return fail(LB_ERR_ARG, "null pointer");
+  if (!aligned16(x) || !aligned16(qwt8)) return fail(LB_ERR_ARG, "x and qwt8 must be 16-byte aligned");
+  if ((rc = check_t16(M, Kp, N, true)) < 0) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  lbk::GemmArgs a;
+  a.x = x; a.qw = qwt8; a.scales = st; a.y = y;
+  a.M = M; a.Kp = Kp; a.N = N;
+  a.wt16 = true;
+  char *ws = static_cast<char *>(workspace);
+  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
+  return run_bf3(lbk::F_W4A16, a, ws, s, true);
 }
 
 int lbd_mxfp4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *et_bytes) {

@@ -71,6 +71,14 @@ __host__ __device__ inline int t16_groups(int Kp) { return (((Kp + 127) / 128) +
 __host__ __device__ inline size_t t16_qw_bytes(int N, int Kp) { return (size_t)((N + 15) / 16) * t16_groups(Kp) * 1024; }
 __host__ __device__ inline size_t t16_group_entries(int N, int Kp) { return (size_t)((N + 15) / 16) * 16 * t16_groups(Kp); }
 __host__ __device__ inline size_t t16_e8m0_bytes(int N, int Kp) { return (size_t)((N + 15) / 16) * t16_groups(Kp) * 64; }
+// t16f8: the int4 tiles of the bf16 matrix-core path with each code less its
+// zero-point stored as one E4M3 byte of value (code - z) 2^-9 (sign and magnitude,
+// exact for |code - z| <= 15; larger differences, from zero-points above 15, are
+// stored as NaN). Tile (s, g) is 2 KiB:
+//   qwt8 [S][G4][2][64][16 B]  half h, lane l = 16q + c: byte b is nibble h (0 low,
+//                              1 high) of byte 64g + 16q + b of row 16s + c, less z
+// with st as for t16 (there is no zero-point array). Padding bytes are 0.
+__host__ __device__ inline size_t t16f8_qw_bytes(int N, int Kp) { return 2 * t16_qw_bytes(N, Kp); }
 hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N, int Kp, uint8_t *qwt, uint8_t *et,
                                    hipStream_t s);
 // bf16x3 path (W4A16 / MXFP4 on bf16 matrix cores, fp32-exact products): the
@@ -78,7 +86,9 @@ hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N
 // weights. Bytes of the split activations for M rows:
 __host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
 hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
-hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s);
+hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, bool f8 = false);
+// Whether W4A16 at this shape is faster on t16f8 weights than on t16 weights.
+bool w4a16_prefers_t16f8(int M, int N, int num_cus);
 // weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 with groups of `group`
 // (128 or 32; mode 0 absmax, 1 signed-max, 2 asym) or MXFP4
 hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, int group, uint8_t *qw, float *scales,
@@ -86,6 +96,8 @@ hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, int grou
 hipError_t launch_quantize_mxfp4(const float *w, int N, int K, uint8_t *qw, uint8_t *e8m0, hipStream_t s);
 hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
                                   uint8_t *qwt, float *st, uint8_t *zt, hipStream_t s);
+hipError_t launch_repack_int4_t16f8(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                                    uint8_t *qwt8, float *st, hipStream_t s);
 
 // Small-M VALU kernels: largest M they take and the LDS they need.
 constexpr int kGemvMaxM = 4;

@@ -937,11 +937,12 @@ hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipS
 
 // Weight stage of one subtile: the lane's 16 bytes of the group's tile and, for
 // W4A16, its row's scale and the dword of zero-points holding its group's; for
-// MXFP4, the dword of E8M0 bytes holding its block's. Bytes are extracted where
-// they are used (a byte load's zero extension next to the load would make each
-// stage wait for its own load).
+// MXFP4, the dword of E8M0 bytes holding its block's; for the t16f8 layout, the
+// lane's 32 bytes (w, w2) and its row's scale. Bytes are extracted where they are
+// used (a byte load's zero extension next to the load would make each stage wait
+// for its own load).
 struct B3Stage {
-  uint4 w;
+  uint4 w, w2;
   float s;
   uint32_t z;
 };
@@ -965,8 +966,13 @@ __device__ __forceinline__ void w4_bf16x4(uint32_t nib, float zf, uint32_t &d0, 
 // phases accumulate onto them), which leaves the registers for PF weight
 // subtiles in flight. Partial tiles are reduced across waves in LDS once per
 // chunk, in a fixed order.
-template <int F, int TM, int NS, int PF>
+// F8 (W4A16 only): the weights are in the t16f8 layout, each lane's 32 codes
+// already less their zero-point as E4M3 bytes n 2^-9 (sign and magnitude n <= 15),
+// so that one conversion with scale 2^9 makes two bf16 operands, the same values
+// as the nibble path's (float)code - z, with no zero-point load.
+template <int F, int TM, int NS, int PF, bool F8>
 __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
+  static_assert(!F8 || F == F_W4A16, "the t16f8 layout holds int4 weights");
   __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -980,11 +986,12 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   const int nph = (G + kW8Waves - 1) / kW8Waves;
 
   const Rsrc rx = make_rsrc(a.x3, (uint32_t)min(x3_bytes(M, Kp), (size_t)0xFFFFFFF0u));
-  const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(t16_qw_bytes(N, Kp), (size_t)0xFFFFFFF0u));
+  const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(F8 ? t16f8_qw_bytes(N, Kp) : t16_qw_bytes(N, Kp),
+                                                (size_t)0xFFFFFFF0u));
   const size_t gents = t16_group_entries(N, Kp);
   const Rsrc rs = make_rsrc(F == F_W4A16 ? (const void *)a.scales : (const void *)a.e8m0,
                             F == F_W4A16 ? (uint32_t)(gents * 4) : (uint32_t)t16_e8m0_bytes(N, Kp));
-  const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, (F == F_W4A16 && a.zeros) ? (uint32_t)gents : 0u);
+  const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, (F == F_W4A16 && !F8 && a.zeros) ? (uint32_t)gents : 0u);
   const int zadd = (F == F_W4A16 && !a.zeros) ? 8 : 0;
 
   v4u xa[4][3][TM];
@@ -1008,12 +1015,19 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
       // last subtile (in bounds; they fill LDS slots the reduction never reads).
       auto load = [&](B3Stage &st, int j) {
         const uint32_t sj = (uint32_t)min(cb + j, ce - 1);
-        st.w = ld_b128(rw, (uint32_t)lane * 16u, (sj * G4 + g) * (kWave * 16u));
+        if constexpr (F8) {
+          // the tile's two 1 KiB halves: lane bytes 0-15, then 16-31
+          const uint32_t tb = (sj * G4 + g) * (2 * kWave * 16u);
+          st.w = ld_b128(rw, (uint32_t)lane * 16u, tb);
+          st.w2 = ld_b128(rw, (uint32_t)lane * 16u, tb + kWave * 16u);
+        } else {
+          st.w = ld_b128(rw, (uint32_t)lane * 16u, (sj * G4 + g) * (kWave * 16u));
+        }
         if constexpr (F == F_W4A16) {
           // entry ((sj G4/4 + g/4) 16 + c) 4 + g % 4 of the group data
           const uint32_t gu = (sj * (G4 / 4) + g / 4) * 64u;
           st.s = ld_f32(rs, (uint32_t)c * 16u, (gu + (g & 3)) * 4u);
-          st.z = ld_u32(rz, (uint32_t)c * 4u, gu);  // symmetric: a zero-length range reads 0
+          if constexpr (!F8) st.z = ld_u32(rz, (uint32_t)c * 4u, gu);  // symmetric: a zero-length range reads 0
         } else {
           st.s = 0.0f;
           st.z = ld_u32(rs, (uint32_t)(lane & ~3), (sj * G4 + g) * kWave);
@@ -1064,7 +1078,20 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
         }
         v4u b[4];
         float fs;
-        if constexpr (F == F_W4A16) {
+        if constexpr (F8) {
+          // operand u, element e = lane byte 8u + e
+          const uint32_t wd[8] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w, cur.w2.x, cur.w2.y, cur.w2.z, cur.w2.w};
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            b[u][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, false));
+            b[u][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, true));
+            b[u][2] =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, false));
+            b[u][3] =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, true));
+          }
+          fs = cur.s;
+        } else if constexpr (F == F_W4A16) {
           const float zf = (float)(int)(((cur.z >> (8 * (g & 3))) & 0xFFu) + (uint32_t)zadd);
           const uint32_t wd[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
 #pragma unroll
@@ -1144,18 +1171,26 @@ template <int TM> struct B3Cfg {
   static constexpr int PF = NS - 1;
 };
 
-template <int F, int TM>
+// Grid of the bf16x3 GEMM: gy row blocks of 16 TM rows, gx workgroups over the
+// S = ceil(N/16) subtiles, spw subtiles for the busiest workgroup.
+static void bf3_grid(int M, int N, int TM, int cus, int &gx, int &gy, int &spw) {
+  const int S = (N + 15) / 16;
+  gy = (M + 16 * TM - 1) / (16 * TM);
+  gx = std::max(1, std::min(S, cus / gy));
+  spw = (S + gx - 1) / gx;
+}
+
+template <int F, int TM, bool F8>
 static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
   constexpr int NS = B3Cfg<TM>::NS, PF = B3Cfg<TM>::PF;
-  const int gy = (a.M + 16 * TM - 1) / (16 * TM), S = (a.N + 15) / 16;
-  const int gx = std::max(1, std::min(S, cus / gy));
   // every subtile slot of a chunk but the last is computed, so the chunk length
   // is the workgroup's share (up to NS; its loads all in flight)
-  const int spw = (S + gx - 1) / gx;
+  int gx, gy, spw;
+  bf3_grid(a.M, a.N, TM, cus, gx, gy, spw);
   auto go = [&](auto ns) {
     constexpr int C = decltype(ns)::value < NS ? decltype(ns)::value : NS;
-    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF)>), dim3(gx, gy), dim3(kW8Threads), 0, s,
-                       a);
+    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF), F8>), dim3(gx, gy), dim3(kW8Threads),
+                       0, s, a);
   };
   switch (spw) {
     case 1: go(std::integral_constant<int, 1>{}); break;
@@ -1170,9 +1205,20 @@ static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
   }
 }
 
-hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s) {
+bool w4a16_prefers_t16f8(int M, int N, int num_cus) {
+  // Measured at 64 x 11008 x 4096 (6 subtiles per workgroup), 128 x 11008 x 4096 (11),
+  // 256 x 4096 x 4096 (8) and 512 x 4096 x 4096 (16), t16f8 took 3-11 % less time
+  // with the weights cold and 5-15 % less hot; with 2 or 3 subtiles per workgroup
+  // (16 and 32 x 11008 x 4096, 64 x 4096 x 11008) its twice as many weight bytes per
+  // stage cost more than the conversions it saves when cold (5-13 % more time).
+  int gx, gy, spw;
+  bf3_grid(M, N, M > 16 ? 2 : 1, num_cus > 0 ? num_cus : 256, gx, gy, spw);
+  return spw >= 4;
+}
+
+hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, bool f8) {
   const int cus = num_cus > 0 ? num_cus : 256;
-  if (!a.x3 || !a.wt16) return hipErrorInvalidValue;
+  if (!a.x3 || !a.wt16 || (f8 && fmt != F_W4A16)) return hipErrorInvalidValue;
   // W4A16: 32-row blocks halve the weight decode per output once there are two
   // row blocks (its decode VALU, not bytes, bounds it). MXFP4 decodes with a few
   // conversion instructions, and each CU's bytes matter more: the activation terms
@@ -1190,12 +1236,15 @@ hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t 
     };
     tall = cu_bytes(1) > 0.75 * cu_bytes(2);
   }
-  if (fmt == F_W4A16) {
-    if (tall) launch_bf3_t<F_W4A16, 2>(a, cus, s);
-    else launch_bf3_t<F_W4A16, 1>(a, cus, s);
+  if (fmt == F_W4A16 && f8) {
+    if (tall) launch_bf3_t<F_W4A16, 2, true>(a, cus, s);
+    else launch_bf3_t<F_W4A16, 1, true>(a, cus, s);
+  } else if (fmt == F_W4A16) {
+    if (tall) launch_bf3_t<F_W4A16, 2, false>(a, cus, s);
+    else launch_bf3_t<F_W4A16, 1, false>(a, cus, s);
   } else if (fmt == F_MXFP4) {
-    if (tall) launch_bf3_t<F_MXFP4, 2>(a, cus, s);
-    else launch_bf3_t<F_MXFP4, 1>(a, cus, s);
+    if (tall) launch_bf3_t<F_MXFP4, 2, false>(a, cus, s);
+    else launch_bf3_t<F_MXFP4, 1, false>(a, cus, s);
   } else {
     return hipErrorInvalidValue;
   }
@@ -1449,6 +1498,52 @@ __global__ __launch_bounds__(kThreads) void repack_int4_t16_kernel(const uint8_t
   }
 }
 
+// t16f8: one thread per 16-byte chunk of qwt8 (half h of lane l of tile (s, g)):
+// nibble h of the 16 source bytes the t16 lane holds, less the group's zero-point,
+// as E4M3 sign-magnitude bytes; then the scales as for t16.
+__device__ __forceinline__ uint32_t e4m3_small_int(int d) {
+  const int n = d < 0 ? -d : d;
+  if (n > 15) return 0x7Fu;  // not exact in this encoding: NaN
+  return (d < 0 ? 0x80u : 0u) | (uint32_t)n;  // n 2^-9: subnormal below 8, exponent field 1 from 8
+}
+
+__global__ __launch_bounds__(kThreads) void repack_int4_t16f8_kernel(const uint8_t *__restrict__ qw,
+                                                                      const float *__restrict__ scales,
+                                                                      const uint8_t *__restrict__ zeros, int N,
+                                                                      int Kp, uint8_t *__restrict__ qwt8,
+                                                                      float *__restrict__ st) {
+  const int G = Kp / kGroup, G4 = t16_groups(Kp);
+  const size_t rowbytes = (size_t)(Kp >> 1);
+  const size_t nchunk = t16f8_qw_bytes(N, Kp) / 16, nent = t16_group_entries(N, Kp);
+  const size_t stride = (size_t)gridDim.x * kThreads;
+  for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < nchunk; t += stride) {
+    const int l = (int)(t % 64), h = (int)((t / 64) % 2), g = (int)((t / 128) % G4);
+    const size_t sub = t / (128 * (size_t)G4);
+    const size_t row = sub * 16 + (l & 15);
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+    if (row < (size_t)N && g < G) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(qw + row * rowbytes + (size_t)g * 64 + (size_t)(l >> 4) * 16);
+      const int z = zeros ? (int)zeros[row * G + g] : 8;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int d = 0; d < 4; d++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int code = (int)((w[d] >> (8 * k + 4 * h)) & 0xFu);
+          o[d] |= e4m3_small_int(code - z) << (8 * k);
+        }
+    }
+    reinterpret_cast<uint4 *>(qwt8)[t] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  for (size_t e = (size_t)blockIdx.x * kThreads + threadIdx.x; e < nent; e += stride) {
+    const int j = (int)(e % 4), c = (int)((e / 4) % 16);
+    const size_t gq = (e / 64) % (size_t)(G4 / 4), sub = e / (64 * (size_t)(G4 / 4));
+    const size_t row = sub * 16 + c;
+    const int g = (int)(gq * 4) + j;
+    st[e] = (row < (size_t)N && g < G) ? scales[row * G + g] : 0.0f;
+  }
+}
+
 // MXFP4: the same qwt order over rows of Kp/2 bytes (a multiple of 16; chunks past
 // the row are zero), then the E8M0 byte of each lane's block in lane order.
 __global__ __launch_bounds__(kThreads) void repack_mxfp4_t16_kernel(const uint8_t *__restrict__ qw,
@@ -1490,6 +1585,17 @@ hipError_t launch_repack_int4_t16(const uint8_t *qw, const float *scales, const 
   if (blocks == 0) blocks = 1;
   hipLaunchKernelGGL(repack_int4_t16_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, qw, scales, zeros, N, Kp,
                      qwt, st, zt);
+  return hipGetLastError();
+}
+
+hipError_t launch_repack_int4_t16f8(const uint8_t *qw, const float *scales, const uint8_t *zeros, int N, int Kp,
+                                    uint8_t *qwt8, float *st, hipStream_t s) {
+  const size_t work = t16f8_qw_bytes(N, Kp) / 16;
+  size_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 16384) blocks = 16384;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(repack_int4_t16f8_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, qw, scales, zeros, N,
+                     Kp, qwt8, st);
   return hipGetLastError();
 }
 

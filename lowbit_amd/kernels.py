@@ -124,6 +124,10 @@ SIGNATURES = {
     "lbd_repack_int4_t16": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _vp], _int),
     "lbd_gemm_w4a8_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
     "lbd_gemm_w4a16_t16": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
+    "lbd_int4_t16f8_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
+    "lbd_w4a16_prefers_t16f8": ([_int, _int, _int], _int),
+    "lbd_repack_int4_t16f8": ([_vp, _vp, _vp, _int, _int, _vp, _vp, _vp], _int),
+    "lbd_gemm_w4a16_t16f8": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
     "lbd_noalloc_scratch_bytes": ([], _sz),
     "lbd_gemm_w4a8_t16_noalloc": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp], _int),
     "lbd_bf16x3_workspace_bytes": ([_int, _int], _sz),
@@ -341,7 +345,11 @@ class DeviceInt4Weights:
     `t16` is the matrix-core tile layout of the same matrix (include/lowbit_hip.h,
     lbd_repack_int4_t16), built on the device the first time a GEMM takes the
     matrix-core path and kept beside the row-major copy, which the decode kernels
-    read.
+    read. `t16f8` is the layout W4A16 reads on the bf16 matrix cores
+    (lbd_repack_int4_t16f8: each code less its zero-point as one E4M3 byte, twice the
+    bytes of t16), built the same way; it holds the zero-points exactly only up to 15,
+    so `zmax`, the largest zero-point (8 when symmetric, None when not known), chooses
+    between the two for W4A16.
     """
     qw: DeviceBuffer
     scales: DeviceBuffer
@@ -352,6 +360,8 @@ class DeviceInt4Weights:
     nbytes: int
     group: int = GROUP
     t16: tuple | None = None
+    zmax: int | None = None
+    t16f8: tuple | None = None
 
     def tiles(self) -> tuple:
         """(qwt, st, zt or None) in the t16 layout, repacked on first use (once, under a
@@ -376,6 +386,28 @@ class DeviceInt4Weights:
             _check(L.lb_stream_synchronize(None), "lb_stream_synchronize", False)
             self.t16 = (qwt, st, zt)
         return self.t16
+
+    def f8_exact(self) -> bool:
+        """Whether the t16f8 layout holds this matrix exactly (every zero-point <= 15)."""
+        return self.group == GROUP and self.zmax is not None and self.zmax <= 15
+
+    def tiles_f8(self) -> tuple:
+        """(qwt8, st) in the t16f8 layout, repacked on first use (as tiles())."""
+        if not self.f8_exact():
+            raise ValueError("the t16f8 layout needs groups of 128 and zero-points of at most 15")
+        with _TILE_LOCK:
+            if self.t16f8 is None:
+                L = lib()
+                bq, bs = _sz(0), _sz(0)
+                _check(L.lbd_int4_t16f8_bytes(self.n, self.kp, C.byref(bq), C.byref(bs)), "lbd_int4_t16f8_bytes",
+                       False)
+                qwt8, st = DeviceBuffer(bq.value), DeviceBuffer(bs.value)
+                _check(L.lbd_repack_int4_t16f8(self.qw.ptr, self.scales.ptr,
+                                               None if self.zeros is None else self.zeros.ptr, self.n, self.kp,
+                                               qwt8.ptr, st.ptr, None), "lbd_repack_int4_t16f8", False)
+                _check(L.lb_stream_synchronize(None), "lb_stream_synchronize", False)
+                self.t16f8 = (qwt8, st)
+            return self.t16f8
 
 
 @dataclass
@@ -414,9 +446,10 @@ def to_device(w):
     The handle is a snapshot: later edits of the host arrays are not seen.
     """
     if isinstance(w, Int4Weights):
+        zmax = 8 if w.zeros is None else int(w.zeros.max(initial=0))
         return DeviceInt4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.scales),
                                  None if w.zeros is None else DeviceBuffer.from_array(w.zeros),
-                                 w.n, w.kp, w.k, w.nbytes, w.group)
+                                 w.n, w.kp, w.k, w.nbytes, w.group, zmax=zmax)
     if isinstance(w, MXFP4Weights):
         return DeviceMXFP4Weights(DeviceBuffer.from_array(w.qw), DeviceBuffer.from_array(w.e8m0),
                                   w.n, w.kp, w.k, w.nbytes)
@@ -465,7 +498,8 @@ def quantize_int4_device(w, asym: bool = False, scale: str = "absmax", shape=Non
     # other streams read the result
     _check(lib().lb_stream_synchronize(stream), "lb_stream_synchronize", False)
     nbytes = n * kp // 2 + n * g * 4 + (n * g if asym else 0)
-    return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes, group)
+    # the device packer clips zero-points to 0-15, as the host packer does
+    return DeviceInt4Weights(qw, sc, z, n, kp, k, nbytes, group, zmax=15 if asym else 8)
 
 
 def quantize_mxfp4_device(w, shape=None, stream=None) -> "DeviceMXFP4Weights":
@@ -509,6 +543,26 @@ class _Staging(threading.local):
 _STAGE = _Staging()
 
 
+def w4a16_uses_t16f8(w, m: int) -> bool:
+    """Whether W4A16 at M = m on resident weights `w` reads the t16f8 copy: it holds
+    the matrix exactly and the library expects it to be faster at this shape."""
+    return w.f8_exact() and _check(lib().lbd_w4a16_prefers_t16f8(m, w.n, w.kp), "lbd_w4a16_prefers_t16f8",
+                                   False) == 1
+
+
+def gemm_w4a16_tiles(w, dx: int, m: int, dy: int, prm: _Params, ws: int, ws_bytes: int, stream) -> int:
+    """W4A16 on the bf16 matrix cores for resident weights `w`: lbd_gemm_w4a16_t16f8 on
+    the t16f8 copy where w4a16_uses_t16f8, else lbd_gemm_w4a16_t16 on the t16 copy (the
+    same results bit for bit). Returns the C call's code."""
+    L = lib()
+    if w4a16_uses_t16f8(w, m):
+        qwt8, st = w.tiles_f8()
+        return L.lbd_gemm_w4a16_t16f8(dx, m, w.kp, qwt8.ptr, st.ptr, w.n, dy, C.byref(prm), ws, ws_bytes, stream)
+    qwt, st, zt = w.tiles()
+    return L.lbd_gemm_w4a16_t16(dx, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n, dy,
+                                C.byref(prm), ws, ws_bytes, stream)
+
+
 def _run_dev(kind: str, w, m: int, dx: int, dy: int, prm: _Params, stream) -> int:
     """Launch one GEMM on resident weights `w` (device pointers dx / dy) on `stream`;
     the matrix-core regime reads the t16 tile layout, repacked on first use."""
@@ -518,9 +572,7 @@ def _run_dev(kind: str, w, m: int, dx: int, dy: int, prm: _Params, stream) -> in
     if kind in ("w4a16", "mxfp4") and mfma:
         ws = _STAGE.buffer("ws", L.lbd_bf16x3_workspace_bytes(m, w.kp))
         if kind == "w4a16":
-            qwt, st, zt = w.tiles()
-            return L.lbd_gemm_w4a16_t16(dx, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n, dy,
-                                        C.byref(prm), ws.ptr, ws.nbytes, stream)
+            return gemm_w4a16_tiles(w, dx, m, dy, prm, ws.ptr, ws.nbytes, stream)
         qwt, et = w.tiles()
         return L.lbd_gemm_mxfp4_t16(dx, m, w.kp, qwt.ptr, et.ptr, w.n, dy, C.byref(prm), ws.ptr, ws.nbytes, stream)
     if kind == "w4a16":

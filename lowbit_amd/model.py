@@ -281,15 +281,12 @@ class Model:
                 rc = L.lbd_gemm_mxfp4(x, m, w.kp, w.qw.ptr, w.e8m0.ptr, w.n, y, C.byref(prm), s)
         else:
             zp = None if w.zeros is None else w.zeros.ptr
-            if mfma:
+            if mfma and self.backend == "w4a16":
+                rc = K.gemm_w4a16_tiles(w, x, m, y, prm, ws.ptr, ws.nbytes, s)
+            elif mfma:
                 qwt, st, zt = w.tiles()
-                ztp = None if zt is None else zt.ptr
-                if self.backend == "w4a16":
-                    rc = L.lbd_gemm_w4a16_t16(x, m, w.kp, qwt.ptr, st.ptr, ztp, w.n, y, C.byref(prm), ws.ptr,
-                                              ws.nbytes, s)
-                else:
-                    rc = L.lbd_gemm_w4a8_t16(x, m, w.kp, qwt.ptr, st.ptr, ztp, w.n, y, C.byref(prm), ws.ptr,
-                                             ws.nbytes, s)
+                rc = L.lbd_gemm_w4a8_t16(x, m, w.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, w.n, y,
+                                         C.byref(prm), ws.ptr, ws.nbytes, s)
             elif self.backend == "w4a16":
                 rc = L.lbd_gemm_w4a16(x, m, w.kp, w.qw.ptr, w.scales.ptr, zp, w.n, y, C.byref(prm), s)
             else:

@@ -165,7 +165,10 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
     dy = K.DeviceBuffer(4 * m * n)
     if mfma:
         for d in pool:
-            d.tiles()
+            if fmt == "w4a16" and K.w4a16_uses_t16f8(d, m):
+                d.tiles_f8()
+            else:
+                d.tiles()
         ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp) if fmt == "w4a8" else L.lbd_bf16x3_workspace_bytes(m, W.kp)
     else:
         ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp)
@@ -182,11 +185,12 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
                 qwt, et = d.tiles()
                 rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, W.kp, qwt.ptr, et.ptr, n, dy.ptr, C.byref(prm), ws.ptr,
                                           ws_bytes, s)
+            elif fmt == "w4a16":
+                rc = K.gemm_w4a16_tiles(d, dx.ptr, m, dy.ptr, prm, ws.ptr, ws_bytes, s)
             else:
                 qwt, st, zt = d.tiles()
-                fn = L.lbd_gemm_w4a8_t16 if fmt == "w4a8" else L.lbd_gemm_w4a16_t16
-                rc = fn(dx.ptr, m, W.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, n, dy.ptr, C.byref(prm),
-                        ws.ptr, ws_bytes, s)
+                rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, n,
+                                         dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
         elif fmt == "mxfp4":
             rc = L.lbd_gemm_mxfp4(dx.ptr, m, W.kp, d.qw.ptr, d.e8m0.ptr, n, dy.ptr, C.byref(prm), s)
         elif fmt == "w4a16":
@@ -201,7 +205,8 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
     _check(L.lb_stream_synchronize(s), "sync")
     y = dy.to_array((m, n), np.float32)
     keep = (pool, dx, dy, ws)  # alive while the caller times `launch`
-    return launch, y, K.ISA_NAMES.get(path, "?"), "t16" if mfma else "row-major", len(pool), keep
+    layout = ("t16f8" if fmt == "w4a16" and K.w4a16_uses_t16f8(first, m) else "t16") if mfma else "row-major"
+    return launch, y, K.ISA_NAMES.get(path, "?"), layout, len(pool), keep
 
 
 def _roofline(fmt: str, layout: str, m: int, n: int, k: int, t: float, wbytes: int) -> tuple[str, float]:

@@ -133,6 +133,18 @@ def test_t16_sizes_and_argument_checks():
     prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
     assert L.lbd_gemm_w4a8_t16(None, 1, 256, None, None, None, 16, None, C.byref(prm), None, 0, None) == -6
     assert L.lbd_gemm_w4a8_t16(None, 0, 256, None, None, None, 16, None, C.byref(prm), None, 0, None) == -1
+    # t16f8: one byte per code, so twice the t16 tile bytes; the same scale array
+    assert L.lbd_int4_t16f8_bytes(17, 256, C.byref(bq), C.byref(bs)) == 0
+    assert (bq.value, bs.value) == (2 * 2 * 4 * 1024, 2 * 16 * 4 * 4)
+    assert L.lbd_int4_t16f8_bytes(11008, 4096, C.byref(bq), None) == 0 and bq.value == 11008 * 4096
+    assert L.lbd_int4_t16f8_bytes(17, 200, C.byref(bq), None) == -1
+    assert L.lbd_repack_int4_t16f8(None, None, None, 16, 256, None, None, None) == -6
+    assert L.lbd_repack_int4_t16f8(None, None, None, 16, 200, None, None, None) == -1
+    assert L.lbd_gemm_w4a16_t16f8(None, 1, 256, None, None, 16, None, C.byref(prm), None, 0, None) == -6
+    assert L.lbd_gemm_w4a16_t16f8(None, 1, 0, None, None, 16, None, C.byref(prm), None, 0, None) == -1
+    # without a device the rule assumes 256 compute units
+    assert L.lbd_w4a16_prefers_t16f8(64, 11008, 4096) == 1 and L.lbd_w4a16_prefers_t16f8(16, 11008, 4096) == 0
+    assert L.lbd_w4a16_prefers_t16f8(64, 4096, 11008) == 0 and L.lbd_w4a16_prefers_t16f8(0, 16, 128) == -1
     assert L.lbd_gemm_path(2, 1, 4096, C.byref(prm)) == K.ISA_GFX950
     assert L.lbd_gemm_path(2, 64, 4096, C.byref(prm)) == K.ISA_GFX950_MFMA
     assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6

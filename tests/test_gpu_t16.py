@@ -149,7 +149,9 @@ def test_w4a16_bf16x3_within_bound(rng, m, n, k, asym):
     W = lb.quantize_int4(_lognormal_rows(rng, n, k), asym=asym)
     D = lb.to_device(W)
     y = K.gemm_w4a16(x, D, isa="gfx950-mfma")
-    assert K.last_path() == "gfx950-mfma" and D.t16 is not None
+    f8 = K.w4a16_uses_t16f8(D, m)
+    assert K.last_path() == "gfx950-mfma" and (D.t16f8 if f8 else D.t16) is not None
+    assert (D.t16 if f8 else D.t16f8) is None
     xp = lb.formats.pad_acts(x, W.kp)
     ref = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros)
     bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
@@ -282,5 +284,6 @@ def test_batch_kernels_every_share_of_subtiles(rng, fmt, m, share):
         y = K.gemm_w4a8(x, D, isa="gfx950-mfma")
         a = lb.quantize_act_int8(x)
         ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
-    assert K.last_path() == "gfx950-mfma" and D.t16 is not None
+    f8 = fmt == "w4a16" and K.w4a16_uses_t16f8(D, m)
+    assert K.last_path() == "gfx950-mfma" and (D.t16f8 if f8 else D.t16) is not None
     O.assert_fp_close(y, ref, bound, 1e-5)
