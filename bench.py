@@ -292,6 +292,52 @@ PROBE_FORMS = ["v_fmac_f32", "v_fma_f32", "v_add_f32", "v_mul_f32", "v_and_b32",
                "v_dot4_i32_i8", "v_pk_add_f16", "v_cvt_scalef32_pk_f32_fp4"]
 
 
+BARRIER_MODES = ("atomic counter", "flag per workgroup", "flags + agent release/acquire fences")
+
+
+def grid_barrier_costs(dev: Dev, cus: int, rounds: int = 200, reps: int = 5) -> dict:
+    """Cost of one device-wide barrier inside a launch (lbd_probe_grid_barrier): HIP
+    events around one eager launch of `rounds` barriers and around one of none (the
+    launch and the clearing of the sync words), median over `reps`, the difference
+    divided by `rounds`. A grid whose waits timed out (not every workgroup resident)
+    is reported as such instead of a time."""
+    L = dev.L
+    sync = dev.K.DeviceBuffer((64 + 1024) * 4)
+    status = dev.K.DeviceBuffer(4)
+
+    def launch_ms(g, r, mode):
+        e0, e1 = dev.event(), dev.event()
+        dev.check(L.lb_event_record(e0, dev.stream), "record")
+        dev.check(L.lbd_probe_grid_barrier(g, r, mode, sync.ptr, sync.nbytes, status.ptr, dev.stream),
+                  "barrier probe")
+        dev.check(L.lb_event_record(e1, dev.stream), "record")
+        dev.check(L.lb_event_synchronize(e1), "sync")
+        ms = dev.elapsed_ms(e0, e1)
+        L.lb_event_destroy(e0)
+        L.lb_event_destroy(e1)
+        return ms, int(status.to_array((1,), np.uint32)[0])
+
+    out = {}
+    for g, modes in ((cus, (0, 1, 2)), (cus // 4, (0, 1)), (4 * cus, (0,))):
+        for mode in modes:
+            base, full, timed_out = [], [], 0
+            for _ in range(reps):
+                ms0, t0 = launch_ms(g, 0, mode)
+                ms1, t1 = launch_ms(g, rounds, mode)
+                base.append(ms0)
+                full.append(ms1)
+                timed_out |= t0 | t1
+            key = f"{g} workgroups, {BARRIER_MODES[mode]}"
+            if timed_out:
+                out[key] = "timed out"
+                log(f"grid barrier, {key}: a wait timed out")
+                continue
+            us = (float(np.median(full)) - float(np.median(base))) * 1e3 / rounds
+            out[key] = round(us, 3)
+            log(f"grid barrier, {key}: {us:.2f} us per barrier")
+    return out
+
+
 def machine_facts(dev: Dev, warmup: int) -> dict:
     """The device facts the kernel designs rest on, measured by the library's probe
     kernels (lb_probe.hip): the issue cost of single VALU instruction forms (16 waves
@@ -314,7 +360,8 @@ def machine_facts(dev: Dev, warmup: int) -> dict:
         ms = dev.time_launches(lambda i, g=g: dev.check(L.lbd_empty_kernel(g, dev.stream), "empty"), 200, warmup)
         empty[f"{g}x512"] = round(ms * 1e3, 3)
         log(f"empty kernel {g} x 512 threads: {empty[f'{g}x512']:.2f} us per graph-replayed launch")
-    return {"valu_ns_per_wave_instruction_per_cu": rates, "empty_launch_us": empty,
+    barrier = grid_barrier_costs(dev, cus)
+    return {"valu_ns_per_wave_instruction_per_cu": rates, "empty_launch_us": empty, "grid_barrier_us": barrier,
             "probe": {"workgroups": wgs, "threads": 512, "iters": iters, "instructions_per_iter": 32,
                       "independent_registers": 8}}
 

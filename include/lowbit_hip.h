@@ -464,6 +464,17 @@ int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream);
 int lbd_probe_forms(void);
 /* a kernel of `workgroups` x 512 threads that does nothing: the fixed cost of a launch */
 int lbd_empty_kernel(int workgroups, void *stream);
+/* Device-wide barrier probe (no reference counterpart; the measurement behind the
+ * choice of one launch per decode phase over a persistent kernel): `rounds` (0 ..
+ * 100000) barriers between `workgroups` (1 .. 1024) one-wave workgroups of one launch.
+ * `mode` 0: one agent-scope atomic counter; 1: one flag per workgroup, polled by all;
+ * 2: as 1 with agent-scope release / acquire fences around each barrier (what data
+ * handed across it needs). `sync` is a device buffer of at least (64 + workgroups) * 4
+ * bytes and `status` one device dword; both are cleared on `stream` before the launch
+ * (so the call is not for graph capture). Every wait is bounded: status becomes 1 if
+ * one timed out (a workgroup that was not resident), and the launch still ends. */
+int lbd_probe_grid_barrier(int workgroups, int rounds, int mode, uint32_t *sync, size_t sync_bytes,
+                           uint32_t *status, void *stream);
 
 #ifdef __cplusplus
 }

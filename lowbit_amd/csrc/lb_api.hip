@@ -1378,6 +1378,17 @@ int lbd_empty_kernel(int workgroups, void *stream) {
   if (e != hipSuccess) return fail_hip(e, "empty kernel launch");
   return ok(0);
 }
+int lbd_probe_grid_barrier(int workgroups, int rounds, int mode, uint32_t *sync, size_t sync_bytes,
+                           uint32_t *status, void *stream) {
+  if (!sync || !status) return fail(LB_ERR_ARG, "barrier probe needs a sync buffer and a status word");
+  if (workgroups <= 0 || workgroups > lbk::kBarrierMaxWorkgroups || rounds < 0 || rounds > 100000 || mode < 0 ||
+      mode > 2)
+    return fail(LB_ERR_ARG, "barrier probe: 1..1024 workgroups, 0..100000 rounds, mode 0, 1 or 2");
+  if (sync_bytes < (size_t)(64 + workgroups) * 4) return fail(LB_ERR_ARG, "barrier probe: sync buffer too small");
+  hipError_t e = lbk::launch_grid_barrier(workgroups, rounds, mode, sync, status, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "barrier probe launch");
+  return ok(0);
+}
 int lbd_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {
   if (!dst || !src || bytes % 16 || !aligned16(dst) || !aligned16(src))
     return fail(LB_ERR_ARG, "copy needs 16-byte aligned pointers and a multiple of 16 bytes");

@@ -118,7 +118,7 @@ __device__ __forceinline__ void attn_run(const AttnRound<D> &first, float4 q4, f
   constexpr int LPR = AttnCfg<D>::kLPR, RPL = AttnCfg<D>::kRPL, U = AttnCfg<D>::kU, KB = AttnCfg<D>::kKB;
   constexpr int NW = NT / kWave;
   static_assert(NT % kWave == 0, "whole waves");
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), r = lane / LPR, e4 = lane % LPR;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), r = lane / LPR;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const float scale = 1.0f / sqrtf((float)D);
   float m = -INFINITY, l = 0.0f;

@@ -146,6 +146,14 @@ hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipS
 int valu_probe_forms();
 // a kernel that does nothing, workgroups of 512 threads
 hipError_t launch_empty(int workgroups, hipStream_t s);
+// Device-wide barrier probe (lb_probe.hip): `rounds` barriers between `workgroups`
+// (1 .. kBarrierMaxWorkgroups) one-wave workgroups, `mode` 0 (one atomic counter), 1
+// (a flag per workgroup) or 2 (flags with agent-scope release / acquire fences).
+// Clears sync[64 + workgroups] and status[1] on the stream first (not for capture);
+// status[0] becomes 1 if a wait timed out.
+constexpr int kBarrierMaxWorkgroups = 1024;
+hipError_t launch_grid_barrier(int workgroups, int rounds, int mode, uint32_t *sync, uint32_t *status,
+                               hipStream_t s);
 
 // Decoder-layer kernels (lb_model.hip).
 hipError_t launch_embed(const float *table, int vocab, int hidden, const int32_t *tok, int T, float *x, hipStream_t s);

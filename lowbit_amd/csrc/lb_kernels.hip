@@ -753,10 +753,15 @@ __global__ __launch_bounds__(kW8Threads) void w4a8_gemm_kernel(GemmArgs a) {
 // compile without spills; PF is not: with t16 weights, deeper prefetch queues so
 // many weight loads ahead of the activation operands that the first tile starts
 // later (per-wave timelines at 64 x 11008 x 4096: first tile 5.6 us after the start
-// with 5 subtiles in flight, 3.4 us with 2; the GEMM 10.5 -> 8.5 us).
+// with 5 subtiles in flight, 3.4 us with 2; the GEMM 10.5 -> 8.5 us). Two 16-row
+// blocks (TM = 2) keep one subtile in flight: 160 VGPRs instead of 182, and the
+// quantizer + GEMM call at 64 x 11008 x 4096 hot 12.42-12.47 -> 12.05-12.10 us
+// (alternating in one process; 64 x 4096 x 4096 within 0.1 us either way). More
+// waves did not help: 16-row blocks at two workgroups per CU (4 waves per SIMD,
+// 111-118 VGPRs) took 13.1-13.8 us.
 template <int TM> struct W8Cfg {
   static constexpr int NS = TM >= 4 ? 1 : 6;
-  static constexpr int PF = TM >= 4 ? 0 : 2;
+  static constexpr int PF = TM >= 4 ? 0 : TM == 2 ? 1 : 2;
   static constexpr int PFR = TM >= 4 ? 0 : 4;
   static constexpr int PFS = TM >= 4 ? 0 : TM == 2 ? 2 : 3;
 };

@@ -140,6 +140,68 @@ hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipS
 
 int valu_probe_forms() { return kProbeForms; }
 
+// ---- device-wide barrier probe: the cost of one barrier between all workgroups of
+//      a launch, the synchronisation a persistent kernel needs between dependent
+//      phases (each phase of a one-token decode step reads what every workgroup of
+//      the previous phase wrote). One wave per workgroup; the host keeps the grid
+//      small enough to be resident. Every wait is bounded: after `spin_limit` polls a
+//      workgroup records the time-out in status[0] and returns, so the launch always
+//      ends, whether or not every workgroup was resident.
+//   mode 0: one counter (sync[0]); a workgroup adds 1 per round (agent-scope atomic)
+//           and polls it until every workgroup's addition for the round is there
+//   mode 1: one flag per workgroup (sync[64 + b], its own cache line group apart
+//           from the counter); a workgroup stores its round number and polls all
+//           flags, one per lane (no atomic read-modify-write: nothing serialises)
+//   mode 2: mode 1 with an agent-scope release fence before the flag store and an
+//           agent-scope acquire fence after the wait, which is what data written
+//           before the barrier and read after it by another workgroup needs
+// Counter and flags only grow, so a workgroup already in the next round never
+// undoes a condition a slower one is still waiting for.
+__global__ __launch_bounds__(kWave) void grid_barrier_kernel(uint32_t *sync, int rounds, int mode,
+                                                             uint32_t spin_limit, uint32_t *status) {
+  const uint32_t G = gridDim.x;
+  const uint32_t lane = threadIdx.x;
+  uint32_t *flags = sync + 64;
+  for (int r = 0; r < rounds; r++) {
+    const uint32_t want = (uint32_t)r + 1;
+    if (mode == 2) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (lane == 0) {
+      if (mode == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else __hip_atomic_store(flags + blockIdx.x, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (uint32_t spin = 0;; spin++) {
+      bool ok = true;
+      if (mode == 0) {
+        ok = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want * G;
+      } else {
+        for (uint32_t i = lane; i < G; i += kWave)
+          ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want;
+      }
+      if (__all(ok)) break;
+      if (spin >= spin_limit) {
+        if (lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (mode == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+}
+
+hipError_t launch_grid_barrier(int workgroups, int rounds, int mode, uint32_t *sync, uint32_t *status,
+                               hipStream_t s) {
+  if (workgroups <= 0 || workgroups > kBarrierMaxWorkgroups || rounds < 0 || rounds > 100000 || mode < 0 ||
+      mode > 2)
+    return hipErrorInvalidValue;
+  // the counter reaches rounds * workgroups <= 1.03e8, far below 2^32
+  hipError_t e = hipMemsetAsync(sync, 0, (size_t)(64 + workgroups) * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(status, 0, 4, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(grid_barrier_kernel, dim3(workgroups), dim3(kWave), 0, s, sync, rounds, mode,
+                     (uint32_t)(1u << 16), status);
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(512) void empty_kernel() {}
 
 hipError_t launch_empty(int workgroups, hipStream_t s) {

@@ -151,7 +151,8 @@ def test_t16_sizes_and_argument_checks():
 
 
 def test_probe_argument_checks():
-    """The measurement probes (lbd_probe_valu, lbd_empty_kernel, lbd_read_kernel) reject
+    """The measurement probes (lbd_probe_valu, lbd_empty_kernel, lbd_read_kernel,
+    lbd_probe_grid_barrier) reject
     bad arguments before any device work, and the probe count matches the instruction
     forms bench.py names."""
     import bench
@@ -169,6 +170,15 @@ def test_probe_argument_checks():
     assert L.lbd_read_kernel(out, 1000, 1, 256, 1, out, None) == -6   # not a multiple of 16
     assert L.lbd_read_kernel(out, 1024, 1, 128, 1, out, None) == -6   # 128 threads
     assert L.lbd_read_kernel(out, 1024, 1, 256, 3, out, None) == -6   # 3 loads
+    sync = (64 + 256) * 4
+    assert L.lbd_probe_grid_barrier(256, 10, 0, None, sync, out, None) == -6    # no sync buffer
+    assert L.lbd_probe_grid_barrier(256, 10, 0, out, sync, None, None) == -6    # no status word
+    assert L.lbd_probe_grid_barrier(0, 10, 0, out, sync, out, None) == -6       # no workgroups
+    assert L.lbd_probe_grid_barrier(1025, 10, 0, out, 8192, out, None) == -6    # past 1024 workgroups
+    assert L.lbd_probe_grid_barrier(256, -1, 0, out, sync, out, None) == -6     # negative rounds
+    assert L.lbd_probe_grid_barrier(256, 100001, 0, out, sync, out, None) == -6
+    assert L.lbd_probe_grid_barrier(256, 10, 3, out, sync, out, None) == -6     # no mode 3
+    assert L.lbd_probe_grid_barrier(256, 10, 0, out, sync - 4, out, None) == -6  # sync too small
 
 
 def test_argmax_slot_count_matches_header():
