@@ -216,6 +216,9 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
             if fmt == "w4a8":
                 rc = L.lbd_gemm_w4a8_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
                                          dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
+            elif fmt == "w4a16":
+                rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, b[2].ptr if b[2] else None, n,
+                                          dy.ptr, C.byref(prm), ws.ptr, ws_bytes, s)
             else:
                 rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, W.kp, b[0].ptr, b[1].ptr, n, dy.ptr, C.byref(prm), ws.ptr,
                                           ws_bytes, s)
@@ -654,6 +657,8 @@ def main() -> int:
                     help="only sweep the plain streaming read of the headline weight bytes (cold and hot) "
                          "and print its JSON")
     ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor sweep")
+    ap.add_argument("--batch-m", type=int, default=BATCH[0], metavar="M",
+                    help="rows of the hot batch GEMMs (default 64, the BASELINE shape)")
     ap.add_argument("--machine-facts", action="store_true",
                     help="only measure the device facts the kernels are designed around (VALU issue cost per "
                          "instruction form, launch cost, the plain-read floor) and print their JSON")
@@ -720,13 +725,14 @@ def main() -> int:
             f"call through ctypes {r['call_us']:.1f} us  ({r['timed_launches']} launches, "
             f"{r['bytes_rotated'] >> 20} MiB rotated)")
 
-    # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167)
+    # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167);
+    # --batch-m selects another M (the counter profiles of the M = 16 kernels)
     if not args.only_headline:
-        mb, nb, kb = BATCH
+        mb, nb, kb = args.batch_m, BATCH[1], BATCH[2]
         xb = rng.standard_normal((mb, kb)).astype(np.float32)
         for fmt in ["w4a8", "w4a16", "mxfp4"]:
             W = mx if fmt == "mxfp4" else w4
-            r = measure(dev, fmt, BATCH, W, xb, cold=False, steps=args.steps,
+            r = measure(dev, fmt, (mb, nb, kb), W, xb, cold=False, steps=args.steps,
                         warmup=max(2, args.warmup // 4), graph=graph)
             r["max_rel_err"] = float(f"{rel_err(fmt, W, xb, r.pop('y')):.3g}")
             if fmt == "w4a8":
@@ -740,8 +746,8 @@ def main() -> int:
             else:
                 r["mfma"] = "fp32"
                 r["mfma_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
-            results[f"{fmt}_m64"] = r
-            log(f"{fmt:6s} M=64 hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
+            results[f"{fmt}_m{mb}"] = r
+            log(f"{fmt:6s} M={mb} hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
                 f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}  "
                 f"call through ctypes {r['call_us']:.1f} us")
 
