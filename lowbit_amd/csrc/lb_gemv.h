@@ -623,7 +623,7 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
     const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (in && a.zeros) ? (uint32_t)G : 0u);
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
-      const uint32_t ci = cbase + (uint32_t)lane + kWave * it, gi = ci >> 2;
+      const uint32_t ci = cbase + (uint32_t)lane + kWave * it, gi = fmt_g32(F) ? ci : ci >> 2;
       const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
       st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
       st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gi * 4), 0, kPacedAux);
@@ -638,7 +638,7 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
 template <int F, bool DW>
 __device__ __forceinline__ uint32_t paced_byte(uint32_t word, uint32_t ci) {
   if constexpr (!DW) return word & 0xFFu;
-  const uint32_t idx = F == F_MXFP4 ? ci : ci >> 2;  // block or group index
+  const uint32_t idx = fmt_group(F) == 32 ? ci : ci >> 2;  // block or group index
   return (word >> (8 * (idx & 3u))) & 0xFFu;
 }
 
@@ -655,7 +655,8 @@ __device__ __forceinline__ float div127(float a) {
 
 template <int F, int NIT, bool DW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
-  constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q);
+  constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q || F == F_W4A8G32);
+  constexpr bool kW16 = (F == F_W4A16 || F == F_W4A16G32);  // int4 codes, fp32 activations
   constexpr int T = kGemvThreads;
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float red[kGemvWaves];
@@ -663,7 +664,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   const int nch = Kp >> 5;
   const int nit = (nch + kWave - 1) / kWave;
   const int nchp = nit * kWave;
-  const int G = Kp / fmt_group(F), Gp = nchp / 4;
+  const int G = Kp / fmt_group(F), Gp = fmt_g32(F) ? nchp : nchp / 4;  // padded group count
   // ---- 1. the activation row into registers (the kernel's first loads), then the
   //         row shares and the first row's weights
   constexpr int S = NIT;
@@ -679,7 +680,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   // W4A16 chunk sums) gates every row, queue ahead of the weight stream (1 x 11008 x
   // 4096 cold: W4A8 6.23 -> 5.77 us, W4A16 6.49 -> 6.40; 64 and 128 clocks gain
   // less, 320 and more lose again; MXFP4 gains nothing)
-  if constexpr (F == F_W4A8 || F == F_W4A16) __builtin_amdgcn_s_sleep(4);
+  if constexpr (F == F_W4A8 || F == F_W4A8G32 || kW16) __builtin_amdgcn_s_sleep(4);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   // rows of this workgroup (an even share: N / grid and N % grid come from the host),
@@ -700,7 +701,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. the prologue: stage (or quantize) the activations into the LDS planes
-  if constexpr (F == F_W4A16 || F == F_MXFP4) {
+  if constexpr (kW16 || F == F_MXFP4) {
 #pragma unroll
     for (int i = 0; i < S; i++) {
       if (i >= nit) continue;
@@ -708,7 +709,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
       chunk_pos(F, threadIdx.x * 4 + i * T * 4, ci, half, within);
       *reinterpret_cast<float4 *>(xl + ((size_t)(half * 4 + (within >> 2)) * nchp + ci) * 4) = xr[i];
     }
-  } else if constexpr (F == F_W4A8) {
+  } else if constexpr (F == F_W4A8 || F == F_W4A8G32) {
     float amax = 0.0f;  // padding reads +0 and cannot raise it
 #pragma unroll
     for (int i = 0; i < S; i++) {
@@ -732,8 +733,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
       chunk_pos(F, e, ci, half, within);
       const uint32_t qv = quant4_fast(xr[i], sc, inv);
       *reinterpret_cast<uint32_t *>(ql + ((size_t)half * nchp + ci) * 16 + within) = qv;
-      const int gs = half_wave_sum(sum_i8x4(qv));
-      if ((threadIdx.x & 31) == 31) asl[e >> 7] = gs;
+      if constexpr (F == F_W4A8G32) {
+        const int gs = eighth_wave_sum(sum_i8x4(qv));  // a group of 32 is eight threads
+        if ((threadIdx.x & 7) == 7) asl[e >> 5] = gs;
+      } else {
+        const int gs = half_wave_sum(sum_i8x4(qv));  // a group of 128 is one half-wave
+        if ((threadIdx.x & 31) == 31) asl[e >> 7] = gs;
+      }
     }
   } else {  // F_W4A8Q: codes, group sums and the token scale as given
     const Rsrc rq = make_rsrc(a.xq, (uint32_t)Kp);
@@ -750,9 +756,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   // ---- 3. this lane's activation operands into registers (rows up to 4096 elements:
   //         fp32, 64 VGPRs, or int8 codes, 16), read from the LDS planes once
   constexpr bool kXReg = NIT <= 2;
-  constexpr bool kF32 = (F == F_W4A16 || F == F_MXFP4);
+  constexpr bool kF32 = (kW16 || F == F_MXFP4);
   float4 xv[kXReg && kF32 ? NIT : 1][8];
-  float xsm[kXReg && F == F_W4A16 ? NIT : 1];
+  float xsm[kXReg && kW16 ? NIT : 1];
   uint4 al[kXReg && kInt8 ? NIT : 1], ah[kXReg && kInt8 ? NIT : 1];
   int as[kXReg && kInt8 ? NIT : 1];
   if constexpr (kXReg) {
@@ -762,11 +768,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
       if constexpr (kF32) {
 #pragma unroll
         for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
-        if constexpr (F == F_W4A16) xsm[it] = chunk_xsum(xv[it]);
+        if constexpr (kW16) xsm[it] = chunk_xsum(xv[it]);
       } else {
         al[it] = *reinterpret_cast<const uint4 *>(ql + (size_t)ci * 16);
         ah[it] = *reinterpret_cast<const uint4 *>(ql + ((size_t)nchp + ci) * 16);
-        as[it] = (ci & 3) == 0 ? asl[ci >> 2] : 0;
+        // the zero-point term once per group, by the lane holding its first chunk
+        if constexpr (fmt_g32(F)) as[it] = asl[ci];
+        else as[it] = (ci & 3) == 0 ? asl[ci >> 2] : 0;
       }
     }
   }
@@ -780,7 +788,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
 #pragma unroll
       for (int it = 0; it < NIT; it++) {
         const uint32_t ci = (uint32_t)lane + kWave * it;
-        if constexpr (F == F_W4A16) {
+        if constexpr (kW16) {
           const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
           acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
         } else if constexpr (F == F_MXFP4) {
@@ -844,7 +852,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
 
 // ============================================================ paced decode GEMV, rows split (M = 1, K > 4096)
 //
-// W4A16 and MXFP4 rows of more than 128 chunks (4096 elements): their fp32
+// W4A16 (either group size) and MXFP4 rows of more than 128 chunks (4096 elements): their fp32
 // activations no longer fit a wave's registers (64 VGPRs hold two chunks per lane),
 // and reading them from LDS for every row costs more LDS bandwidth than the row's
 // weights (4096 x 11008: 44 KB per row, 16 waves per CU). Here a row's chunks are cut
@@ -861,7 +869,8 @@ constexpr int kSplitChunks = 2 * kWave;  // chunks per slice
 
 template <int F, bool DW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs a) {
-  static_assert(F == F_W4A16 || F == F_MXFP4, "fp32 activations");
+  static_assert(F == F_W4A16 || F == F_W4A16G32 || F == F_MXFP4, "fp32 activations");
+  constexpr bool kW16 = (F == F_W4A16 || F == F_W4A16G32);
   constexpr int T = kGemvThreads, NIT = 2, SX = kGemvMaxNit;  // X staging: up to 8 float4 per thread
   extern __shared__ __align__(16) unsigned char lds[];
   const int Kp = a.Kp;
@@ -878,7 +887,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
     for (int i = 0; i < SX; i++) xr[i] = ld_f4(rx, (threadIdx.x + i * T) * 16);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (F == F_W4A16) __builtin_amdgcn_s_sleep(4);  // as in the one-row kernel
+  if constexpr (kW16) __builtin_amdgcn_s_sleep(4);  // as in the one-row kernel
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   unsigned bx = blockIdx.x;
@@ -914,7 +923,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
     const int ci = (int)cb + lane + kWave * it;
 #pragma unroll
     for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
-    xsm[it] = F == F_W4A16 ? chunk_xsum(xv[it]) : 0.0f;
+    xsm[it] = kW16 ? chunk_xsum(xv[it]) : 0.0f;
   }
 
   // ---- 4. rows: the next one's loads out, then this one's slice sum into `part`
@@ -924,7 +933,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
 #pragma unroll
     for (int it = 0; it < NIT; it++) {
       const uint32_t ci = cb + (uint32_t)lane + kWave * it;
-      if constexpr (F == F_W4A16) {
+      if constexpr (kW16) {
         const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
         acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
       } else {
@@ -974,10 +983,9 @@ inline size_t gemv_split_lds_bytes(int Kp, int rows_max) {
 
 // Whether the paced kernel runs this launch: one activation row, no fused prologue or
 // epilogue, rows longer than 1024 elements (shorter ones load two rows per wave load
-// in gemv_kernel), group-128 int4 or MXFP4.
-inline bool gemv_paced_eligible(int fmt, const GemmArgs &a) {
-  return a.M == 1 && !fmt_g32(fmt) && gemv_prologue(a) == 0 && !a.bias && !a.res && !a.amax_key && !a.glu &&
-         (a.Kp >> 5) > kWave / 2;
+// in gemv_kernel); every format, int4 of either group size.
+inline bool gemv_paced_eligible(const GemmArgs &a) {
+  return a.M == 1 && gemv_prologue(a) == 0 && !a.bias && !a.res && !a.amax_key && !a.glu && (a.Kp >> 5) > kWave / 2;
 }
 
 // Rows held at once (R) from the share of rows each wave gets under the
@@ -1050,9 +1058,9 @@ static GemvPick pick_gemv(int nit, int nch, int rpw) {
 template <int F>
 static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipStream_t s, GemvPlan *plan) {
   const int nit = ((a.Kp >> 5) + kWave - 1) / kWave;
-  // metadata bytes per row: E8M0 one per 32 elements, zero-points one per 128
-  const bool dw = ((F == F_MXFP4 ? a.Kp / 32 : a.Kp / 128) % 4) == 0;
-  if constexpr (F == F_W4A16 || F == F_MXFP4) {
+  // metadata bytes per row: E8M0 or zero-points one per group (32 or 128 elements)
+  const bool dw = ((a.Kp / fmt_group(F)) % 4) == 0;
+  if constexpr (F == F_W4A16 || F == F_W4A16G32 || F == F_MXFP4) {
     // rows of more than 4096 elements: split over the waves, where the planes of
     // whole slices stay within the GEMV's LDS budget (rows up to 12288 elements)
     if (nit > 2 && gemv_split_lds_bytes(a.Kp, 0) <= kGemvLdsLimit) {
@@ -1132,8 +1140,8 @@ static hipError_t launch_gemv_mb(const GemmArgs &a, int num_cus, size_t lds, hip
   // it runs faster with the CU to itself (gate/up 9728 x 896: 5.1 -> 4.5 us)
   const double wg_bytes = (double)a.N * (a.Kp / 2) / (2.0 * cus);
   int per_cu = (kQuant && (a.N < 2 * 2 * cus * kGemvWaves || (PRO != 0 && wg_bytes < 32768.0))) ? 1 : 2;
-  if constexpr (MB == 1 && PRO == 0 && !fmt_g32(F)) {
-    if (gemv_paced_eligible(F, a)) return launch_gemv_paced<F>(a, cus, lds, s, plan);
+  if constexpr (MB == 1 && PRO == 0) {
+    if (gemv_paced_eligible(a)) return launch_gemv_paced<F>(a, cus, lds, s, plan);
   }
   for (;;) {
     int grid = (a.N + kGemvWaves - 1) / kGemvWaves;

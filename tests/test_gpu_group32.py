@@ -44,8 +44,13 @@ def test_device_packer_matches_host(rng, asym, scale, n, k):
         np.testing.assert_array_equal(D.zeros.to_array(ref.zeros.shape, np.uint8), ref.zeros)
 
 
+# M = 1 with rows past 1024 elements runs the paced kernels: (1, 45, 2080) holds its
+# activations in registers with byte-wise zero-point loads (65 groups, not a multiple
+# of four); (1, 33, 4160), (1, 50, 6000) and (1, 37, 11008) are W4A16's split variant
+# (2-3 slices, partial last slice) and W4A8's longer-row instantiations
 SHAPES = [(1, 64, 32), (1, 300, 896), (2, 33, 100), (3, 70, 4096), (4, 17, 4864), (5, 40, 1024),
-          (9, 11, 320), (1, 11008, 4096), (64, 96, 4096), (1, 40, 14336), (2, 20, 11008)]
+          (9, 11, 320), (1, 11008, 4096), (64, 96, 4096), (1, 40, 14336), (2, 20, 11008),
+          (1, 45, 2080), (1, 33, 4160), (1, 50, 6000), (1, 37, 11008)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
