@@ -204,7 +204,7 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
         dev.check(L.lb_stream_synchronize(s), "sync")
         pool = tiled
         if fmt != "w4a8":
-            ws_bytes = L.lbd_bf16x3_workspace_bytes(m, W.kp)
+            ws_bytes = L.lbd_bf16x3_workspace_bytes_split(0 if fmt == "w4a16" else 1, m, n, W.kp)
             ws = K.DeviceBuffer(ws_bytes)
 
     def launch(i):

@@ -222,6 +222,16 @@ int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                        const lb_params *p, void *workspace,
                        size_t workspace_bytes, void *stream);
 size_t lbd_bf16x3_workspace_bytes(int M, int Kp);
+/* Workspace bytes for the bf16x3 GEMMs (lbd_gemm_w4a16_t16 / _t16f8, kind 0, and
+ * lbd_gemm_mxfp4_t16, kind 1) that also lets them split K over the workgroups of a
+ * column where the shape gains (rows of at least 8192 elements): the split
+ * activations, then the slices' partial outputs, added by one more launch in slice
+ * order. A workspace of this size (or NULL) takes the split, one of
+ * lbd_bf16x3_workspace_bytes the unsplit GEMM; both meet the same bound, not the
+ * same bits. Equals lbd_bf16x3_workspace_bytes rounded up to 256 where no split is
+ * taken; 0 for an invalid argument. (No reference counterpart: the reference's
+ * GEMMs take no workspace.) */
+size_t lbd_bf16x3_workspace_bytes_split(int kind, int M, int N, int Kp);
 /* ---- "t16f8": int4 g128 weights for lbd_gemm_w4a16 on bf16 matrix cores with the
  *      zero-point folded in (no reference counterpart: a device-private copy of an
  *      Int4Weights matrix, src/lowbit/formats.py:56-87, that the bf16 matrix cores

@@ -263,6 +263,20 @@ int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s, bool f8 =
   return ok(LB_ISA_GFX950_MFMA);
 }
 
+// The workspace of a bf16x3 call: the split activations, then (K split over the
+// workgroups, where the shape takes it) the slices' partial outputs. A caller's
+// workspace of at least lbd_bf16x3_workspace_bytes bytes runs the unsplit GEMM; one
+// of lbd_bf16x3_workspace_bytes_split bytes, or none (the per-thread buffer), the
+// split one. The two give results within the same bound, not the same bits.
+int bf3_call(int fmt, lbk::GemmArgs &a, char *ws, size_t given, hipStream_t s, bool f8 = false) {
+  const size_t x3 = align256(lbk::x3_bytes(a.M, a.Kp)), part = lbk::bf3_part_bytes(fmt, a.M, a.N, a.Kp);
+  const bool own = ws == nullptr;
+  const int rc = take_workspace(own ? x3 + part : lbk::x3_bytes(a.M, a.Kp), given, s, &ws);
+  if (rc < 0) return rc;
+  if (part && (own || given >= x3 + part)) a.ypart = reinterpret_cast<float *>(ws + x3);
+  return run_bf3(fmt, a, ws, s, f8);
+}
+
 // Shared checks of the t16 GEMM entry points (32-bit offsets inside the kernels).
 int check_t16(int M, int Kp, int N, bool f8 = false) {
   if ((size_t)M * Kp * 4 > 0xFFFFFFF0u || lbk::x3_bytes(M, Kp) > 0xFFFFFFF0u)
@@ -528,6 +542,11 @@ size_t lbd_bf16x3_workspace_bytes(int M, int Kp) {
   return lbk::x3_bytes(M, Kp);
 }
 
+size_t lbd_bf16x3_workspace_bytes_split(int kind, int M, int N, int Kp) {
+  if (M <= 0 || N <= 0 || Kp <= 0 || (kind != 0 && kind != 1)) return 0;
+  return align256(lbk::x3_bytes(M, Kp)) + lbk::bf3_part_bytes(kind == 1 ? lbk::F_MXFP4 : lbk::F_W4A16, M, N, Kp);
+}
+
 int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt, const float *st, const uint8_t *zt,
                        int N, float *y, const lb_params *p, void *workspace, size_t workspace_bytes,
                        void *stream) {
@@ -543,8 +562,7 @@ int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt, const 
   a.M = M; a.Kp = Kp; a.N = N;
   a.wt16 = true;
   char *ws = static_cast<char *>(workspace);
-  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
-  return run_bf3(lbk::F_W4A16, a, ws, s);
+  return bf3_call(lbk::F_W4A16, a, ws, workspace_bytes, s);
 }
 
 int lbd_int4_t16f8_bytes(int N, int Kp, size_t *qwt8_bytes, size_t *st_bytes) {
@@ -590,8 +608,7 @@ int lbd_gemm_w4a16_t16f8(const float *x, int M, int Kp, const uint8_t *qwt8, con
   a.M = M; a.Kp = Kp; a.N = N;
   a.wt16 = true;
   char *ws = static_cast<char *>(workspace);
-  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
-  return run_bf3(lbk::F_W4A16, a, ws, s, true);
+  return bf3_call(lbk::F_W4A16, a, ws, workspace_bytes, s, true);
 }
 
 int lbd_mxfp4_t16_bytes(int N, int Kp, size_t *qwt_bytes, size_t *et_bytes) {
@@ -628,8 +645,7 @@ int lbd_gemm_mxfp4_t16(const float *x, int M, int Kp, const uint8_t *qwt, const 
   a.M = M; a.Kp = Kp; a.N = N;
   a.wt16 = true;
   char *ws = static_cast<char *>(workspace);
-  if ((rc = take_workspace(lbk::x3_bytes(M, Kp), workspace_bytes, s, &ws)) < 0) return rc;
-  return run_bf3(lbk::F_MXFP4, a, ws, s);
+  return bf3_call(lbk::F_MXFP4, a, ws, workspace_bytes, s);
 }
 
 }  // extern "C"

@@ -32,6 +32,7 @@ struct GemmArgs {
   // that no division runs ahead of the kernel's first loads
   int split_base = 0, split_rem = 0;
   const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path)
+  float *ypart = nullptr;         // bf16x3 split over K: the slices' partial outputs [ks][M][N]
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
   bool wt16 = false;              // qw / scales / zeros / e8m0 in the MFMA tile layout (t16)
   // Decode fusions of the small-M kernels (gemv regime). Prologues (M == 1):
@@ -87,6 +88,10 @@ hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N
 __host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
 hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, bool f8 = false);
+// K slices of the bf16x3 GEMM at this shape (1: no split), and the bytes of their
+// partial outputs that launch_bf3_gemm needs at a.ypart when the split is taken.
+int bf3_k_slices(int fmt, int M, int Kp);
+size_t bf3_part_bytes(int fmt, int M, int N, int Kp);
 // Whether W4A16 at this shape is faster on t16f8 weights than on t16 weights.
 bool w4a16_prefers_t16f8(int M, int N, int num_cus);
 // weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 with groups of `group`

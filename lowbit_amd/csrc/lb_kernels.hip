@@ -988,7 +988,13 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   const int sbase = (int)((unsigned)S / gridDim.x), srem = S - sbase * (int)gridDim.x;
   const int bx = blockIdx.x;
   const int sb = bx * sbase + min(bx, srem), se = sb + sbase + (bx < srem ? 1 : 0);
-  const int nph = (G + kW8Waves - 1) / kW8Waves;
+  // K split over gridDim.z workgroups of a column: this one sums groups [g0, g1) and
+  // writes its partial tile to its slice of a.ypart (gridDim.z == 1: all groups, Y)
+  const int KS = gridDim.z, ks = blockIdx.z;
+  const int gsl = (G + KS - 1) / KS;
+  const int g0 = min(G, ks * gsl), g1 = min(G, g0 + gsl), GL = g1 - g0;
+  const int nph = (GL + kW8Waves - 1) / kW8Waves;
+  float *const yo = KS > 1 ? a.ypart + (size_t)ks * M * N : a.y;
 
   const Rsrc rx = make_rsrc(a.x3, (uint32_t)min(x3_bytes(M, Kp), (size_t)0xFFFFFFF0u));
   const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(F8 ? t16f8_qw_bytes(N, Kp) : t16_qw_bytes(N, Kp),
@@ -1002,8 +1008,8 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   v4u xa[4][3][TM];
   for (int cb = sb; cb < se; cb += NS) {
     const int ce = min(cb + NS, se);
-    if (wave >= G) {
-      // no group in any phase (Kp < 1024): this wave's partial tiles are zero
+    if (wave >= GL) {
+      // no group in any phase (fewer than eight groups): this wave's partial tiles are zero
       for (int j = 0; j < ce - cb; j++)
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -1011,8 +1017,8 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
               v4f{0.f, 0.f, 0.f, 0.f};
     }
     for (int ph = 0; ph < nph; ph++) {
-      const int g = ph * kW8Waves + wave;
-      if (g >= G) continue;  // wave-uniform: this wave has no group in the last phase
+      const int g = g0 + ph * kW8Waves + wave;
+      if (g >= g1) continue;  // wave-uniform: this wave has no group in the last phase
       // Each stage's address is one lane offset (shared by all stages) plus a
       // workgroup-uniform scalar offset: per-stage vector addresses would be
       // allocated to the registers of earlier stages' pending loads, which makes
@@ -1162,11 +1168,21 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
       if (n < N) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (m0 + lr + r < M) a.y[(size_t)(m0 + lr + r) * N + n] = v[r];
+          if (m0 + lr + r < M) yo[(size_t)(m0 + lr + r) * N + n] = v[r];
       }
     }
     __syncthreads();  // red is rewritten by the next chunk
   }
+}
+
+// y = the K slices' partial outputs added in slice order (deterministic).
+__global__ __launch_bounds__(256) void bf3_reduce_kernel(const float *__restrict__ part, int ks, size_t n,
+                                                         float *__restrict__ y) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float t = part[i];
+  for (int k = 1; k < ks; k++) t += part[(size_t)k * n + i];
+  y[i] = t;
 }
 
 // Largest chunk (its partial tiles fill NS * TM * 8 KiB of LDS) and weight subtiles
@@ -1186,16 +1202,22 @@ static void bf3_grid(int M, int N, int TM, int cus, int &gx, int &gy, int &spw) 
 }
 
 template <int F, int TM, bool F8>
-static void launch_bf3_t(const GemmArgs &a, int cus, hipStream_t s) {
+static void launch_bf3_t(const GemmArgs &a, int cus, int ks, hipStream_t s) {
   constexpr int NS = B3Cfg<TM>::NS, PF = B3Cfg<TM>::PF;
   // every subtile slot of a chunk but the last is computed, so the chunk length
   // is the workgroup's share (up to NS; its loads all in flight)
   int gx, gy, spw;
   bf3_grid(a.M, a.N, TM, cus, gx, gy, spw);
+  if (ks > 1) {
+    // a K split keeps one workgroup per CU: ks times fewer columns, each CU with
+    // ks times the subtiles over 1/ks of K (and of the activation terms)
+    gx = std::max(1, gx / ks);
+    spw = ((a.N + 15) / 16 + gx - 1) / gx;
+  }
   auto go = [&](auto ns) {
     constexpr int C = decltype(ns)::value < NS ? decltype(ns)::value : NS;
-    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF), F8>), dim3(gx, gy), dim3(kW8Threads),
-                       0, s, a);
+    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF), F8>), dim3(gx, gy, ks),
+                       dim3(kW8Threads), 0, s, a);
   };
   switch (spw) {
     case 1: go(std::integral_constant<int, 1>{}); break;
@@ -1221,9 +1243,30 @@ bool w4a16_prefers_t16f8(int M, int N, int num_cus) {
   return spw >= 4;
 }
 
+// K slices: each CU reads its rows' activation terms (6 bytes per element) for all
+// of K, ~1 MB at 16 x 11008, which bounds these shapes; a split reads 1/ks of them
+// per CU at the cost of a reduce launch (~1.6 us in a graph) and ks times the
+// subtiles per workgroup. Measured (hot): 16 x 4096 x 11008 W4A16 18.5 -> 16.4 us
+// (2), MXFP4 17.2 -> 14.2 us (4); 64 x 4096 x 11008 W4A16 36.7 -> 32.9 us (2), MXFP4
+// 29.2 -> 28.9 (2, not taken); at K = 4096 every split lost (13.8 -> 15.7 us at 16 x
+// 11008 x 4096), and with two row blocks more subtiles mean more chunks, each
+// reloading the activations.
+int bf3_k_slices(int fmt, int M, int Kp) {
+  if (Kp < 8192) return 1;
+  if (fmt == F_MXFP4) return M <= 16 ? 4 : 1;
+  return fmt == F_W4A16 ? 2 : 1;
+}
+
+size_t bf3_part_bytes(int fmt, int M, int N, int Kp) {
+  const int ks = bf3_k_slices(fmt, M, Kp);
+  return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+}
+
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, bool f8) {
   const int cus = num_cus > 0 ? num_cus : 256;
   if (!a.x3 || !a.wt16 || (f8 && fmt != F_W4A16)) return hipErrorInvalidValue;
+  // the split only where the caller gave room for its partial outputs
+  const int ks = a.ypart ? bf3_k_slices(fmt, a.M, a.Kp) : 1;
   // W4A16: 32-row blocks halve the weight decode per output once there are two
   // row blocks (its decode VALU, not bytes, bounds it). MXFP4 decodes with a few
   // conversion instructions, and each CU's bytes matter more: the activation terms
@@ -1242,16 +1285,22 @@ hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t 
     tall = cu_bytes(1) > 0.75 * cu_bytes(2);
   }
   if (fmt == F_W4A16 && f8) {
-    if (tall) launch_bf3_t<F_W4A16, 2, true>(a, cus, s);
-    else launch_bf3_t<F_W4A16, 1, true>(a, cus, s);
+    if (tall) launch_bf3_t<F_W4A16, 2, true>(a, cus, ks, s);
+    else launch_bf3_t<F_W4A16, 1, true>(a, cus, ks, s);
   } else if (fmt == F_W4A16) {
-    if (tall) launch_bf3_t<F_W4A16, 2, false>(a, cus, s);
-    else launch_bf3_t<F_W4A16, 1, false>(a, cus, s);
+    if (tall) launch_bf3_t<F_W4A16, 2, false>(a, cus, ks, s);
+    else launch_bf3_t<F_W4A16, 1, false>(a, cus, ks, s);
   } else if (fmt == F_MXFP4) {
-    if (tall) launch_bf3_t<F_MXFP4, 2, false>(a, cus, s);
-    else launch_bf3_t<F_MXFP4, 1, false>(a, cus, s);
+    if (tall) launch_bf3_t<F_MXFP4, 2, false>(a, cus, ks, s);
+    else launch_bf3_t<F_MXFP4, 1, false>(a, cus, ks, s);
   } else {
     return hipErrorInvalidValue;
+  }
+  if (ks > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t n = (size_t)a.M * a.N;
+    hipLaunchKernelGGL(bf3_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.ypart, ks, n, a.y);
   }
   return hipGetLastError();
 }

@@ -132,6 +132,7 @@ SIGNATURES = {
     "lbd_noalloc_scratch_bytes": ([], _sz),
     "lbd_gemm_w4a8_t16_noalloc": ([_vp, _int, _int, _vp, _vp, _vp, _int, _vp, _pp, _vp], _int),
     "lbd_bf16x3_workspace_bytes": ([_int, _int], _sz),
+    "lbd_bf16x3_workspace_bytes_split": ([_int, _int, _int, _int], _sz),
     "lbd_mxfp4_t16_bytes": ([_int, _int, C.POINTER(_sz), C.POINTER(_sz)], _int),
     "lbd_repack_mxfp4_t16": ([_vp, _vp, _int, _int, _vp, _vp, _vp], _int),
     "lbd_gemm_mxfp4_t16": ([_vp, _int, _int, _vp, _vp, _int, _vp, _pp, _vp, _sz, _vp], _int),
@@ -571,7 +572,7 @@ def _run_dev(kind: str, w, m: int, dx: int, dy: int, prm: _Params, stream) -> in
     zp = None if getattr(w, "zeros", None) is None else w.zeros.ptr
     mfma = _check(L.lbd_gemm_path(KIND_IDS[kind], m, w.kp, C.byref(prm)), "lbd_gemm_path", False) == ISA_GFX950_MFMA
     if kind in ("w4a16", "mxfp4") and mfma:
-        ws = _STAGE.buffer("ws", L.lbd_bf16x3_workspace_bytes(m, w.kp))
+        ws = _STAGE.buffer("ws", L.lbd_bf16x3_workspace_bytes_split(KIND_IDS[kind], m, w.n, w.kp))
         if kind == "w4a16":
             return gemm_w4a16_tiles(w, dx, m, dy, prm, ws.ptr, ws.nbytes, stream)
         qwt, et = w.tiles()

@@ -169,7 +169,8 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
                 d.tiles_f8()
             else:
                 d.tiles()
-        ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp) if fmt == "w4a8" else L.lbd_bf16x3_workspace_bytes(m, W.kp)
+        ws_bytes = (L.lbd_w4a8_workspace_bytes(m, W.kp) if fmt == "w4a8"
+                    else L.lbd_bf16x3_workspace_bytes_split(_KIND[fmt], m, n, W.kp))
     else:
         ws_bytes = L.lbd_w4a8_workspace_bytes(m, W.kp)
     ws = K.DeviceBuffer(ws_bytes)

@@ -150,6 +150,21 @@ def test_t16_sizes_and_argument_checks():
     assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6
 
 
+def test_bf16x3_split_workspace_sizes():
+    """The split workspace adds the slices' partial outputs only where K is split."""
+    L = K.lib()
+    base = L.lbd_bf16x3_workspace_bytes(16, 11008)
+    align = (base + 255) // 256 * 256
+    assert L.lbd_bf16x3_workspace_bytes_split(0, 16, 4096, 11008) == align + 2 * 16 * 4096 * 4
+    assert L.lbd_bf16x3_workspace_bytes_split(1, 16, 4096, 11008) == align + 4 * 16 * 4096 * 4
+    b64 = L.lbd_bf16x3_workspace_bytes(64, 11008)
+    assert L.lbd_bf16x3_workspace_bytes_split(1, 64, 4096, 11008) == (b64 + 255) // 256 * 256  # MXFP4, 64 rows: no split
+    b4 = L.lbd_bf16x3_workspace_bytes(16, 4096)
+    assert L.lbd_bf16x3_workspace_bytes_split(0, 16, 4096, 4096) == (b4 + 255) // 256 * 256
+    for args in ((2, 16, 64, 4096), (-1, 16, 64, 4096), (0, 0, 64, 4096), (0, 16, 0, 4096), (1, 16, 64, 0)):
+        assert L.lbd_bf16x3_workspace_bytes_split(*args) == 0
+
+
 def test_probe_argument_checks():
     """The measurement probes (lbd_probe_valu, lbd_empty_kernel, lbd_read_kernel,
     lbd_probe_grid_barrier) reject
