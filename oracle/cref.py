@@ -63,13 +63,18 @@ class RefParams(C.Structure):
     _fields_ = [(f, C.c_int) for f in ("isa", "mr", "nr", "nb", "kb", "order", "nthreads")]
 
 
+def ref_path() -> Path:
+    """Where the reference C library is looked for (LOWBIT_REF_LIB overrides)."""
+    return Path(os.environ.get("LOWBIT_REF_LIB", str(REF_SO)))
+
+
 @lru_cache(maxsize=1)
 def ref_lib() -> C.CDLL | None:
     """The reference C library, or None if oracle/_ref was never built."""
-    path = os.environ.get("LOWBIT_REF_LIB", str(REF_SO))
-    if not Path(path).exists():
+    path = ref_path()
+    if not path.exists():
         return None
-    so = C.CDLL(path)
+    so = C.CDLL(str(path))
     pp = C.POINTER(RefParams)
     sig = {
         "lb_version": ([], _int),

@@ -8,7 +8,7 @@
  *                                       src/lowbit/csrc/kern_scalar.c:49-59
  *   - float64 W4A16 / MXFP4 / W4A8 GEMMs src/lowbit/reference.py:9-34
  *   - the error-bound magnitudes        tests/conftest.py:22-27,
- *                                       tests/test_kernels.py:135-143
+ *                                       tests/test_kernels.py:108-116
  * Packed layouts: src/lowbit/csrc/lowbit.h:9-19.
  *
  * Build: oracle/Makefile (gcc -O2, no fast-math: the quantizer must round

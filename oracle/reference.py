@@ -145,7 +145,7 @@ def gemm_w4a8_ref(xq, xs, qw, scales, zeros, group: int = GROUP) -> np.ndarray:
 
 def w4a8_lane_bound(xq, xs, asum, qw, scales, zeros, group: int = GROUP) -> np.ndarray:
     """Magnitude the W4A8 fp32 rescale error is measured against: per group
-    sum_k q|a| + z|sum a|, times |s| and xs (tests/test_kernels.py:135-143).
+    sum_k q|a| + z|sum a|, times |s| and xs (tests/test_kernels.py:108-116).
     `asum` holds the activation sums per group of `group`."""
     xq = np.atleast_2d(np.asarray(xq, np.float64))
     q = unpack_codes(qw, group).astype(np.float64)

@@ -16,9 +16,26 @@ from lowbit_amd import formats as F
 from oracle import cref
 from oracle import reference as O
 
-GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_vectors.npz")
-REF = cref.ref_lib()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref (reference C library) not built")
+class _Gold:
+    """The golden vectors, opened on first use (collection alone loads nothing)."""
+    _npz = None
+
+    def _open(self):
+        if _Gold._npz is None:
+            _Gold._npz = np.load(Path(__file__).resolve().parent / "golden" / "ref_vectors.npz")
+        return _Gold._npz
+
+    def __getitem__(self, key):
+        return self._open()[key]
+
+    @property
+    def files(self):
+        return self._open().files
+
+
+GOLD = _Gold()
+# The reference's C library is mapped only inside the tests that call it.
+needs_ref = pytest.mark.skipif(not cref.ref_path().exists(), reason="oracle/_ref (reference C library) not built")
 
 
 # ------------------------------------------------------------------ brute force helpers
@@ -127,7 +144,7 @@ def test_quantizer_matches_reference_c(rng, shape):
     xp = F.pad_acts(x, kp)
     m = shape[0]
     rq, rs, ra = np.empty((m, kp), np.int8), np.empty(m, np.float32), np.empty((m, kp // 128), np.int32)
-    REF.lb_quant_act_int8(xp, m, kp, rq, rs, ra)
+    cref.ref_lib().lb_quant_act_int8(xp, m, kp, rq, rs, ra)
     for xq, xs, asum in (O.quant_act_int8(x), cref.c_quant_act_int8(xp)):
         np.testing.assert_array_equal(xq, rq)
         np.testing.assert_array_equal(xs, rs)
@@ -138,7 +155,7 @@ def test_quantizer_matches_reference_c(rng, shape):
 
 @pytest.mark.parametrize("tag", ["sym", "asym"])
 def test_group_acc_matches_golden_reference_vectors(tag):
-    zeros = GOLD.get(f"ga_{tag}_zeros") if f"ga_{tag}_zeros" in GOLD.files else None
+    zeros = GOLD[f"ga_{tag}_zeros"] if f"ga_{tag}_zeros" in GOLD.files else None
     got = O.w4a8_group_acc_ref(GOLD["q_xq"], GOLD[f"ga_{tag}_qw"], zeros)
     np.testing.assert_array_equal(got, GOLD[f"ga_{tag}_out"])
     np.testing.assert_array_equal(cref.c_group_acc(GOLD["q_xq"], GOLD[f"ga_{tag}_qw"], zeros), got)
@@ -171,7 +188,7 @@ def test_group_acc_matches_reference_c(rng, shape, asym):
     want = O.w4a8_group_acc_ref(xq, W.qw, W.zeros)
     for isa in (0, -1):  # reference scalar path and its best SIMD path
         out = np.empty((m, n, W.kp // 128), np.int32)
-        assert REF.lb_w4a8_group_acc(xq, asum, m, W.kp, W.qw, cref.zp(W.zeros), n, out, isa) >= 0
+        assert cref.ref_lib().lb_w4a8_group_acc(xq, asum, m, W.kp, W.qw, cref.zp(W.zeros), n, out, isa) >= 0
         np.testing.assert_array_equal(out, want)
     np.testing.assert_array_equal(cref.c_group_acc(xq, W.qw, W.zeros), want)
 
@@ -229,16 +246,16 @@ def test_gemms_match_reference_c(rng, shape):
         W = F.quantize_int4(w, asym=asym)
         xp = F.pad_acts(x, W.kp)
         y = np.empty((m, n), np.float32)
-        assert REF.lb_gemm_w4a16(xp, m, W.kp, W.qw, W.scales, cref.zp(W.zeros), n, y, C.byref(p)) >= 0
+        assert cref.ref_lib().lb_gemm_w4a16(xp, m, W.kp, W.qw, W.scales, cref.zp(W.zeros), n, y, C.byref(p)) >= 0
         O.assert_fp_close(y, O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros), _bound_int4(xp, W))
-        assert REF.lb_gemm_w4a8(xp, m, W.kp, W.qw, W.scales, cref.zp(W.zeros), n, y, C.byref(p)) >= 0
+        assert cref.ref_lib().lb_gemm_w4a8(xp, m, W.kp, W.qw, W.scales, cref.zp(W.zeros), n, y, C.byref(p)) >= 0
         xq, xs, asum = O.quant_act_int8(xp)
         _, bound = cref.c_gemm_w4a8(xq, xs, asum, W.qw, W.scales, W.zeros)
         O.assert_fp_close(y, O.gemm_w4a8_ref(xq, xs, W.qw, W.scales, W.zeros), bound)
     Wm = F.quantize_mxfp4(w)
     xp = F.pad_acts(x, Wm.kp)
     y = np.empty((m, n), np.float32)
-    assert REF.lb_gemm_mxfp4(xp, m, Wm.kp, Wm.qw, Wm.e8m0, n, y, C.byref(p)) >= 0
+    assert cref.ref_lib().lb_gemm_mxfp4(xp, m, Wm.kp, Wm.qw, Wm.e8m0, n, y, C.byref(p)) >= 0
     O.assert_fp_close(y, O.gemm_mxfp4_ref(xp, Wm.qw, Wm.e8m0), O.fp_bound(xp, O.dequant_mxfp4(Wm.qw, Wm.e8m0)))
 
 
