@@ -474,6 +474,13 @@ int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream);
 int lbd_probe_forms(void);
 /* a kernel of `workgroups` x 512 threads that does nothing: the fixed cost of a launch */
 int lbd_empty_kernel(int workgroups, void *stream);
+/* Check of the one-row W4A8 quantizer's token scale (no reference counterpart: the
+ * reference divides, src/lowbit/csrc/dispatch.c:231-257, and the paced GEMV replaces
+ * that division by 127 with a multiply and two fused multiply-adds): on this device,
+ * that replacement against the IEEE quotient a / 127.0f for every non-negative finite
+ * float32 and +inf. out is two device dwords: out[0] = how many differ, out[1] = the
+ * smallest differing bit pattern (0xFFFFFFFF when none). */
+int lbd_probe_div127(uint32_t *out, void *stream);
 /* Device-wide barrier probe (no reference counterpart; the measurement behind the
  * choice of one launch per decode phase over a persistent kernel): `rounds` (0 ..
  * 100000) barriers between `workgroups` (1 .. 1024) one-wave workgroups of one launch.

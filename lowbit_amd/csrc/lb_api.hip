@@ -1394,6 +1394,12 @@ int lbd_empty_kernel(int workgroups, void *stream) {
   if (e != hipSuccess) return fail_hip(e, "empty kernel launch");
   return ok(0);
 }
+int lbd_probe_div127(uint32_t *out, void *stream) {
+  if (!out || (reinterpret_cast<uintptr_t>(out) & 3)) return fail(LB_ERR_ARG, "div127 probe needs two device dwords");
+  hipError_t e = lbk::launch_div127_probe(out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "div127 probe launch");
+  return ok(0);
+}
 int lbd_probe_grid_barrier(int workgroups, int rounds, int mode, uint32_t *sync, size_t sync_bytes,
                            uint32_t *status, void *stream) {
   if (!sync || !status) return fail(LB_ERR_ARG, "barrier probe needs a sync buffer and a status word");

@@ -273,6 +273,19 @@ __device__ __forceinline__ float row_scale(float amax) {
   return amax > 0.0f ? amax / 127.0f : 1.0f;
 }
 
+// fl(a / 127) for a >= 0: one multiply and two fused multiply-adds instead of the IEEE
+// division sequence. q0 = fl(a * fl(1/127)), r = a - 127 q0 (exact), q0 + r fl(1/127)
+// rounded once; equal to the IEEE quotient for every finite float32 a >= 0. Host and
+// device compile the same code: tests/csrc/div127_exhaustive.hip checks every such a
+// on the CPU, lbd_probe_div127 on the GPU, both against a / 127.0f. +inf takes the
+// division.
+__host__ __device__ __forceinline__ float div127(float a) {
+  constexpr float kR = 1.0f / 127.0f;
+  const float q0 = a * kR;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kR, q0);
+  return a <= 3.4028234663852886e38f ? q1 : a / 127.0f;
+}
+
 // ---------------------------------------------------------------- argmax keys
 //
 // (value, index) as one unsigned 64-bit key whose unsigned order is numpy's

@@ -642,17 +642,6 @@ __device__ __forceinline__ uint32_t paced_byte(uint32_t word, uint32_t ci) {
   return (word >> (8 * (idx & 3u))) & 0xFFu;
 }
 
-// fl(a / 127) for a >= 0: one multiply and two fused multiply-adds instead of the IEEE
-// division sequence. q0 = fl(a * fl(1/127)), r = a - 127 q0 (exact), q0 + r fl(1/127)
-// rounded once; equal to the IEEE quotient for every finite float32 a >= 0 (checked
-// exhaustively against a / 127.0f on the host). +inf takes the division.
-__device__ __forceinline__ float div127(float a) {
-  constexpr float kR = 1.0f / 127.0f;
-  const float q0 = a * kR;
-  const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kR, q0);
-  return a <= 3.4028234663852886e38f ? q1 : a / 127.0f;
-}
-
 template <int F, int NIT, bool DW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   constexpr bool kInt8 = (F == F_W4A8 || F == F_W4A8Q || F == F_W4A8G32);

@@ -151,6 +151,9 @@ hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipS
 int valu_probe_forms();
 // a kernel that does nothing, workgroups of 512 threads
 hipError_t launch_empty(int workgroups, hipStream_t s);
+// div127 against a / 127.0f on every non-negative finite float32 and +inf: out[0] the
+// number that differ, out[1] the smallest differing bit pattern (0xFFFFFFFF: none)
+hipError_t launch_div127_probe(uint32_t *out, hipStream_t s);
 // Device-wide barrier probe (lb_probe.hip): `rounds` barriers between `workgroups`
 // (1 .. kBarrierMaxWorkgroups) one-wave workgroups, `mode` 0 (one atomic counter), 1
 // (a flag per workgroup) or 2 (flags with agent-scope release / acquire fences).

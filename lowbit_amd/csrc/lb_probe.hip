@@ -202,6 +202,43 @@ hipError_t launch_grid_barrier(int workgroups, int rounds, int mode, uint32_t *s
   return hipGetLastError();
 }
 
+// ---- the one-row W4A8 quantizer's division by 127 (div127, lb_device.h) on every
+//      non-negative finite float32 and +inf (bit patterns 0 .. 0x7F800000) against the
+//      IEEE quotient a / 127.0f, both as this device computes them. out[0] counts the
+//      patterns that differ, out[1] holds the smallest of them (0xFFFFFFFF: none); the
+//      init kernel sets both first. Every thread visits a fixed set of patterns
+//      (grid-stride, the largest index below 0x7F800000 + stride < 2^32).
+__global__ __launch_bounds__(64) void div127_init_kernel(uint32_t *out) {
+  if (threadIdx.x == 0) {
+    out[0] = 0u;
+    out[1] = 0xFFFFFFFFu;
+  }
+}
+
+__global__ __launch_bounds__(256) void div127_probe_kernel(uint32_t *out) {
+  const uint32_t stride = gridDim.x * 256u;
+  uint32_t bad = 0, first = 0xFFFFFFFFu;
+  for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u <= 0x7F800000u; u += stride) {
+    const float a = __uint_as_float(u);
+    if (__float_as_uint(div127(a)) != __float_as_uint(a / 127.0f)) {
+      bad++;
+      first = min(first, u);
+    }
+  }
+  if (bad) {
+    atomicAdd(out, bad);
+    atomicMin(out + 1, first);
+  }
+}
+
+hipError_t launch_div127_probe(uint32_t *out, hipStream_t s) {
+  hipLaunchKernelGGL(div127_init_kernel, dim3(1), dim3(64), 0, s, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(div127_probe_kernel, dim3(2048), dim3(256), 0, s, out);
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(512) void empty_kernel() {}
 
 hipError_t launch_empty(int workgroups, hipStream_t s) {

@@ -118,6 +118,7 @@ SIGNATURES = {
     "lbd_probe_valu": ([_int, _int, _int, _vp, _vp], _int),
     "lbd_probe_forms": ([], _int),
     "lbd_empty_kernel": ([_int, _vp], _int),
+    "lbd_probe_div127": ([_vp, _vp], _int),
     "lbd_probe_grid_barrier": ([_int, _int, _int, _vp, _sz, _vp, _vp], _int),
     "lbd_gemm_path": ([_int, _int, _int, _pp], _int),
     "lbd_gemm_plan": ([_int, _int, _int, _int, _pp, C.c_void_p], _int),
