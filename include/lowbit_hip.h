@@ -251,7 +251,9 @@ int lbd_repack_int4_t16f8(const uint8_t *qw, const float *scales,
                           float *st, void *stream);
 /* 1 when lbd_gemm_w4a16_t16f8 is expected to be faster than lbd_gemm_w4a16_t16 at
  * this shape on the current device (enough weight subtiles per workgroup to hide
- * the t16f8 layout's doubled weight bytes), else 0; or LB_ERR_SHAPE */
+ * the t16f8 layout's doubled weight bytes, counted for the launch with the K split a
+ * workspace of lbd_bf16x3_workspace_bytes_split bytes, or NULL, gives), else 0; or
+ * LB_ERR_SHAPE */
 int lbd_w4a16_prefers_t16f8(int M, int N, int Kp);
 /* y = x . w^T as lbd_gemm_w4a16_t16 (same workspace contract, same results bit for
  * bit) on t16f8 weights; always the matrix-core path */

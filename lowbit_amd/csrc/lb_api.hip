@@ -591,7 +591,7 @@ int lbd_w4a16_prefers_t16f8(int M, int N, int Kp) {
   int cus = 0;
   DevInfo di;
   if (device_info(&di) == 0) cus = di.cus;
-  return lbk::w4a16_prefers_t16f8(M, N, cus) ? 1 : 0;
+  return lbk::w4a16_prefers_t16f8(M, N, Kp, cus) ? 1 : 0;
 }
 
 int lbd_gemm_w4a16_t16f8(const float *x, int M, int Kp, const uint8_t *qwt8, const float *st, int N, float *y,

@@ -92,8 +92,9 @@ hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t 
 // partial outputs that launch_bf3_gemm needs at a.ypart when the split is taken.
 int bf3_k_slices(int fmt, int M, int Kp);
 size_t bf3_part_bytes(int fmt, int M, int N, int Kp);
-// Whether W4A16 at this shape is faster on t16f8 weights than on t16 weights.
-bool w4a16_prefers_t16f8(int M, int N, int num_cus);
+// Whether W4A16 at this shape is faster on t16f8 weights than on t16 weights (with
+// the K split the shape takes when the workspace has room for it).
+bool w4a16_prefers_t16f8(int M, int N, int Kp, int num_cus);
 // weight quantizers (lb_wquant.hip): fp32 [N, K] -> packed int4 with groups of `group`
 // (128 or 32; mode 0 absmax, 1 signed-max, 2 asym) or MXFP4
 hipError_t launch_quantize_int4(const float *w, int N, int K, int mode, int group, uint8_t *qw, float *scales,

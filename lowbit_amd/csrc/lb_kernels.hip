@@ -1232,14 +1232,20 @@ static void launch_bf3_t(const GemmArgs &a, int cus, int ks, hipStream_t s) {
   }
 }
 
-bool w4a16_prefers_t16f8(int M, int N, int num_cus) {
-  // Measured at 64 x 11008 x 4096 (6 subtiles per workgroup), 128 x 11008 x 4096 (11),
-  // 256 x 4096 x 4096 (8) and 512 x 4096 x 4096 (16), t16f8 took 3-11 % less time
-  // with the weights cold and 5-15 % less hot; with 2 or 3 subtiles per workgroup
-  // (16 and 32 x 11008 x 4096, 64 x 4096 x 11008) its twice as many weight bytes per
-  // stage cost more than the conversions it saves when cold (5-13 % more time).
+bool w4a16_prefers_t16f8(int M, int N, int Kp, int num_cus) {
+  // Subtiles per workgroup of the launch as it runs (after a K split). Measured at 64 x
+  // 11008 x 4096 (6 subtiles per workgroup), 128 x 11008 x 4096 (11), 256 x 4096 x 4096
+  // (8) and 512 x 4096 x 4096 (16), t16f8 took 3-11 % less time with the weights cold
+  // and 5-15 % less hot; with 2 or 3 subtiles per workgroup (16 and 32 x 11008 x 4096,
+  // and at K = 11008 16 and 32 rows split in two) its twice as many weight bytes per
+  // stage cost more than the conversions it saves when cold (5-13 % more time). At 64
+  // x 4096 x 11008 split in two (4 subtiles) t16f8 took 27.2 against 30.2 us hot, 32.1
+  // against 32.3 cold; 128 x 4096 x 11008 unsplit (4), 43.3 against 49.6 hot.
   int gx, gy, spw;
-  bf3_grid(M, N, M > 16 ? 2 : 1, num_cus > 0 ? num_cus : 256, gx, gy, spw);
+  const int cus = num_cus > 0 ? num_cus : 256;
+  bf3_grid(M, N, M > 16 ? 2 : 1, cus, gx, gy, spw);
+  const int ks = bf3_k_slices(F_W4A16, M, Kp);
+  if (ks > 1) spw = ((N + 15) / 16 + std::max(1, gx / ks) - 1) / std::max(1, gx / ks);
   return spw >= 4;
 }
 
@@ -1250,11 +1256,14 @@ bool w4a16_prefers_t16f8(int M, int N, int num_cus) {
 // (2), MXFP4 17.2 -> 14.2 us (4); 64 x 4096 x 11008 W4A16 36.7 -> 32.9 us (2), MXFP4
 // 29.2 -> 28.9 (2, not taken); at K = 4096 every split lost (13.8 -> 15.7 us at 16 x
 // 11008 x 4096), and with two row blocks more subtiles mean more chunks, each
-// reloading the activations.
+// reloading the activations. W4A16 above 64 rows is not split: at 128 x 4096 x 11008
+// the split took 65.9 against 49.6 us hot on t16 (57.8 against 43.3 on t16f8); 256
+// rows gained 8 % (94.8 against 102.8 on t16f8), too little for a partial-output
+// workspace that grows with M (ks M N 4 bytes, 256 MiB at 8192 x 4096 x 11008).
 int bf3_k_slices(int fmt, int M, int Kp) {
   if (Kp < 8192) return 1;
   if (fmt == F_MXFP4) return M <= 16 ? 4 : 1;
-  return fmt == F_W4A16 ? 2 : 1;
+  return fmt == F_W4A16 && M <= 64 ? 2 : 1;
 }
 
 size_t bf3_part_bytes(int fmt, int M, int N, int Kp) {

@@ -255,7 +255,13 @@ class Model:
         self.gu, self.m = _buf(T * 2 * I * 4), _buf(T * I * 4)
         self.logits = _buf(cfg.vocab_size * 4)
         kmax = max(h, I, cfg.num_heads * D)
-        self.ws = _buf(max(self.L.lbd_w4a8_workspace_bytes(T, kmax), self.L.lbd_bf16x3_workspace_bytes(T, kmax)))
+        # room for the K split of the bf16x3 prefill GEMMs (rows of 8192+ elements), so
+        # the model's matrix-core GEMMs are the launches lb.gemm_* and bench.py time
+        kind = 1 if self.backend == "mxfp4" else 0
+        lin = [w for ly in self.layers for w in (ly.qkv, ly.o, ly.gate_up, ly.down)] + [self.lm_head]
+        split = max(self.L.lbd_bf16x3_workspace_bytes_split(kind, T, w.n, w.kp) for w in lin)
+        self.ws = _buf(max(self.L.lbd_w4a8_workspace_bytes(T, kmax), self.L.lbd_bf16x3_workspace_bytes(T, kmax),
+                           split))
 
     @property
     def linear_weight_bytes(self) -> int:

@@ -144,7 +144,9 @@ def test_t16_sizes_and_argument_checks():
     assert L.lbd_gemm_w4a16_t16f8(None, 1, 0, None, None, 16, None, C.byref(prm), None, 0, None) == -1
     # without a device the rule assumes 256 compute units
     assert L.lbd_w4a16_prefers_t16f8(64, 11008, 4096) == 1 and L.lbd_w4a16_prefers_t16f8(16, 11008, 4096) == 0
-    assert L.lbd_w4a16_prefers_t16f8(64, 4096, 11008) == 0 and L.lbd_w4a16_prefers_t16f8(0, 16, 128) == -1
+    # at K = 11008 the split launch counts: 64 rows split in two give 4 subtiles per workgroup
+    assert L.lbd_w4a16_prefers_t16f8(64, 4096, 11008) == 1 and L.lbd_w4a16_prefers_t16f8(0, 16, 128) == -1
+    assert L.lbd_w4a16_prefers_t16f8(16, 4096, 11008) == 0 and L.lbd_w4a16_prefers_t16f8(32, 4096, 11008) == 0
     assert L.lbd_gemm_path(2, 1, 4096, C.byref(prm)) == K.ISA_GFX950
     assert L.lbd_gemm_path(2, 64, 4096, C.byref(prm)) == K.ISA_GFX950_MFMA
     assert L.lbd_gemm_path(7, 1, 4096, C.byref(prm)) == -6

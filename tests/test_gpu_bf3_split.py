@@ -17,30 +17,34 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(fmt, D, x, m, split, f8=False):
+    """split True: a workspace of lbd_bf16x3_workspace_bytes_split bytes; False: of
+    lbd_bf16x3_workspace_bytes; None: no workspace (the library's per-thread buffer)."""
     L = K.lib()
     dx = K.DeviceBuffer.from_array(x)
     dy = K.DeviceBuffer(m * D.n * 4)
     kind = 0 if fmt == "w4a16" else 1
     nb = L.lbd_bf16x3_workspace_bytes_split(kind, m, D.n, D.kp) if split else L.lbd_bf16x3_workspace_bytes(m, D.kp)
-    ws = K.DeviceBuffer(nb)
+    ws = K.DeviceBuffer(nb) if split is not None else None
+    wp, nb = (ws.ptr, nb) if ws is not None else (None, 0)
     prm = K._Params(-1, 0, 0, 0, 0, 0, 0)
     if fmt == "mxfp4":
         qwt, et = D.tiles()
-        rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, D.kp, qwt.ptr, et.ptr, D.n, dy.ptr, C.byref(prm), ws.ptr, nb, None)
+        rc = L.lbd_gemm_mxfp4_t16(dx.ptr, m, D.kp, qwt.ptr, et.ptr, D.n, dy.ptr, C.byref(prm), wp, nb, None)
     elif f8:
         qwt8, st8 = D.tiles_f8()
-        rc = L.lbd_gemm_w4a16_t16f8(dx.ptr, m, D.kp, qwt8.ptr, st8.ptr, D.n, dy.ptr, C.byref(prm), ws.ptr, nb, None)
+        rc = L.lbd_gemm_w4a16_t16f8(dx.ptr, m, D.kp, qwt8.ptr, st8.ptr, D.n, dy.ptr, C.byref(prm), wp, nb, None)
     else:
         qwt, st, zt = D.tiles()
         rc = L.lbd_gemm_w4a16_t16(dx.ptr, m, D.kp, qwt.ptr, st.ptr, None if zt is None else zt.ptr, D.n, dy.ptr,
-                                  C.byref(prm), ws.ptr, nb, None)
+                                  C.byref(prm), wp, nb, None)
     assert rc == K.ISA_GFX950_MFMA
     assert L.lb_dev_synchronize() == 0
     return dy.to_array((m, D.n), np.float32)
 
 
 @pytest.mark.parametrize("fmt", ["w4a16", "mxfp4"])
-@pytest.mark.parametrize("m,n,k", [(16, 520, 11008), (64, 300, 11008), (5, 77, 8200), (16, 96, 16384)])
+@pytest.mark.parametrize("m,n,k", [(16, 520, 11008), (64, 300, 11008), (5, 77, 8200), (16, 96, 16384),
+                                   (128, 200, 11008)])
 @pytest.mark.parametrize("asym", [False, True])
 def test_split_within_bound(rng, fmt, m, n, k, asym):
     if fmt == "mxfp4" and asym:
@@ -58,6 +62,9 @@ def test_split_within_bound(rng, fmt, m, n, k, asym):
     O.assert_fp_close(yu, ref, bound, 1e-5)
     if fmt == "w4a16" and D.f8_exact():
         np.testing.assert_array_equal(_run(fmt, D, xp, m, True, f8=True), ys)
+    # no workspace: the per-thread buffer has room for the partial outputs, so the
+    # call takes the split, bit for bit the result with a split-sized workspace
+    np.testing.assert_array_equal(_run(fmt, D, xp, m, None), ys)
     # the Python call takes the split (its staging workspace has room for it)
     y = K.gemm_mxfp4(x, D) if fmt == "mxfp4" else K.gemm_w4a16(x, D)
     np.testing.assert_array_equal(y, ys)

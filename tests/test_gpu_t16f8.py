@@ -199,10 +199,13 @@ def test_threads_share_one_t16f8_repack(rng):
 
 @pytest.mark.parametrize("m,n,k,want", [(64, 11008, 4096, True), (128, 11008, 4096, True), (256, 4096, 4096, True),
                                         (512, 4096, 4096, True), (16, 11008, 4096, False),
-                                        (32, 11008, 4096, False), (64, 4096, 11008, False)])
+                                        (32, 11008, 4096, False), (16, 4096, 11008, False),
+                                        (32, 4096, 11008, False), (64, 4096, 11008, True),
+                                        (128, 4096, 11008, True)])
 def test_w4a16_layout_choice_at_measured_shapes(m, n, k, want):
     """The shapes whose timings set the rule (256 compute units): t16f8 where each
-    workgroup has 4 or more weight subtiles, t16 below."""
+    workgroup of the launch as it runs (K split in two at K = 11008 up to 64 rows) has
+    4 or more weight subtiles, t16 below."""
     if K.device_info()["compute_units"] != 256:
         pytest.skip("the measured rule is stated for 256 compute units")
     assert K.lib().lbd_w4a16_prefers_t16f8(m, n, k) == int(want)
