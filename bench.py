@@ -408,6 +408,27 @@ def call_time(dev: Dev, fmt: str, W, x: np.ndarray, pool, layout: str, n_calls: 
     return round(float(np.median(ts)) * 1e6, 2)
 
 
+def call_time_host(dev: Dev, fmt: str, W, x: np.ndarray, n_calls: int, implicit: bool) -> float:
+    """Median wall time (us) of lowbit_amd.gemm_<fmt>(x, W) on the host container W, the
+    call the reference's linear layers make (src/lowbit/model.py:139-141): with implicit
+    residency (the container's device copy, made on its first call, reused), or through
+    the host-pointer ABI (lb_gemm_*: the weights cross PCIe on every call, as a binary
+    drop-in of the reference's library behaves)."""
+    K = dev.K
+    fn = K.GEMMS[fmt]
+    with K.implicit_residency(implicit):
+        i, t_end = 0, time.perf_counter() + 0.3
+        while i < 3 or time.perf_counter() < t_end:
+            fn(x, W)
+            i += 1
+        ts = []
+        for _ in range(n_calls):
+            t0 = time.perf_counter()
+            fn(x, W)
+            ts.append(time.perf_counter() - t0)
+    return round(float(np.median(ts)) * 1e6, 2)
+
+
 def rel_err(fmt: str, W, x, y) -> float:
     """max|y - ref| / max|ref| against the float64 C oracle (the reference's bench check)."""
     from lowbit_amd import formats as F
@@ -719,10 +740,14 @@ def main() -> int:
         r = measure(dev, fmt, DECODE, W, x, cold=True, steps=args.steps, warmup=args.warmup, graph=graph)
         r["max_rel_err"] = float(f"{rel_err(fmt, W, x, r.pop('y')):.3g}")
         r["hbm_frac"] = round(r["weight_gbps"] / HBM_PEAK_GBS, 4)
+        # the same call on the host container: implicit residency, and the pointer ABI
+        r["call_us_host_container"] = call_time_host(dev, fmt, W, x, 200, implicit=True)
+        r["call_us_pointer_abi"] = call_time_host(dev, fmt, W, x, 20, implicit=False)
         results[f"{fmt}_decode"] = r
         log(f"{fmt:6s} M=1 cold: {r['us_per_call']:8.2f} us  {r['weight_gbps']:7.1f} GB/s "
             f"({100 * r['hbm_frac']:.1f}% HBM)  path {r['path']}  rel err {r['max_rel_err']}  "
-            f"call through ctypes {r['call_us']:.1f} us  ({r['timed_launches']} launches, "
+            f"call through ctypes {r['call_us']:.1f} us (host container {r['call_us_host_container']:.1f}, "
+            f"pointer ABI {r['call_us_pointer_abi']:.0f})  ({r['timed_launches']} launches, "
             f"{r['bytes_rotated'] >> 20} MiB rotated)")
 
     # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167);
@@ -804,6 +829,8 @@ def main() -> int:
         "timed_launches": head["timed_launches"],
         "bytes_rotated": head["bytes_rotated"],
         "call_us": head["call_us"],
+        "call_us_host_container": head["call_us_host_container"],
+        "call_us_pointer_abi": head["call_us_pointer_abi"],
         "cpu_baseline": cpu,
         "per_format": {kk: {f: v for f, v in vv.items() if f not in ("N", "K")} for kk, vv in results.items()},
         "decoder": decoder,

@@ -158,7 +158,9 @@ int lbd_w4a8_group_acc(const int8_t *xq, const int32_t *asum, int M, int Kp,
 
 /* regime (LB_ISA_GFX950 or LB_ISA_GFX950_MFMA) an lbd_gemm_* of kind 0 = W4A16,
  * 1 = MXFP4, 2 = W4A8 with this shape and lb_params runs in (no reference
- * counterpart; the reference's effective ISA does not depend on the shape) */
+ * counterpart; the reference's effective ISA does not depend on the shape), or the
+ * error such a call would return for its shape or lb_params (LB_ERR_SHAPE, or
+ * LB_ERR_TILE for a micro-tile the reference does not compile) */
 int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p);
 /* The regime and, on the small-M (VALU) path, the kernel configuration an lbd_gemm_*
  * of kind 0 = W4A16, 1 = MXFP4, 2 = W4A8 with this shape takes on the current device

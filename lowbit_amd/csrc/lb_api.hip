@@ -286,6 +286,13 @@ int check_t16(int M, int Kp, int N, bool f8 = false) {
   return 0;
 }
 
+// Whether a host-pointer call can take the t16 matrix-core route (the limits check_t16
+// enforces, tested without recording an error).
+bool host_t16_fits(int M, int Kp, int N) {
+  return (size_t)M * Kp * 4 <= 0xFFFFFFF0u && lbk::x3_bytes(M, Kp) <= 0xFFFFFFF0u &&
+         lbk::t16_qw_bytes(N, Kp) <= 0xFFFFFFF0u;
+}
+
 // fp32 activations in; quantized inside (fused into the GEMV, or a quantizer
 // kernel into `ws` before the MFMA kernel).
 int run_w4a8(const lbk::GemmArgs &a, const lb_params *p, char *ws, hipStream_t s) {
@@ -454,6 +461,8 @@ int lbd_gemm_path(int kind, int M, int Kp, const lb_params *p) {
   static const int fmts[] = {lbk::F_W4A16, lbk::F_MXFP4, lbk::F_W4A8};
   if (kind < 0 || kind > 2) return fail(LB_ERR_ARG, "unknown GEMM kind");
   if (M <= 0 || Kp <= 0) return fail(LB_ERR_SHAPE, "bad shape");
+  const int rc = check_params(p, M);
+  if (rc < 0) return rc;
   return ok(choose_path(fmts[kind], M, Kp, p));
 }
 
@@ -1034,8 +1043,16 @@ int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float 
   const int G = Kp / LB_GROUP;
   const size_t bx = (size_t)M * Kp * 4, bq = (size_t)N * Kp / 2, bs = (size_t)N * G * 4,
                bz = zeros ? (size_t)N * G : 0, by = (size_t)M * N * 4;
+  // the matrix-core regime runs the bf16x3 GEMM on a t16 copy repacked on the device
+  // in the call (as a resident handle's first matrix-core GEMM does), with room for
+  // the K split; shapes past the t16 limits keep the fp32 MFMA kernel
+  const bool t16 = choose_path(lbk::F_W4A16, M, Kp, p) == LB_ISA_GFX950_MFMA && host_t16_fits(M, Kp, N);
+  const size_t bqt = t16 ? lbk::t16_qw_bytes(N, Kp) : 0, bst = t16 ? lbk::t16_group_entries(N, Kp) * 4 : 0,
+               bzt = t16 && zeros ? lbk::t16_group_entries(N, Kp) : 0,
+               bw = t16 ? lbd_bf16x3_workspace_bytes_split(0, M, N, Kp) : 0;
   Arena ar;
   const size_t ox = ar.take(bx), oq = ar.take(bq), os = ar.take(bs), oz = ar.take(bz), oy = ar.take(by);
+  const size_t oqt = ar.take(bqt), ost = ar.take(bst), ozt = ar.take(bzt), ow = ar.take(bw);
   if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
   char *b = c->buf;
   hipStream_t s = c->stream;
@@ -1043,9 +1060,19 @@ int lb_gemm_w4a16(const float *x, int M, int Kp, const uint8_t *qw, const float 
   LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
   LB_HIP(hipMemcpyAsync(b + os, scales, bs, hipMemcpyHostToDevice, s), "copy scales");
   if (zeros) LB_HIP(hipMemcpyAsync(b + oz, zeros, bz, hipMemcpyHostToDevice, s), "copy zeros");
-  rc = lbd_gemm_w4a16(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
-                      reinterpret_cast<float *>(b + os), zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr, N,
-                      reinterpret_cast<float *>(b + oy), p, s);
+  const auto *dq = reinterpret_cast<uint8_t *>(b + oq);
+  const auto *ds = reinterpret_cast<float *>(b + os);
+  const auto *dz = zeros ? reinterpret_cast<uint8_t *>(b + oz) : nullptr;
+  if (t16) {
+    auto *qt = reinterpret_cast<uint8_t *>(b + oqt), *zt = zeros ? reinterpret_cast<uint8_t *>(b + ozt) : nullptr;
+    auto *st = reinterpret_cast<float *>(b + ost);
+    if ((rc = lbd_repack_int4_t16(dq, ds, dz, N, Kp, qt, st, zt, s)) < 0) return rc;
+    rc = lbd_gemm_w4a16_t16(reinterpret_cast<float *>(b + ox), M, Kp, qt, st, zt, N,
+                            reinterpret_cast<float *>(b + oy), p, b + ow, bw, s);
+  } else {
+    rc = lbd_gemm_w4a16(reinterpret_cast<float *>(b + ox), M, Kp, dq, ds, dz, N, reinterpret_cast<float *>(b + oy),
+                        p, s);
+  }
   if (rc < 0) return rc;
   LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
   LB_HIP(hipStreamSynchronize(s), "synchronize");
@@ -1062,16 +1089,28 @@ int lb_gemm_mxfp4(const float *x, int M, int Kp, const uint8_t *qw, const uint8_
   if ((rc = get_ctx(&c)) < 0) return rc;
   const size_t bx = (size_t)M * Kp * 4, bq = (size_t)N * Kp / 2, be = (size_t)N * (Kp / LB_MXBLOCK),
                by = (size_t)M * N * 4;
+  // as lb_gemm_w4a16: the matrix-core regime repacks to t16 and runs bf16x3
+  const bool t16 = choose_path(lbk::F_MXFP4, M, Kp, p) == LB_ISA_GFX950_MFMA && host_t16_fits(M, Kp, N);
+  const size_t bqt = t16 ? lbk::t16_qw_bytes(N, Kp) : 0, bet = t16 ? lbk::t16_e8m0_bytes(N, Kp) : 0,
+               bw = t16 ? lbd_bf16x3_workspace_bytes_split(1, M, N, Kp) : 0;
   Arena ar;
   const size_t ox = ar.take(bx), oq = ar.take(bq), oe = ar.take(be), oy = ar.take(by);
+  const size_t oqt = ar.take(bqt), oet = ar.take(bet), ow = ar.take(bw);
   if ((rc = grow(&c->buf, &c->cap, ar.off, c->stream)) < 0) return rc;
   char *b = c->buf;
   hipStream_t s = c->stream;
   LB_HIP(hipMemcpyAsync(b + ox, x, bx, hipMemcpyHostToDevice, s), "copy x");
   LB_HIP(hipMemcpyAsync(b + oq, qw, bq, hipMemcpyHostToDevice, s), "copy qw");
   LB_HIP(hipMemcpyAsync(b + oe, e8m0, be, hipMemcpyHostToDevice, s), "copy e8m0");
-  rc = lbd_gemm_mxfp4(reinterpret_cast<float *>(b + ox), M, Kp, reinterpret_cast<uint8_t *>(b + oq),
-                      reinterpret_cast<uint8_t *>(b + oe), N, reinterpret_cast<float *>(b + oy), p, s);
+  const auto *dq = reinterpret_cast<uint8_t *>(b + oq), *de = reinterpret_cast<uint8_t *>(b + oe);
+  if (t16) {
+    auto *qt = reinterpret_cast<uint8_t *>(b + oqt), *et = reinterpret_cast<uint8_t *>(b + oet);
+    if ((rc = lbd_repack_mxfp4_t16(dq, de, N, Kp, qt, et, s)) < 0) return rc;
+    rc = lbd_gemm_mxfp4_t16(reinterpret_cast<float *>(b + ox), M, Kp, qt, et, N, reinterpret_cast<float *>(b + oy),
+                            p, b + ow, bw, s);
+  } else {
+    rc = lbd_gemm_mxfp4(reinterpret_cast<float *>(b + ox), M, Kp, dq, de, N, reinterpret_cast<float *>(b + oy), p, s);
+  }
   if (rc < 0) return rc;
   LB_HIP(hipMemcpyAsync(y, b + oy, by, hipMemcpyDeviceToHost, s), "copy y");
   LB_HIP(hipStreamSynchronize(s), "synchronize");

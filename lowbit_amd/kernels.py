@@ -9,15 +9,27 @@ all forced by the device:
     "avx512") and "auto"/None mean "choose by shape"; there are no CPU tiers.
   * `threads` is accepted and ignored; `Params` tile fields are validated like
     the reference (an uncompiled (mr, nr) raises) and otherwise ignored.
-  * Weights passed as Int4Weights / MXFP4Weights are uploaded on every call
-    (the pointer ABI keeps no state). `to_device(w)` uploads once and returns a
-    resident handle that every gemm_* accepts in place of the host container.
+  * Weights passed as Int4Weights / MXFP4Weights are uploaded once, on their
+    first GEMM, and the device copy is reused while the container holds the same
+    arrays (implicit residency). To keep that copy exact, the first GEMM marks
+    the container's arrays read-only: an in-place edit then raises instead of
+    going unseen, and a caller that means to edit sets `flags.writeable = True`
+    (the next GEMM sees that and uploads again) or calls `release(w)`. A view
+    taken before the first GEMM stays writeable and is not watched. With
+    LOWBIT_RESIDENT=0, or inside `implicit_residency(False)`, every call goes
+    through the pointer ABI (lb_gemm_*), which uploads the weights per call as the
+    reference's C library reads them per call. `to_device(w)` uploads explicitly
+    and returns a resident handle that every gemm_* accepts in place of the host
+    container.
 The library is never compiled here; a missing build raises RuntimeError.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
+import os
 import threading
+import weakref
 from dataclasses import asdict, dataclass
 from functools import lru_cache
 
@@ -517,6 +529,106 @@ def quantize_mxfp4_device(w, shape=None, stream=None) -> "DeviceMXFP4Weights":
     return DeviceMXFP4Weights(qw, e, n, kp, k, n * kp // 2 + n * kp // MXBLOCK)
 
 
+# ------------------------------------------------------------------ implicit residency
+
+class _ResidencyState(threading.local):
+    def __init__(self):
+        self.enabled = os.environ.get("LOWBIT_RESIDENT", "1") != "0"
+
+
+_RES_STATE = _ResidencyState()
+_RES_LOCK = threading.RLock()  # re-entrant: a weakref callback may run inside the lock
+# id(container) -> (weak reference to it, array key, device copy, arrays this package froze)
+_RES: dict[int, tuple] = {}
+RESIDENT_UPLOADS = [0]  # device copies made for host containers (a counter for tests and bench)
+
+
+@contextlib.contextmanager
+def implicit_residency(enabled: bool):
+    """Within the block, gemm_* on host containers use (True) or bypass (False, the
+    pointer ABI: weights uploaded per call) the cached device copy, on this thread."""
+    prev = _RES_STATE.enabled
+    _RES_STATE.enabled = bool(enabled)
+    try:
+        yield
+    finally:
+        _RES_STATE.enabled = prev
+
+
+def _host_arrays(w) -> tuple:
+    return (w.qw, w.scales, w.zeros) if isinstance(w, Int4Weights) else (w.qw, w.e8m0)
+
+
+def _array_key(w) -> tuple:
+    """What identifies the arrays a device copy was made from: each array object, its
+    data pointer, shape and dtype (a replaced or reshaped array changes the key), and
+    the container's logical K and group size."""
+    key = tuple((id(a), a.ctypes.data, a.shape, a.dtype.str) if a is not None else None for a in _host_arrays(w))
+    return key + (w.k, getattr(w, "group", None))
+
+
+def _forget(wid: int):
+    with _RES_LOCK:
+        _RES.pop(wid, None)
+
+
+def resident(w):
+    """The device copy gemm_* uses for the host container `w` (Int4Weights or
+    MXFP4Weights): made on first use, reused while the container holds the same arrays
+    and those stay read-only, made again otherwise. Device handles pass through."""
+    if isinstance(w, (DeviceInt4Weights, DeviceMXFP4Weights)):
+        return w
+    if not isinstance(w, (Int4Weights, MXFP4Weights)):
+        raise TypeError(f"cannot make {type(w).__name__} resident")
+    arrays = [a for a in _host_arrays(w) if a is not None]
+    key = _array_key(w)
+    with _RES_LOCK:
+        ent = _RES.get(id(w))
+        if ent is not None and ent[0]() is w and ent[1] == key and not any(a.flags.writeable for a in arrays):
+            return ent[2]
+        # freeze first, then copy: an edit can no longer land between the upload and
+        # the next call without the caller making an array writeable again
+        froze = [a for a in arrays if a.flags.writeable]
+        if ent is not None and ent[0]() is w:
+            froze = list({id(a): a for a in list(ent[3]) + froze}.values())
+        for a in arrays:
+            a.flags.writeable = False
+        d = to_device(w)
+        RESIDENT_UPLOADS[0] += 1
+        wid = id(w)
+        _RES[wid] = (weakref.ref(w, lambda _r, wid=wid: _forget(wid)), key, d, froze)
+        return d
+
+
+def release(w) -> bool:
+    """Drop the device copy of host container `w` (freed when no call still uses it)
+    and make writeable again the arrays the first GEMM made read-only. True if there
+    was a copy."""
+    with _RES_LOCK:
+        ent = _RES.get(id(w))
+        if ent is None or ent[0]() is not w:
+            return False
+        del _RES[id(w)]
+    for a in ent[3]:
+        try:
+            a.flags.writeable = True
+        except ValueError:  # a view whose base is read-only
+            pass
+    return True
+
+
+def _use_resident(w, kind: str, m: int, prm: _Params) -> bool:
+    """Whether this call takes the resident copy of a host container. The arguments
+    are checked first, as the pointer ABI checks them before it reads any weights:
+    a bad shape or micro-tile raises ValueError without an upload."""
+    if not (_RES_STATE.enabled and isinstance(w, (Int4Weights, MXFP4Weights))):
+        return False
+    if w.n <= 0:
+        raise ValueError(f"lbd_gemm_{kind} failed (rc=-1): bad shape (M, N, Kp <= 0 or Kp % block)")
+    _check(lib().lbd_gemm_path(KIND_IDS[kind], m, w.kp, C.byref(prm)), f"lbd_gemm_{kind}", False)
+    return True
+
+
 class _Staging(threading.local):
     """Per-thread device staging for calls on resident weights: a stream and device
     buffers for X, Y and the matrix-core workspace, grown on demand and reused by
@@ -607,6 +719,27 @@ def _dev_gemm(kind: str, pr: _Prepared, w, prm: _Params) -> np.ndarray:
     return pr.y
 
 
+def _dev_gemm_q(a: Int8Acts, w, prm: _Params, y: np.ndarray) -> np.ndarray:
+    """gemm_w4a8_q on resident weights: codes, token scales and group sums up, the GEMM
+    (lbd_gemm_w4a8_q), Y down, on the calling thread's stream."""
+    L = lib()
+    m = a.xq.shape[0]
+    xq = np.ascontiguousarray(a.xq, np.int8)
+    xs = np.ascontiguousarray(a.scale, np.float32)
+    gs = np.ascontiguousarray(a.gsum, np.int32)
+    s = _STAGE.get_stream()
+    dq, ds, dg = _STAGE.buffer("xq", xq.nbytes), _STAGE.buffer("xs", xs.nbytes), _STAGE.buffer("gs", gs.nbytes)
+    dy = _STAGE.buffer("y", y.nbytes)
+    for d, h in ((dq, xq), (ds, xs), (dg, gs)):
+        _check(L.lb_memcpy_h2d_async(d.ptr, h.ctypes.data, h.nbytes, s), "lb_memcpy_h2d_async", False)
+    _check(L.lbd_gemm_w4a8_q(dq.ptr, ds.ptr, dg.ptr, m, w.kp, w.qw.ptr, w.scales.ptr,
+                             None if w.zeros is None else w.zeros.ptr, w.n, dy.ptr, C.byref(prm), s),
+           "lbd_gemm_w4a8_q")
+    _check(L.lb_memcpy_d2h_async(y.ctypes.data, dy.ptr, y.nbytes, s), "lb_memcpy_d2h_async", False)
+    _check(L.lb_stream_synchronize(s), "lb_stream_synchronize", False)
+    return y
+
+
 def _g32_gemm(kind: str, pr: _Prepared, w) -> np.ndarray:
     """Group-32 int4 GEMMs (lbd_gemm_w4a16_g32 / lbd_gemm_w4a8_g32): host containers
     are uploaded for the call, device handles used in place."""
@@ -636,6 +769,8 @@ def gemm_w4a16(x, w, params: Params | None = None, isa=None, threads: int | None
     """Y = X @ dequant(W)^T, fp32 activations and accumulation (src/lowbit/kernels.py:149-156)."""
     pr = _prep or _Prepared(x, w.kp, w.n)
     prm = _params(params, isa, threads, "w4a16", (pr.x.shape[0], w.n, w.k))
+    if _use_resident(w, "w4a16", pr.x.shape[0], prm):
+        w = resident(w)
     if _int4_group(w) != GROUP:
         return _g32_gemm("w4a16", pr, w)
     if isinstance(w, DeviceInt4Weights):
@@ -651,6 +786,8 @@ def gemm_mxfp4(x, w, params: Params | None = None, isa=None, threads: int | None
     """Y = X @ dequant(W)^T for OCP MXFP4 weights (src/lowbit/kernels.py:159-166)."""
     pr = _prep or _Prepared(x, w.kp, w.n)
     prm = _params(params, isa, threads, "mxfp4", (pr.x.shape[0], w.n, w.k))
+    if _use_resident(w, "mxfp4", pr.x.shape[0], prm):
+        w = resident(w)
     if isinstance(w, DeviceMXFP4Weights):
         return _dev_gemm("mxfp4", pr, w, prm)
     rc = lib().lb_gemm_mxfp4(pr.x, pr.x.shape[0], w.kp, w.qw, w.e8m0, w.n, pr.y, C.byref(prm))
@@ -664,6 +801,8 @@ def gemm_w4a8(x, w, params: Params | None = None, isa=None, threads: int | None 
     (src/lowbit/kernels.py:169-177)."""
     pr = _prep or _Prepared(x, w.kp, w.n)
     prm = _params(params, isa, threads, "w4a8", (pr.x.shape[0], w.n, w.k))
+    if _use_resident(w, "w4a8", pr.x.shape[0], prm):
+        w = resident(w)
     if _int4_group(w) != GROUP:
         return _g32_gemm("w4a8", pr, w)
     if isinstance(w, DeviceInt4Weights):
@@ -681,6 +820,8 @@ def gemm_w4a8_q(a: Int8Acts, w: Int4Weights, params: Params | None = None, isa=N
         raise ValueError("gemm_w4a8_q takes the reference's group-128 weights and group sums")
     y = np.empty((a.xq.shape[0], w.n), np.float32)
     prm = _params(params, isa, threads, "w4a8", (a.xq.shape[0], w.n, w.k))
+    if isinstance(w, DeviceInt4Weights) or _use_resident(w, "w4a8", a.xq.shape[0], prm):
+        return _dev_gemm_q(a, resident(w), prm, y)
     rc = lib().lb_gemm_w4a8_q(np.ascontiguousarray(a.xq), np.ascontiguousarray(a.scale, np.float32),
                               np.ascontiguousarray(a.gsum, np.int32), a.xq.shape[0], w.kp, w.qw,
                               w.scales, _zp(w.zeros), w.n, y, C.byref(prm))

@@ -3,8 +3,9 @@
 Every shape the benchmark configurations name runs here through the C ABI:
   C1  W4A16 decode, M=1 N=4096 K=4096, asym and sym weights;
   C2  all three formats at M=1 N=11008 K=4096 (the headline shape), through the
-      host-pointer ABI (lb_gemm_*) and through resident device handles (lbd_gemm_*),
-      on the small-M kernel configuration bench.py times (asserted via lbd_gemm_plan);
+      host-pointer ABI (lb_gemm_*), through resident device handles (lbd_gemm_*) and
+      through host containers made resident on first use (implicit residency), on the
+      small-M kernel configuration bench.py times (asserted via lbd_gemm_plan);
   C3  W4A8 at M=16 and 64, N=11008 and 4096, K=4096, sym and asym, on both weight
       layouts of the matrix-core path, plus worst-case operand tiles (codes 0/15,
       zero-points 0/7/8/15, activations +-127/-128) at 4096 x 4096;
@@ -51,6 +52,16 @@ def _x(m, k, seed):
     return np.random.default_rng(seed + 1).standard_normal((m, k)).astype(np.float32)
 
 
+def _call(fn, x, W, how):
+    """how: "pointer" (the host-pointer ABI lb_gemm_*, weights uploaded per call),
+    "handle" (an explicit to_device handle) or "implicit" (the host container, made
+    resident on its first GEMM)."""
+    if how == "handle":
+        return fn(x, lb.to_device(W))
+    with K.implicit_residency(how == "implicit"):
+        return fn(x, W)
+
+
 def _check(fmt, x, W, y):
     xp = lb.formats.pad_acts(x, W.kp)
     if fmt == "w4a16":
@@ -69,11 +80,11 @@ def _check(fmt, x, W, y):
 # ------------------------------------------------------------------ C1
 
 @pytest.mark.parametrize("asym", [True, False])
-@pytest.mark.parametrize("resident", [False, True])
-def test_c1_w4a16_decode_4096(asym, resident):
+@pytest.mark.parametrize("how", ["pointer", "handle"])
+def test_c1_w4a16_decode_4096(asym, how):
     W = _packed("w4a16", 4096, 4096, 0, asym)
     x = _x(1, 4096, 0)
-    y = K.gemm_w4a16(x, lb.to_device(W) if resident else W)
+    y = _call(K.gemm_w4a16, x, W, how)
     assert K.last_path() == "gfx950"
     _check("w4a16", x, W, y)
 
@@ -95,19 +106,20 @@ def test_c2_plan_is_the_benchmarked_kernel(fmt, asym):
     assert plan["workgroups"] * 8 * plan["rows_per_wave"] >= 11008
 
 
-@pytest.mark.parametrize("resident", [False, True])
+@pytest.mark.parametrize("how", ["pointer", "handle", "implicit"])
 @pytest.mark.parametrize("fmt,asym", C2)
-def test_c2_decode_11008x4096(fmt, asym, resident):
+def test_c2_decode_11008x4096(fmt, asym, how):
     W = _packed(fmt, 11008, 4096, 0, asym)
     x = _x(1, 4096, 0)
     fn = K.GEMMS[fmt]
-    y = fn(x, lb.to_device(W) if resident else W)
+    y = _call(fn, x, W, how)
     assert K.last_path() == "gfx950"
     _check(fmt, x, W, y)
     if fmt == "w4a8":
         a = lb.quantize_act_int8(x)
         ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
-        O.assert_fp_close(K.gemm_w4a8_q(a, W), ref, bound, RTOL)
+        with K.implicit_residency(how != "pointer"):
+            O.assert_fp_close(K.gemm_w4a8_q(a, W), ref, bound, RTOL)
 
 
 @pytest.mark.parametrize("case", ["subnormal", "huge", "max", "under"])
@@ -141,14 +153,14 @@ def test_c2_w4a16_activation_range(case, asym):
 C3 = [(m, n, asym) for m in (16, 64) for n in (11008, 4096) for asym in (True, False)]
 
 
-@pytest.mark.parametrize("resident", [True, False])
+@pytest.mark.parametrize("how", ["handle", "pointer"])
 @pytest.mark.parametrize("m,n,asym", C3)
-def test_c3_w4a8_batches(m, n, asym, resident):
+def test_c3_w4a8_batches(m, n, asym, how):
     """Resident handles run on the t16 tile layout, the pointer ABI on the row-major
     layout; both are the int8 matrix-core path."""
     W = _packed("w4a8", n, 4096, 1, asym)
     x = _x(m, 4096, 1)
-    y = K.gemm_w4a8(x, lb.to_device(W) if resident else W)
+    y = _call(K.gemm_w4a8, x, W, how)
     assert K.last_path() == "gfx950-mfma"
     _check("w4a8", x, W, y)
 
@@ -184,15 +196,15 @@ def test_c3_worst_case_tiles_bit_exact(rng, isa, asym):
 
 # ------------------------------------------------------------------ C4 (down-projection shape)
 
-@pytest.mark.parametrize("resident", [True, False])
+@pytest.mark.parametrize("how", ["handle", "pointer"])
 @pytest.mark.parametrize("m", [1, 16, 64])
 @pytest.mark.parametrize("fmt,asym", [("mxfp4", False), ("w4a16", True), ("w4a16", False)])
-def test_c4_down_projection_lognormal_rows(fmt, asym, m, resident):
+def test_c4_down_projection_lognormal_rows(fmt, asym, m, how):
     W = _packed(fmt, 4096, 11008, 2, asym, lognormal=True)
     if fmt == "mxfp4":
         assert len(np.unique(W.e8m0)) >= 6  # the row scaling spreads the block exponents
     x = _x(m, 11008, 2)
-    y = K.GEMMS[fmt](x, lb.to_device(W) if resident else W)
+    y = _call(K.GEMMS[fmt], x, W, how)
     assert K.last_path() == ("gfx950" if m == 1 else "gfx950-mfma")
     _check(fmt, x, W, y)
 

@@ -5,7 +5,9 @@ int32 group accumulators; |y - ref| <= 1e-5 * (|X| @ |W|^T) against float64 for
 W4A16 / MXFP4, and 1e-5 times the lane magnitudes sum_k q|a| + z|sum a| (times
 |s| and xs) for W4A8 (tests/conftest.py:22-27, tests/test_kernels.py:100-146).
 Both device regimes are exercised: "gfx950" (VALU decode kernels, M <= 4) and
-"gfx950-mfma" (matrix cores).
+"gfx950-mfma" (matrix cores). Host containers go through the host-pointer ABI
+(lb_gemm_*, weights uploaded per call) here; implicit residency has its own tests
+(tests/test_gpu_resident.py).
 """
 import numpy as np
 import pytest
@@ -16,6 +18,12 @@ from oracle import cref
 from oracle import reference as O
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _pointer_abi():
+    with K.implicit_residency(False):
+        yield
 
 # (M, N, K): the reference's odd shapes (tests/test_kernels.py:39-40) plus M tails
 # for the 16-row MFMA tiles.

@@ -4,7 +4,8 @@ include/lowbit_hip.h promises that the lb_* entry points may be called from seve
 threads at once: each thread has its own stream and staging memory. The reference's
 ctypes binding releases the GIL around every call (src/lowbit/kernels.py:46-74), so
 Python callers do run them concurrently. Here eight threads call the host-pointer
-ABI (lb_gemm_*) and the resident-weight path (gemm_* on to_device handles) on
+ABI (lb_gemm_*), the resident-weight path (gemm_* on to_device handles) and host
+containers made resident on first use (one device copy shared by every thread) on
 different shapes and formats, interleaved; every result must equal, bit for bit,
 the same call made alone beforehand (the kernels are deterministic).
 """
@@ -32,12 +33,21 @@ def _operands(rng, fmt, m, n, k):
     return x, W, lb.to_device(W)
 
 
+def _pointer(fn):
+    """fn through the host-pointer ABI (lb_gemm_*) on the calling thread."""
+    def call(x, w):
+        with K.implicit_residency(False):
+            return fn(x, w)
+    return call
+
+
 def test_concurrent_calls_match_serial(rng):
     ops = [_operands(rng, *c) for c in CASES]
     calls = []
     for (fmt, m, n, k), (x, W, D) in zip(CASES, ops):
         fn = K.GEMMS[fmt]
-        calls.append((f"{fmt} {m}x{n}x{k} host", fn, x, W))
+        calls.append((f"{fmt} {m}x{n}x{k} host", _pointer(fn), x, W))
+        calls.append((f"{fmt} {m}x{n}x{k} implicit", fn, x, W))
         calls.append((f"{fmt} {m}x{n}x{k} resident", fn, x, D))
     serial = {name: fn(x, w).copy() for name, fn, x, w in calls}
     paths = {}
