@@ -52,6 +52,7 @@ COLD_POOL_BYTES = 1280 << 20  # > 2 x (256 MB MALL + 32 MB L2)
 DECODE = (1, 11008, 4096)
 BATCH = (64, 11008, 4096)
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_w4a8_gemv_1x11008x4096.txt"
+TRACE_FILE = ROOT / "profiles" / "kernel_trace_headline_w4a8_1x11008x4096.md"
 
 
 def log(*a):
@@ -89,9 +90,40 @@ class Dev:
         self.check(self.L.lb_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
         return ms.value
 
-    def time_launches(self, launch, n_launch: int, warmup: int, graph: bool = True) -> float:
-        """ms per launch of `launch(i)` over n_launch launches (HIP events on the stream)."""
+    GATE_WGS = 256
+
+    def gate(self, us: float):
+        """Enqueue a busy kernel (the fmac issue-rate probe) of about `us` microseconds on
+        the stream: launches enqueued behind it start back to back when it ends, however
+        slowly the host (or a tracer intercepting every launch) enqueues them."""
         L = self.L
+        if not hasattr(self, "_gate_out"):
+            # calibrate on the last of several runs: the first ones run while the clocks
+            # of an idle GPU ramp up (2000 iterations took 1.6 ms cold, ~0.3 ms warm)
+            self._gate_out = self.K.DeviceBuffer(self.GATE_WGS * 512 * 4)
+            iters = 20000
+            e0, e1 = self.event(), self.event()
+            for _ in range(4):
+                self.check(L.lb_dev_synchronize(), "sync")
+                self.check(L.lb_event_record(e0, self.stream), "record")
+                self.check(L.lbd_probe_valu(0, iters, self.GATE_WGS, self._gate_out.ptr, self.stream), "gate")
+                self.check(L.lb_event_record(e1, self.stream), "record")
+                self.check(L.lb_event_synchronize(e1), "sync")
+            self._gate_iters_per_us = iters / max(1e-3, self.elapsed_ms(e0, e1) * 1e3)
+            L.lb_event_destroy(e0)
+            L.lb_event_destroy(e1)
+        iters = max(1, int(us * self._gate_iters_per_us))
+        self.check(L.lbd_probe_valu(0, iters, self.GATE_WGS, self._gate_out.ptr, self.stream), "gate")
+
+    GATE_US_PER_LAUNCH = 40.0  # host time per queued launch the gate covers (tracer included)
+
+    def time_launches(self, launch, n_launch: int, warmup: int, graph: bool = True) -> float:
+        """ms per launch of `launch(i)` over n_launch launches (HIP events on the stream):
+        a replayed graph, or (graph=False) plain launches queued behind a busy kernel so
+        that they run back to back as the graph's do."""
+        L = self.L
+        if not graph:
+            self.gate(self.GATE_US_PER_LAUNCH * warmup)
         for i in range(warmup):
             launch(i)
         self.check(L.lb_stream_synchronize(self.stream), "sync")
@@ -112,6 +144,7 @@ class Dev:
             L.lb_graph_destroy(ex.value)
         else:
             self.check(L.lb_dev_synchronize(), "sync")
+            self.gate(self.GATE_US_PER_LAUNCH * n_launch)
             self.check(L.lb_event_record(e0, self.stream), "record")
             for i in range(n_launch):
                 launch(i)
@@ -151,7 +184,11 @@ def weight_pool(dev: Dev, arrays: list[np.ndarray], nbytes: int, cold: bool):
 # ------------------------------------------------------------------ one GPU measurement
 
 def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int, warmup: int,
-            graph: bool = True) -> dict:
+            graph: bool = True, eager_too: bool = False, call: bool = True) -> dict:
+    """One GEMM configuration: device time per launch over >= MIN_LAUNCHES launches
+    (HIP events around a replayed graph, or around plain launches with graph=False;
+    eager_too adds the plain-launch time beside the graph's), and the wall time of
+    one synchronous Python call (call=False skips it, for kernel traces)."""
     from lowbit_amd import formats as F
     K = dev.K
     L = dev.L
@@ -240,13 +277,16 @@ def measure(dev: Dev, fmt: str, shape, W, x: np.ndarray, cold: bool, steps: int,
     # launches, whatever --steps asks for
     n_launch = timed_launches(steps, len(pool))
     ms = dev.time_launches(launch, n_launch, warmup, graph=graph)
+    ms_eager = dev.time_launches(launch, n_launch, warmup, graph=False) if (eager_too and graph) else None
     t = ms * 1e-3
-    call_us = call_time(dev, fmt, W, x, pool, layout, n_launch, warmup)
+    call_us = call_time(dev, fmt, W, x, pool, layout, n_launch, warmup) if call else None
     return {
         "format": fmt, "M": m, "N": n, "K": k, "cache": "cold" if cold else "hot",
         "path": K.ISA_NAMES.get(path, "?"), "weight_layout": layout, "pool_copies": len(pool),
         "timed_launches": n_launch, "bytes_rotated": int(min(n_launch, len(pool)) * W.nbytes),
-        "us_per_call": round(ms * 1e3, 3), "call_us": call_us, "weight_bytes": int(W.nbytes),
+        "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_eager": None if ms_eager is None else round(ms_eager * 1e3, 3),
+        "call_us": call_us, "weight_bytes": int(W.nbytes),
         "weight_gbps": round(W.nbytes / t / 1e9, 1),
         "gflops": round(2.0 * m * n * k / t / 1e9, 1),
         "y": y,
@@ -288,6 +328,46 @@ def read_floor(dev: Dev, nbytes: int, steps: int, warmup: int, graph: bool = Tru
     log(f"read floor {nbytes} B: cold {out['cold']['us']:.2f} us ({out['cold']['gbps']:.0f} GB/s) "
         f"{out['cold']['config']}, hot {out['hot']['us']:.2f} us ({out['hot']['gbps']:.0f} GB/s) {out['hot']['config']}")
     return out
+
+
+# The plain read at sizes from the headline's 24.3 MB to 1 GiB (cold), to separate the
+# fixed cost of a launch from the streaming rate: t(S) = t0 + S / B, least squares.
+FLOOR_SIZE_FACTORS = (1, 2, 4, 8, 16, 32)
+FLOOR_SIZE_CONFIGS = [(wg, 512, ld) for wg in (512, 1024, 2048) for ld in (2, 4, 8)]
+
+
+def read_floor_sizes(dev: Dev, base_bytes: int, steps: int, warmup: int, graph: bool = True) -> dict:
+    """The fastest cold plain read (over FLOOR_SIZE_CONFIGS) at base_bytes x
+    FLOOR_SIZE_FACTORS and at 1 GiB, and the fit t = t0 + S / B over those sizes."""
+    K, L = dev.K, dev.L
+    sizes = [(base_bytes * f + 15) // 16 * 16 for f in FLOOR_SIZE_FACTORS] + [1 << 30]
+    sink = K.DeviceBuffer(16)
+    rows = []
+    for nbytes in sizes:
+        copies = max(2, math.ceil(COLD_POOL_BYTES / nbytes))
+        pool = [K.DeviceBuffer(nbytes) for _ in range(copies)]
+        for i, b in enumerate(pool):
+            dev.check(L.lb_memset_d(b.ptr, 0x21 + i % 200, nbytes), "memset")
+        best = None
+        for wg, th, ld in FLOOR_SIZE_CONFIGS:
+            def launch(i, wg=wg, th=th, ld=ld):
+                b = pool[i % copies]
+                return dev.check(L.lbd_read_kernel(b.ptr, nbytes, wg, th, ld, sink.ptr, dev.stream), "read kernel")
+
+            us = dev.time_launches(launch, timed_launches(steps, copies), warmup, graph=graph) * 1e3
+            if best is None or us < best[0]:
+                best = (us, {"workgroups": wg, "threads": th, "loads": ld})
+        rows.append({"bytes": nbytes, "us": round(best[0], 3), "gbps": round(nbytes / (best[0] * 1e-6) / 1e9, 1),
+                     "config": best[1], "pool_copies": copies})
+        del pool
+        log(f"read floor {nbytes / 2**20:8.1f} MiB cold: {best[0]:8.2f} us ({rows[-1]['gbps']:.0f} GB/s) {best[1]}")
+    S = np.array([r["bytes"] for r in rows], np.float64)
+    T = np.array([r["us"] for r in rows], np.float64) * 1e-6
+    slope, t0 = np.polyfit(S, T, 1)  # T = t0 + slope * S
+    bw = 1.0 / slope / 1e9
+    return {"sizes": rows, "fit": {"t0_us": round(t0 * 1e6, 3), "asymptotic_gbps": round(bw, 1),
+                                   "asymptotic_frac_of_peak": round(bw / HBM_PEAK_GBS, 4),
+                                   "max_resid_us": round(float(np.max(np.abs(T - (t0 + slope * S)))) * 1e6, 3)}}
 
 
 PROBE_FORMS = ["v_fmac_f32", "v_fma_f32", "v_add_f32", "v_mul_f32", "v_and_b32", "v_lshrrev_b32",
@@ -657,6 +737,17 @@ def traffic_bytes() -> int | None:
     return None
 
 
+def traced_kernel_us() -> float | None:
+    """Mean kernel-trace duration of the headline kernel's timed dispatches, from the
+    committed trace summary (a traced run launches every kernel on its own)."""
+    if not TRACE_FILE.exists():
+        return None
+    for ln in TRACE_FILE.read_text().splitlines():
+        if ln.startswith("traced_kernel_mean_us:"):
+            return float(ln.split(":", 1)[1])
+    return None
+
+
 # ------------------------------------------------------------------ main
 
 def main() -> int:
@@ -678,6 +769,8 @@ def main() -> int:
                     help="only sweep the plain streaming read of the headline weight bytes (cold and hot) "
                          "and print its JSON")
     ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor sweep")
+    ap.add_argument("--no-call-time", action="store_true",
+                    help="skip the synchronous Python call timings (kernel traces of the timed launches only)")
     ap.add_argument("--batch-m", type=int, default=BATCH[0], metavar="M",
                     help="rows of the hot batch GEMMs (default 64, the BASELINE shape)")
     ap.add_argument("--machine-facts", action="store_true",
@@ -714,8 +807,9 @@ def main() -> int:
     graph = not args.no_graph
     headline_bytes = 11008 * (4096 // 2 + (4096 // 128) * 5)  # int4 g128 asym weights of the headline
     if args.read_floor:
-        print(json.dumps({"read_floor": read_floor(dev, headline_bytes, args.steps, args.warmup, graph)}),
-              flush=True)
+        print(json.dumps({"read_floor": read_floor(dev, headline_bytes, args.steps, args.warmup, graph),
+                          "read_floor_sizes": read_floor_sizes(dev, headline_bytes, args.steps, args.warmup,
+                                                               graph)}), flush=True)
         return 0
     if args.machine_facts:
         facts = machine_facts(dev, args.warmup)
@@ -737,18 +831,22 @@ def main() -> int:
     order = ["w4a8"] if args.only_headline else ["w4a8", "w4a16", "mxfp4"]
     for fmt in order:
         W = mx if fmt == "mxfp4" else w4
-        r = measure(dev, fmt, DECODE, W, x, cold=True, steps=args.steps, warmup=args.warmup, graph=graph)
+        r = measure(dev, fmt, DECODE, W, x, cold=True, steps=args.steps, warmup=args.warmup, graph=graph,
+                    eager_too=(fmt == "w4a8"), call=not args.no_call_time)
         r["max_rel_err"] = float(f"{rel_err(fmt, W, x, r.pop('y')):.3g}")
         r["hbm_frac"] = round(r["weight_gbps"] / HBM_PEAK_GBS, 4)
         # the same call on the host container: implicit residency, and the pointer ABI
-        r["call_us_host_container"] = call_time_host(dev, fmt, W, x, 200, implicit=True)
-        r["call_us_pointer_abi"] = call_time_host(dev, fmt, W, x, 20, implicit=False)
+        if not args.no_call_time:
+            r["call_us_host_container"] = call_time_host(dev, fmt, W, x, 200, implicit=True)
+            r["call_us_pointer_abi"] = call_time_host(dev, fmt, W, x, 20, implicit=False)
         results[f"{fmt}_decode"] = r
-        log(f"{fmt:6s} M=1 cold: {r['us_per_call']:8.2f} us  {r['weight_gbps']:7.1f} GB/s "
+        calls = ("" if args.no_call_time else
+                 f"call through ctypes {r['call_us']:.1f} us (host container {r['call_us_host_container']:.1f}, "
+                 f"pointer ABI {r['call_us_pointer_abi']:.0f})  ")
+        eager = "" if r["us_per_call_eager"] is None else f"(plain launches {r['us_per_call_eager']:.2f} us)  "
+        log(f"{fmt:6s} M=1 cold: {r['us_per_call']:8.2f} us  {eager}{r['weight_gbps']:7.1f} GB/s "
             f"({100 * r['hbm_frac']:.1f}% HBM)  path {r['path']}  rel err {r['max_rel_err']}  "
-            f"call through ctypes {r['call_us']:.1f} us (host container {r['call_us_host_container']:.1f}, "
-            f"pointer ABI {r['call_us_pointer_abi']:.0f})  ({r['timed_launches']} launches, "
-            f"{r['bytes_rotated'] >> 20} MiB rotated)")
+            f"{calls}({r['timed_launches']} launches, {r['bytes_rotated'] >> 20} MiB rotated)")
 
     # batch: M=64, hot (the reference measures batch shapes hot, src/lowbit/bench.py:167);
     # --batch-m selects another M (the counter profiles of the M = 16 kernels)
@@ -758,7 +856,7 @@ def main() -> int:
         for fmt in ["w4a8", "w4a16", "mxfp4"]:
             W = mx if fmt == "mxfp4" else w4
             r = measure(dev, fmt, (mb, nb, kb), W, xb, cold=False, steps=args.steps,
-                        warmup=max(2, args.warmup // 4), graph=graph)
+                        warmup=max(2, args.warmup // 4), graph=graph, call=not args.no_call_time)
             r["max_rel_err"] = float(f"{rel_err(fmt, W, xb, r.pop('y')):.3g}")
             if fmt == "w4a8":
                 r["mfma"] = "int8"
@@ -773,15 +871,16 @@ def main() -> int:
                 r["mfma_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
             results[f"{fmt}_m{mb}"] = r
             log(f"{fmt:6s} M={mb} hot: {r['us_per_call']:8.2f} us  {r['gflops']:9.1f} GFLOP/s "
-                f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}  "
-                f"call through ctypes {r['call_us']:.1f} us")
+                f"({100 * r['mfma_frac']:.1f}% of {r['mfma']} MFMA peak)  path {r['path']}" +
+                ("" if r["call_us"] is None else f"  call through ctypes {r['call_us']:.1f} us"))
 
-    floor = None
+    floor = sizes = None
     if not args.no_floor:
         floor = read_floor(dev, headline_bytes, args.steps, args.warmup, graph)
         for kk, r in results.items():
             if r["M"] == 1:
                 r["frac_of_read_floor"] = round(floor["cold"]["us"] / r["us_per_call"], 4)
+        sizes = read_floor_sizes(dev, headline_bytes, args.steps, args.warmup, graph)
 
     decoder = None
     if not (args.only_headline or args.no_decoder):
@@ -792,6 +891,12 @@ def main() -> int:
     # algorithmic bytes of one launch: packed weights + fp32 X + fp32 Y
     algo_bytes = head["weight_bytes"] + 4 * k * m + 4 * n * m
     achieved = algo_bytes / t_launch_s / 1e9
+    eager = None
+    if head["us_per_call_eager"]:
+        a_e = algo_bytes / (head["us_per_call_eager"] * 1e-6) / 1e9
+        # plain launches, the way a kernel trace sees them (durations comparable method for method)
+        eager = {"us_per_launch": head["us_per_call_eager"], "achieved": round(a_e, 1),
+                 "frac": round(a_e / HBM_PEAK_GBS, 4)}
     cpu = None
     if not args.no_cpu:
         try:
@@ -825,12 +930,24 @@ def main() -> int:
                          "cold_us": floor["cold"]["us"], "cold_gbps": floor["cold"]["gbps"],
                          "hot_us": floor["hot"]["us"], "hot_gbps": floor["hot"]["gbps"],
                          "config": floor["cold"]["config"],
-                         "frac_of_floor": round(floor["cold"]["us"] / head["us_per_call"], 4)}},
+                         "frac_of_floor": round(floor["cold"]["us"] / head["us_per_call"], 4),
+                         "size_sweep": sizes,
+                         "frac_of_asymptotic": None if sizes is None else round(
+                             achieved / sizes["fit"]["asymptotic_gbps"], 4),
+                         # the launch's bytes over its time past the fitted fixed cost t0
+                         "streaming_frac_of_peak": None if sizes is None else round(
+                             algo_bytes / ((head["us_per_call"] - sizes["fit"]["t0_us"]) * 1e-6) / 1e9
+                             / HBM_PEAK_GBS, 4)},
+                     "eager": eager,
+                     "traced": None if traced_kernel_us() is None else {
+                         "kernel_us": traced_kernel_us(),
+                         "frac": round(algo_bytes / (traced_kernel_us() * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "source": TRACE_FILE.name}},
         "timed_launches": head["timed_launches"],
         "bytes_rotated": head["bytes_rotated"],
         "call_us": head["call_us"],
-        "call_us_host_container": head["call_us_host_container"],
-        "call_us_pointer_abi": head["call_us_pointer_abi"],
+        "call_us_host_container": head.get("call_us_host_container"),
+        "call_us_pointer_abi": head.get("call_us_pointer_abi"),
         "cpu_baseline": cpu,
         "per_format": {kk: {f: v for f, v in vv.items() if f not in ("N", "K")} for kk, vv in results.items()},
         "decoder": decoder,
