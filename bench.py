@@ -421,6 +421,32 @@ def grid_barrier_costs(dev: Dev, cus: int, rounds: int = 200, reps: int = 5) -> 
     return out
 
 
+MFMA_VALU_VARIANTS = ["mfma", "valu", "interleaved", "blocks"]
+
+
+def mfma_valu_sharing(dev: Dev, cus: int, warmup: int) -> dict:
+    """Whether one SIMD overlaps int8 MFMA with independent VALU work
+    (lbd_probe_mfma_valu): ns per loop iteration (per wave: 8 v_mfma_i32_16x16x64_i8,
+    64 v_fmac_f32, or both) at one workgroup per CU of 256 or 512 threads, i.e. one or
+    two waves per SIMD. Overlap shows as both near the larger alone; sharing as both
+    near the sum."""
+    K, L = dev.K, dev.L
+    iters = 1024
+    out = K.DeviceBuffer(cus * 512 * 4)
+    res = {}
+    for threads in (256, 512):
+        row = {}
+        for v, name in enumerate(MFMA_VALU_VARIANTS):
+            ms = dev.time_launches(lambda i, v=v, t=threads: dev.check(
+                L.lbd_probe_mfma_valu(v, iters, cus, t, out.ptr, dev.stream), "probe"), 5, max(2, warmup // 10))
+            row[name] = round(ms * 1e6 / iters, 2)
+        key = f"{threads // 256}_wave_per_simd"
+        res[key] = row
+        log(f"MFMA / VALU on one SIMD, {key}: " + ", ".join(f"{k} {v:.1f}" for k, v in row.items()) +
+            f" ns per iteration (sum of the two alone {row['mfma'] + row['valu']:.1f})")
+    return res
+
+
 def machine_facts(dev: Dev, warmup: int) -> dict:
     """The device facts the kernel designs rest on, measured by the library's probe
     kernels (lb_probe.hip): the issue cost of single VALU instruction forms (16 waves
@@ -444,7 +470,9 @@ def machine_facts(dev: Dev, warmup: int) -> dict:
         empty[f"{g}x512"] = round(ms * 1e3, 3)
         log(f"empty kernel {g} x 512 threads: {empty[f'{g}x512']:.2f} us per graph-replayed launch")
     barrier = grid_barrier_costs(dev, cus)
+    sharing = mfma_valu_sharing(dev, cus, warmup)
     return {"valu_ns_per_wave_instruction_per_cu": rates, "empty_launch_us": empty, "grid_barrier_us": barrier,
+            "mfma_valu_ns_per_iteration": sharing,
             "probe": {"workgroups": wgs, "threads": 512, "iters": iters, "instructions_per_iter": 32,
                       "independent_registers": 8}}
 

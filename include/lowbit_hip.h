@@ -476,6 +476,14 @@ int lbd_read_kernel(const void *src, size_t bytes, int workgroups, int threads, 
  * receives workgroups * 512 floats of no meaning (they keep the work alive). */
 int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream);
 int lbd_probe_forms(void);
+/* Matrix-core / VALU sharing probe (no reference counterpart; the measurement behind
+ * the int8 GEMM's arithmetic bound): per iteration 8 independent
+ * v_mfma_i32_16x16x64_i8 (variant 0), 64 independent v_fmac_f32 (1), both with one
+ * MFMA before each eight FMACs (2) or all MFMAs first (3); `workgroups` workgroups of
+ * `threads` = 256 or 512 threads (one or two waves per SIMD at one workgroup per CU);
+ * `out` receives workgroups * threads floats of no meaning. */
+int lbd_probe_mfma_valu(int variant, int iters, int workgroups, int threads, float *out,
+                        void *stream);
 /* a kernel of `workgroups` x 512 threads that does nothing: the fixed cost of a launch */
 int lbd_empty_kernel(int workgroups, void *stream);
 /* Check of the one-row W4A8 quantizer's token scale (no reference counterpart: the

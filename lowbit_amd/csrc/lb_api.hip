@@ -1427,6 +1427,16 @@ int lbd_probe_valu(int op, int iters, int workgroups, float *out, void *stream) 
   return ok(0);
 }
 int lbd_probe_forms(void) { return lbk::valu_probe_forms(); }
+int lbd_probe_mfma_valu(int variant, int iters, int workgroups, int threads, float *out, void *stream) {
+  if (!out) return fail(LB_ERR_ARG, "probe needs an output buffer");
+  if (variant < 0 || variant > 3 || iters <= 0 || workgroups <= 0 || workgroups > 65536 ||
+      (threads != 256 && threads != 512))
+    return fail(LB_ERR_ARG, "probe: variant 0..3, iters > 0, 1..65536 workgroups of 256 or 512 threads");
+  hipError_t e = lbk::launch_mfma_valu_probe(variant, iters, workgroups, threads, out,
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "probe launch");
+  return ok(0);
+}
 int lbd_empty_kernel(int workgroups, void *stream) {
   if (workgroups <= 0 || workgroups > 65536) return fail(LB_ERR_ARG, "empty kernel: 1..65536 workgroups");
   hipError_t e = lbk::launch_empty(workgroups, static_cast<hipStream_t>(stream));

@@ -152,6 +152,9 @@ hipError_t launch_valu_probe(int op, int iters, int workgroups, float *out, hipS
 int valu_probe_forms();
 // a kernel that does nothing, workgroups of 512 threads
 hipError_t launch_empty(int workgroups, hipStream_t s);
+// Matrix-core / VALU sharing probe: variant 0 MFMA only, 1 VALU only, 2 both
+// interleaved, 3 both in blocks; `threads` 256 or 512; out: workgroups * threads floats.
+hipError_t launch_mfma_valu_probe(int variant, int iters, int workgroups, int threads, float *out, hipStream_t s);
 // div127 against a / 127.0f on every non-negative finite float32 and +inf: out[0] the
 // number that differ, out[1] the smallest differing bit pattern (0xFFFFFFFF: none)
 hipError_t launch_div127_probe(uint32_t *out, hipStream_t s);

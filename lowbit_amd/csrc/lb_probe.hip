@@ -241,6 +241,63 @@ hipError_t launch_div127_probe(uint32_t *out, hipStream_t s) {
 
 __global__ __launch_bounds__(512) void empty_kernel() {}
 
+// ---- matrix-core / VALU sharing probe: per loop iteration 8 independent
+//      v_mfma_i32_16x16x64_i8 (eight accumulators), 64 independent v_fmac_f32 (eight
+//      registers), or both, either one MFMA before each eight FMACs (interleaved) or
+//      all eight MFMAs before the 64 FMACs (blocks). Written as inline assembly so the
+//      order is exactly this; no memory access in the loop. With 256 threads per
+//      workgroup and one workgroup per CU each SIMD runs one wave, with 512 two: the
+//      question is whether one SIMD's matrix-core and VALU instructions overlap
+//      (time of both near the larger of the two alone) or add up.
+template <int V>
+__global__ __launch_bounds__(512) void mfma_valu_probe_kernel(int iters, float *out) {
+  v4i acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) acc[j] = v4i{0, 0, 0, 0};
+  const v4i a = v4i{(int)threadIdx.x, 1, 2, 3}, b = v4i{3, 2, 1, (int)threadIdx.x};
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) r[j] = 1.0f + (float)threadIdx.x * 0.0009765625f + (float)j;
+  const float x = 0.999f, y = 1e-7f;
+  for (int i = 0; i < iters; i++) {
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+      if constexpr (V == 0 || V == 2 || V == 3)
+        asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(acc[m]) : "v"(a), "v"(b));
+      if constexpr (V == 1 || V == 2) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) asm volatile("v_fmac_f32_e32 %0, %1, %2" : "+v"(r[j]) : "v"(x), "v"(y));
+      }
+    }
+    if constexpr (V == 3) {
+#pragma unroll
+      for (int m = 0; m < 8; m++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) asm volatile("v_fmac_f32_e32 %0, %1, %2" : "+v"(r[j]) : "v"(x), "v"(y));
+    }
+  }
+  // the last matrix-core results are read only after the longest MFMA's wait states
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  float f = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) f += r[j] + (float)(acc[j].x + acc[j].y + acc[j].z + acc[j].w);
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = f;
+}
+
+hipError_t launch_mfma_valu_probe(int variant, int iters, int workgroups, int threads, float *out, hipStream_t s) {
+  if (variant < 0 || variant > 3 || iters <= 0 || workgroups <= 0 || workgroups > 65536 ||
+      (threads != 256 && threads != 512))
+    return hipErrorInvalidValue;
+  const dim3 g(workgroups), b(threads);
+  switch (variant) {
+    case 0: hipLaunchKernelGGL(mfma_valu_probe_kernel<0>, g, b, 0, s, iters, out); break;
+    case 1: hipLaunchKernelGGL(mfma_valu_probe_kernel<1>, g, b, 0, s, iters, out); break;
+    case 2: hipLaunchKernelGGL(mfma_valu_probe_kernel<2>, g, b, 0, s, iters, out); break;
+    default: hipLaunchKernelGGL(mfma_valu_probe_kernel<3>, g, b, 0, s, iters, out); break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_empty(int workgroups, hipStream_t s) {
   if (workgroups <= 0 || workgroups > 65536) return hipErrorInvalidValue;
   hipLaunchKernelGGL(empty_kernel, dim3(workgroups), dim3(512), 0, s);

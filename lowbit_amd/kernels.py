@@ -129,6 +129,7 @@ SIGNATURES = {
     "lbd_read_kernel": ([_vp, _sz, _int, _int, _int, _vp, _vp], _int),
     "lbd_probe_valu": ([_int, _int, _int, _vp, _vp], _int),
     "lbd_probe_forms": ([], _int),
+    "lbd_probe_mfma_valu": ([_int, _int, _int, _int, _vp, _vp], _int),
     "lbd_empty_kernel": ([_int, _vp], _int),
     "lbd_probe_div127": ([_vp, _vp], _int),
     "lbd_probe_grid_barrier": ([_int, _int, _int, _vp, _sz, _vp, _vp], _int),

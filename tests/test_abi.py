@@ -182,6 +182,10 @@ def test_probe_argument_checks():
     assert L.lbd_probe_valu(0, 0, 1, out, None) == -6               # no iterations
     assert L.lbd_probe_valu(0, 16, 0, out, None) == -6              # no workgroups
     assert L.lbd_empty_kernel(0, None) == -6
+    assert L.lbd_probe_mfma_valu(0, 16, 1, 256, None, None) == -6      # no output buffer
+    assert L.lbd_probe_mfma_valu(4, 16, 1, 256, out, None) == -6       # past the last variant
+    assert L.lbd_probe_mfma_valu(0, 16, 1, 128, out, None) == -6       # 128 threads
+    assert L.lbd_probe_mfma_valu(0, 0, 1, 512, out, None) == -6        # no iterations
     assert L.lbd_empty_kernel(70000, None) == -6
     assert L.lbd_read_kernel(None, 1024, 1, 256, 1, None, None) == -6
     assert L.lbd_read_kernel(out, 1000, 1, 256, 1, out, None) == -6   # not a multiple of 16
