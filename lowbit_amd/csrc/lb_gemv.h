@@ -122,36 +122,59 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
 // ---- per-chunk arithmetic, shared by gemv_kernel and gemv_paced_kernel so that the
 //      two give the same bits
 
-// Sum of one chunk's 32 fp32 activations (low-nibble half, then high-nibble half), in
-// the order the W4A16 products are summed, so that sum(q*x) - z*sum(x) is exactly 0
-// when every q == z and z is a power of two (z = 8: symmetric zero rows and padding).
-__device__ __forceinline__ float chunk_xsum(const float4 (&xv)[8]) {
-  float sl = 0.0f, sh = 0.0f;
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    sl += xv[p].x; sl += xv[p].y; sl += xv[p].z; sl += xv[p].w;
-    sh += xv[4 + p].x; sh += xv[4 + p].y; sh += xv[4 + p].z; sh += xv[4 + p].w;
-  }
-  return sl + sh;
+// W4A16: the codes of one 32-bit word of a chunk (four low nibbles, four high nibbles)
+// as the two's complement bytes q - z, for any zero-point z in 0..15: 128 - z is added
+// to every byte holding a nibble q (each stays within 113..143, so no carry crosses a
+// byte) and bit 7 is flipped back. One conversion then sign-extends and converts each
+// byte (v_cvt_f32_i32 with a sign-extended byte source), so the products below are
+// those of the dequantized weight, as the reference forms them
+// (src/lowbit/csrc/kern_scalar.c:10-29), and a row's fp32 rounding stays relative to
+// sum |q - z| |x|, the bound's scale, even where a large activation meets a code equal
+// to the zero-point (the split sum q x - z sum x rounds relative to sum q |x|).
+__device__ __forceinline__ uint32_t w4a16_bias(int z) { return 0x80808080u - (uint32_t)z * 0x01010101u; }
+__device__ __forceinline__ uint32_t w4a16_lo(uint32_t w, uint32_t bias) {
+  return ((w & 0x0F0F0F0Fu) + bias) ^ 0x80808080u;
 }
+__device__ __forceinline__ uint32_t w4a16_hi(uint32_t w, uint32_t bias) {
+  return (((w >> 4) & 0x0F0F0F0Fu) + bias) ^ 0x80808080u;
+}
+__device__ __forceinline__ float sbyte(uint32_t v, int k) { return (float)(int8_t)(v >> (8 * k)); }
 
-// W4A16: sum_k (q_k - z) x_k of one 16-byte chunk, as sum q x - z * sum x.
-__device__ __forceinline__ float w4a16_chunk(uint4 w, const float4 (&xv)[8], int z, float xsum) {
+// W4A16: sum_k (q_k - z) x_k of one 16-byte chunk (low-nibble half, then high-nibble
+// half, each in element order).
+__device__ __forceinline__ float w4a16_chunk(uint4 w, const float4 (&xv)[8], int z) {
+  const uint32_t bias = w4a16_bias(z);
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   float pl = 0.0f, ph = 0.0f;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
-    const uint32_t lo = opaque(lo_nibbles(wd[d])), hi = opaque(hi_nibbles(wd[d]));
-    pl = __builtin_fmaf((float)(lo & 0xFF), xv[d].x, pl);
-    pl = __builtin_fmaf((float)((lo >> 8) & 0xFF), xv[d].y, pl);
-    pl = __builtin_fmaf((float)((lo >> 16) & 0xFF), xv[d].z, pl);
-    pl = __builtin_fmaf((float)(lo >> 24), xv[d].w, pl);
-    ph = __builtin_fmaf((float)(hi & 0xFF), xv[4 + d].x, ph);
-    ph = __builtin_fmaf((float)((hi >> 8) & 0xFF), xv[4 + d].y, ph);
-    ph = __builtin_fmaf((float)((hi >> 16) & 0xFF), xv[4 + d].z, ph);
-    ph = __builtin_fmaf((float)(hi >> 24), xv[4 + d].w, ph);
+    const uint32_t lo = w4a16_lo(wd[d], bias), hi = w4a16_hi(wd[d], bias);
+    pl = __builtin_fmaf(sbyte(lo, 0), xv[d].x, pl);
+    pl = __builtin_fmaf(sbyte(lo, 1), xv[d].y, pl);
+    pl = __builtin_fmaf(sbyte(lo, 2), xv[d].z, pl);
+    pl = __builtin_fmaf(sbyte(lo, 3), xv[d].w, pl);
+    ph = __builtin_fmaf(sbyte(hi, 0), xv[4 + d].x, ph);
+    ph = __builtin_fmaf(sbyte(hi, 1), xv[4 + d].y, ph);
+    ph = __builtin_fmaf(sbyte(hi, 2), xv[4 + d].z, ph);
+    ph = __builtin_fmaf(sbyte(hi, 3), xv[4 + d].w, ph);
   }
-  return __builtin_fmaf(-(float)z, xsum, pl + ph);
+  return pl + ph;
+}
+
+// W4A16: the 32 codes of one chunk as the exact floats q - z (low-nibble half in wl,
+// high-nibble half in wh), for rows used against several activation rows.
+__device__ __forceinline__ void w4a16_decode(uint4 w, int z, float (&wl)[16], float (&wh)[16]) {
+  const uint32_t bias = w4a16_bias(z);
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const uint32_t lo = w4a16_lo(wd[d], bias), hi = w4a16_hi(wd[d], bias);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      wl[4 * d + u] = sbyte(lo, u);
+      wh[4 * d + u] = sbyte(hi, u);
+    }
+  }
 }
 
 // MXFP4: the E2M1 pairs (low nibble, high nibble) of each byte of a chunk, exact in fp32.
@@ -168,8 +191,10 @@ __device__ __forceinline__ void mxfp4_decode(uint4 w, float (&wl)[16], float (&w
   }
 }
 
-// MXFP4: sum_k e2m1(q_k) x_k of one chunk (before the block scale).
-__device__ __forceinline__ float mxfp4_dot(const float (&wl)[16], const float (&wh)[16], const float4 (&xv)[8]) {
+// sum_k w_k x_k of one chunk's decoded codes (MXFP4 before the block scale, W4A16
+// before the group scale): low-nibble half, then high-nibble half, each in element
+// order (the order of w4a16_chunk).
+__device__ __forceinline__ float chunk_dot(const float (&wl)[16], const float (&wh)[16], const float4 (&xv)[8]) {
   float pl = 0.0f, ph = 0.0f;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
@@ -211,34 +236,24 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
   for (int it = 0; it < NIT; it++) {
     const int ci = (HW ? lane & 31 : lane) + kWave * it;
     if (it * kWave >= nchp) break;  // uniform: this row length needs fewer chunks
-    if constexpr (F == F_W4A16 || F == F_W4A16G32) {
-#pragma unroll
-      for (int m = 0; m < MB; m++) {
-        float4 xv[8];
-#pragma unroll
-        for (int p = 0; p < 8; p++)
-          xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-        const float xsum = chunk_xsum(xv);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-          if (r >= nr) break;
-          const float part = w4a16_chunk(g.w[r][it], xv, g.zi[r][it], xsum);
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], part, acc[m][r]);
-        }
-      }
-    } else if constexpr (F == F_MXFP4) {
+    if constexpr (F == F_W4A16 || F == F_W4A16G32 || F == F_MXFP4) {
+      // each weight row's codes decoded once, then against every activation row
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (r >= nr) break;
         float wl[16], wh[16];
-        mxfp4_decode(g.w[r][it], wl, wh);
+        if constexpr (F == F_MXFP4) {
+          mxfp4_decode(g.w[r][it], wl, wh);
+        } else {
+          w4a16_decode(g.w[r][it], g.zi[r][it], wl, wh);
+        }
 #pragma unroll
         for (int m = 0; m < MB; m++) {
           float4 xv[8];
 #pragma unroll
           for (int p = 0; p < 8; p++)
             xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], mxfp4_dot(wl, wh, xv), acc[m][r]);
+          acc[m][r] = __builtin_fmaf(g.sc[r][it], chunk_dot(wl, wh, xv), acc[m][r]);
         }
       }
     } else {
@@ -747,7 +762,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
   constexpr bool kXReg = NIT <= 2;
   constexpr bool kF32 = (kW16 || F == F_MXFP4);
   float4 xv[kXReg && kF32 ? NIT : 1][8];
-  float xsm[kXReg && kW16 ? NIT : 1];
   uint4 al[kXReg && kInt8 ? NIT : 1], ah[kXReg && kInt8 ? NIT : 1];
   int as[kXReg && kInt8 ? NIT : 1];
   if constexpr (kXReg) {
@@ -757,7 +771,6 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
       if constexpr (kF32) {
 #pragma unroll
         for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
-        if constexpr (kW16) xsm[it] = chunk_xsum(xv[it]);
       } else {
         al[it] = *reinterpret_cast<const uint4 *>(ql + (size_t)ci * 16);
         ah[it] = *reinterpret_cast<const uint4 *>(ql + ((size_t)nchp + ci) * 16);
@@ -779,11 +792,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
         const uint32_t ci = (uint32_t)lane + kWave * it;
         if constexpr (kW16) {
           const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
-          acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
+          acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z), acc);
         } else if constexpr (F == F_MXFP4) {
           float wl[16], wh[16];
           mxfp4_decode(st.w[it], wl, wh);
-          acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), mxfp4_dot(wl, wh, xv[it]), acc);
+          acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), chunk_dot(wl, wh, xv[it]), acc);
         } else {
           int d = w4a8_chunk(st.w[it], al[it], ah[it]);
           d -= ((int)paced_byte<F, DW>(st.z[it], ci) + zadd) * as[it];
@@ -906,13 +919,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
 
   // ---- 3. this wave's slice of the activations into registers
   float4 xv[NIT][8];
-  float xsm[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
     const int ci = (int)cb + lane + kWave * it;
 #pragma unroll
     for (int p = 0; p < 8; p++) xv[it][p] = *reinterpret_cast<const float4 *>(xl + ((size_t)p * nchp + ci) * 4);
-    xsm[it] = kW16 ? chunk_xsum(xv[it]) : 0.0f;
   }
 
   // ---- 4. rows: the next one's loads out, then this one's slice sum into `part`
@@ -924,11 +935,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
       const uint32_t ci = cb + (uint32_t)lane + kWave * it;
       if constexpr (kW16) {
         const int z = (int)paced_byte<F, DW>(st.z[it], ci) + zadd;
-        acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z, xsm[it]), acc);
+        acc = __builtin_fmaf(__uint_as_float(st.s[it]), w4a16_chunk(st.w[it], xv[it], z), acc);
       } else {
         float wl[16], wh[16];
         mxfp4_decode(st.w[it], wl, wh);
-        acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), mxfp4_dot(wl, wh, xv[it]), acc);
+        acc = __builtin_fmaf(e8m0_to_f32(paced_byte<F, DW>(st.s[it], ci)), chunk_dot(wl, wh, xv[it]), acc);
       }
     }
     const float t = wave_sum(acc);

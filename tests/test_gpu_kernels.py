@@ -16,6 +16,7 @@ import lowbit_amd as lb
 from lowbit_amd import kernels as K
 from oracle import cref
 from oracle import reference as O
+from problems import outlier_int4_problem
 
 pytestmark = pytest.mark.gpu
 
@@ -222,6 +223,24 @@ def test_zero_activation_row(rng, isa):
     for gemm in (K.gemm_w4a8, K.gemm_w4a16):
         y = gemm(x, W, isa=isa)
         assert np.all(y[1] == 0) and np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("isa", PATHS)
+@pytest.mark.parametrize("m,n,k", [(1, 40, 256), (3, 40, 256), (1, 300, 4096), (1, 200, 8320), (2, 64, 2048),
+                                   (16, 70, 1024), (1, 24, 1152)])
+def test_w4a16_outliers_at_zero_point_codes(isa, m, n, k):
+    """Huge activations (1e6) where every weight code equals its zero-point: they add
+    nothing to the reference's bound, and a kernel forming sum q x - z sum x misses it
+    by a factor of tens to thousands (tests/test_w4a16_outliers.py). Every W4A16 path
+    (the paced and split one-row GEMVs, the M = 2..4 GEMV, the matrix-core GEMM, host
+    pointers and resident handles) must stay within it."""
+    rng = np.random.default_rng(1000 + m * 7 + k)
+    x, W = outlier_int4_problem(rng, m, n, k)
+    xp = lb.formats.pad_acts(x, W.kp)
+    ref, bound = O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros), O.fp_bound(xp, W.dequantize())
+    O.assert_fp_close(K.gemm_w4a16(x, W, isa=isa), ref, bound, RTOL)
+    with K.implicit_residency(True):
+        O.assert_fp_close(K.gemm_w4a16(x, lb.to_device(W), isa=isa), ref, bound, RTOL)
 
 
 @pytest.mark.parametrize("isa", PATHS)

@@ -1,0 +1,93 @@
+"""A seeded sweep of shapes (GPU) through every call route, against the oracle.
+
+The fixed-shape tests pin each kernel at chosen shapes; this sweep draws 20 shapes per
+format and route with M on and around every regime boundary (the one-row GEMV, the
+M <= 4 VALU kernels, 16-row MFMA tiles and their tails, 64-row tiles, wide M), N with
+ragged 16-row subtiles and K not a multiple of the group or block (the caller's X is
+padded, as the reference pads it, src/lowbit/formats.py:227-233), and activations that
+are Gaussian, heavy-tailed with outliers, or hold an all-zero row. Routes: the
+host-pointer ABI (weights uploaded per call), implicit residency (host containers made
+resident on their first call) and explicit `to_device` handles. Bar: the reference's
+bounds (tests/conftest.py:22-27, tests/test_kernels.py:108-116 of the reference):
+1e-5 * (|X| @ |W|^T) for W4A16 / MXFP4 and the W4A8 lane bound on the oracle's codes.
+"""
+import numpy as np
+import pytest
+
+import lowbit_amd as lb
+from lowbit_amd import kernels as K
+from oracle import cref
+from oracle import reference as O
+
+pytestmark = pytest.mark.gpu
+
+M_CHOICES = [1, 1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 47, 48, 63, 64, 65, 80, 130]
+ROUTES = ["pointer", "implicit", "handle"]
+RTOL = 1e-5
+
+
+def shapes(seed: int, count: int = 20):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        m = M_CHOICES[i % len(M_CHOICES)]
+        n = int(rng.choice([int(rng.integers(1, 600)), 16 * int(rng.integers(1, 40)) + int(rng.choice([-1, 0, 1]))]))
+        k = int(rng.choice([int(rng.integers(1, 2600)), 128 * int(rng.integers(1, 20)), 32 * int(rng.integers(1, 80))]))
+        out.append((m, max(n, 1), max(k, 1)))
+    return out
+
+
+def activations(rng, m, k, kind):
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if kind == 1:  # heavy tails: a few outliers per row, 1e3 times the rest
+        idx = rng.integers(0, k, (m, max(1, k // 200)))
+        np.put_along_axis(x, idx, rng.standard_normal(idx.shape).astype(np.float32) * 1e3, axis=1)
+    elif kind == 2 and m > 1:
+        x[m // 2] = 0.0
+    return x
+
+
+def run(fmt, route, x, W):
+    fn = {"w4a16": K.gemm_w4a16, "w4a8": K.gemm_w4a8, "mxfp4": K.gemm_mxfp4}[fmt]
+    if route == "handle":
+        return fn(x, lb.to_device(W))
+    with K.implicit_residency(route == "implicit"):
+        y = fn(x, W)
+        if route == "implicit":
+            y2 = fn(x, W)  # the second call reads the resident copy
+            np.testing.assert_array_equal(y2, y)
+            lb.release(W)
+        return y
+
+
+@pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("fmt", ["w4a16", "w4a8", "mxfp4"])
+def test_random_shapes(fmt, route):
+    seed = 20261202 + 97 * ["w4a16", "w4a8", "mxfp4"].index(fmt) + ROUTES.index(route)
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    for i, (m, n, k) in enumerate(shapes(seed)):
+        kind = i % 3
+        asym = bool(i % 2) and fmt != "mxfp4"
+        print(f"[{fmt} {route}] shape {i}: M={m} N={n} K={k} asym={asym} acts={kind}", flush=True)
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        x = activations(rng, m, k, kind)
+        if fmt == "mxfp4":
+            W = lb.quantize_mxfp4(w)
+            xp = lb.formats.pad_acts(x, W.kp)
+            ref, bound = O.gemm_mxfp4_ref(xp, W.qw, W.e8m0), cref.c_gemm_mxfp4(xp, W.qw, W.e8m0, absval=True)
+        elif fmt == "w4a16":
+            W = lb.quantize_int4(w, asym=asym)
+            xp = lb.formats.pad_acts(x, W.kp)
+            ref = O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros)
+            bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
+        else:
+            W = lb.quantize_int4(w, asym=asym)
+            a = lb.quantize_act_int8(x)
+            ref, bound = cref.c_gemm_w4a8(a.xq, a.scale, a.gsum, W.qw, W.scales, W.zeros)
+        y = run(fmt, route, x, W)
+        assert y.shape == (m, n) and y.dtype == np.float32
+        worst = max(worst, O.assert_fp_close(y, ref, bound, RTOL))
+        if kind == 2 and m > 1:
+            assert not y[m // 2].any()  # a zero activation row gives exact zeros
+    print(f"[{fmt} {route}] worst err / limit {worst:.3g}")
