@@ -5,7 +5,9 @@ format and route with M on and around every regime boundary (the one-row GEMV, t
 M <= 4 VALU kernels, 16-row MFMA tiles and their tails, 64-row tiles, wide M), N with
 ragged 16-row subtiles and K not a multiple of the group or block (the caller's X is
 padded, as the reference pads it, src/lowbit/formats.py:227-233), and activations that
-are Gaussian, heavy-tailed with outliers, or hold an all-zero row. Routes: the
+are Gaussian, heavy-tailed with outliers, hold an all-zero row, sit at 1e-30 or 1e15,
+spread over many exponents or are mostly zeros; weight rows are Gaussian, spread over
+exponents, zero or dominated by one entry. Routes: the
 host-pointer ABI (weights uploaded per call), implicit residency (host containers made
 resident on their first call) and explicit `to_device` handles. Bar: the reference's
 bounds (tests/conftest.py:22-27, tests/test_kernels.py:108-116 of the reference):
@@ -37,6 +39,9 @@ def shapes(seed: int, count: int = 20):
     return out
 
 
+ACT_KINDS = 6
+
+
 def activations(rng, m, k, kind):
     x = rng.standard_normal((m, k)).astype(np.float32)
     if kind == 1:  # heavy tails: a few outliers per row, 1e3 times the rest
@@ -44,7 +49,23 @@ def activations(rng, m, k, kind):
         np.put_along_axis(x, idx, rng.standard_normal(idx.shape).astype(np.float32) * 1e3, axis=1)
     elif kind == 2 and m > 1:
         x[m // 2] = 0.0
+    elif kind == 3:  # tiny (1e-30) and huge (1e15) rows, far from 1 in both directions
+        x *= np.where(np.arange(m)[:, None] % 2 == 0, 1e-30, 1e15).astype(np.float32)
+    elif kind == 4:  # rows of very different scale: LogNormal(0, 3) per row
+        x *= np.exp(rng.normal(0.0, 3.0, (m, 1))).astype(np.float32)
+    elif kind == 5:  # sparse: about 90 % exact zeros
+        x *= (rng.random((m, k)) < 0.1).astype(np.float32)
     return x
+
+
+def weights(rng, n, k, kind):
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    if kind == 1:  # rows spread over many exponents (the C4 rows of BASELINE)
+        w *= np.exp(rng.normal(0.0, 0.5, (n, 1))).astype(np.float32)
+    elif kind == 2 and n > 2:  # a zero row and a row with one dominant entry
+        w[0] = 0.0
+        w[1, rng.integers(0, k)] = 1e4
+    return w
 
 
 def run(fmt, route, x, W):
@@ -67,10 +88,10 @@ def test_random_shapes(fmt, route):
     rng = np.random.default_rng(seed)
     worst = 0.0
     for i, (m, n, k) in enumerate(shapes(seed)):
-        kind = i % 3
+        kind, wkind = i % ACT_KINDS, (i // 2) % 3
         asym = bool(i % 2) and fmt != "mxfp4"
-        print(f"[{fmt} {route}] shape {i}: M={m} N={n} K={k} asym={asym} acts={kind}", flush=True)
-        w = rng.standard_normal((n, k)).astype(np.float32)
+        print(f"[{fmt} {route}] shape {i}: M={m} N={n} K={k} asym={asym} acts={kind} weights={wkind}", flush=True)
+        w = weights(rng, n, k, wkind)
         x = activations(rng, m, k, kind)
         if fmt == "mxfp4":
             W = lb.quantize_mxfp4(w)
