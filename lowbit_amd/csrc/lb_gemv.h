@@ -122,58 +122,78 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
 // ---- per-chunk arithmetic, shared by gemv_kernel and gemv_paced_kernel so that the
 //      two give the same bits
 
-// W4A16: the codes of one 32-bit word of a chunk (four low nibbles, four high nibbles)
-// as the two's complement bytes q - z, for any zero-point z in 0..15: 128 - z is added
-// to every byte holding a nibble q (each stays within 113..143, so no carry crosses a
-// byte) and bit 7 is flipped back. One conversion then sign-extends and converts each
-// byte (v_cvt_f32_i32 with a sign-extended byte source), so the products below are
-// those of the dequantized weight, as the reference forms them
+// W4A16: the codes of one 32-bit word of a chunk as float16 pairs of the dequantized
+// integers, exactly, for any zero-point z in 0..15. A nibble n masked into the low
+// mantissa bits of a half under the exponent of 1024 is the float16 1024 + n (or, left
+// in bits 4..7, 1024 + 16 n); subtracting 1024 + z (1024 + 16 z) in float16 is exact
+// and leaves n - z (16 (n - z)). Pairs: p0 = (low nibbles of bytes 0, 2), p1 = (high
+// nibbles of bytes 0, 2) times 16, p2 = (low nibbles of bytes 1, 3), p3 = (high
+// nibbles of bytes 1, 3) times 16. The FMAs then take the half-precision integers
+// directly (v_fma_mix_f32: the conversion to fp32 is exact and the FMA rounds once),
+// so the products are those of the dequantized weight, as the reference forms them
 // (src/lowbit/csrc/kern_scalar.c:10-29), and a row's fp32 rounding stays relative to
 // sum |q - z| |x|, the bound's scale, even where a large activation meets a code equal
 // to the zero-point (the split sum q x - z sum x rounds relative to sum q |x|).
-__device__ __forceinline__ uint32_t w4a16_bias(int z) { return 0x80808080u - (uint32_t)z * 0x01010101u; }
-__device__ __forceinline__ uint32_t w4a16_lo(uint32_t w, uint32_t bias) {
-  return ((w & 0x0F0F0F0Fu) + bias) ^ 0x80808080u;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+struct W16Zero {
+  h2 lo, hi;  // (1024 + z) and (1024 + 16 z), both halves
+};
+__device__ __forceinline__ W16Zero w4a16_zero(int z) {
+  return {__builtin_bit_cast(h2, (0x6400u | (uint32_t)z) * 0x00010001u),
+          __builtin_bit_cast(h2, (0x6400u | (uint32_t)(16 * z)) * 0x00010001u)};
 }
-__device__ __forceinline__ uint32_t w4a16_hi(uint32_t w, uint32_t bias) {
-  return (((w >> 4) & 0x0F0F0F0Fu) + bias) ^ 0x80808080u;
+// (w & mask) | (f & ~mask) in one instruction (v_bfi_b32; the compiler splits the
+// constant form into an AND and an OR)
+__device__ __forceinline__ uint32_t bit_select(uint32_t mask, uint32_t w, uint32_t f) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(w), "v"(f));
+  return r;
 }
-__device__ __forceinline__ float sbyte(uint32_t v, int k) { return (float)(int8_t)(v >> (8 * k)); }
+__device__ __forceinline__ void w4a16_pairs(uint32_t w, const W16Zero &zz, h2 (&p)[4]) {
+  const uint32_t w8 = w >> 8, e = 0x64006400u;  // e: the exponent of 1024 in both halves
+  p[0] = __builtin_bit_cast(h2, bit_select(0x000F000Fu, w, e)) - zz.lo;
+  p[1] = __builtin_bit_cast(h2, bit_select(0x00F000F0u, w, e)) - zz.hi;
+  p[2] = __builtin_bit_cast(h2, bit_select(0x000F000Fu, w8, e)) - zz.lo;
+  p[3] = __builtin_bit_cast(h2, bit_select(0x00F000F0u, w8, e)) - zz.hi;
+}
 
-// W4A16: sum_k (q_k - z) x_k of one 16-byte chunk (low-nibble half, then high-nibble
-// half, each in element order).
+// W4A16: sum_k (q_k - z) x_k of one 16-byte chunk: the low-nibble half in element
+// order, then the high-nibble half (accumulated at 16 times its value, then scaled
+// back: a power of two, so the same roundings as at its own scale).
 __device__ __forceinline__ float w4a16_chunk(uint4 w, const float4 (&xv)[8], int z) {
-  const uint32_t bias = w4a16_bias(z);
+  const W16Zero zz = w4a16_zero(z);
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   float pl = 0.0f, ph = 0.0f;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
-    const uint32_t lo = w4a16_lo(wd[d], bias), hi = w4a16_hi(wd[d], bias);
-    pl = __builtin_fmaf(sbyte(lo, 0), xv[d].x, pl);
-    pl = __builtin_fmaf(sbyte(lo, 1), xv[d].y, pl);
-    pl = __builtin_fmaf(sbyte(lo, 2), xv[d].z, pl);
-    pl = __builtin_fmaf(sbyte(lo, 3), xv[d].w, pl);
-    ph = __builtin_fmaf(sbyte(hi, 0), xv[4 + d].x, ph);
-    ph = __builtin_fmaf(sbyte(hi, 1), xv[4 + d].y, ph);
-    ph = __builtin_fmaf(sbyte(hi, 2), xv[4 + d].z, ph);
-    ph = __builtin_fmaf(sbyte(hi, 3), xv[4 + d].w, ph);
+    h2 p[4];
+    w4a16_pairs(wd[d], zz, p);
+    pl = __builtin_fmaf((float)p[0].x, xv[d].x, pl);
+    pl = __builtin_fmaf((float)p[2].x, xv[d].y, pl);
+    pl = __builtin_fmaf((float)p[0].y, xv[d].z, pl);
+    pl = __builtin_fmaf((float)p[2].y, xv[d].w, pl);
+    ph = __builtin_fmaf((float)p[1].x, xv[4 + d].x, ph);
+    ph = __builtin_fmaf((float)p[3].x, xv[4 + d].y, ph);
+    ph = __builtin_fmaf((float)p[1].y, xv[4 + d].z, ph);
+    ph = __builtin_fmaf((float)p[3].y, xv[4 + d].w, ph);
   }
-  return pl + ph;
+  return pl + ph * 0.0625f;
 }
 
-// W4A16: the 32 codes of one chunk as the exact floats q - z (low-nibble half in wl,
-// high-nibble half in wh), for rows used against several activation rows.
+// W4A16: the 32 codes of one chunk as exact floats (q - z) for the low-nibble half in
+// wl and 16 (q - z) for the high-nibble half in wh (chunk_dot<4> scales that half
+// back), for rows used against several activation rows.
 __device__ __forceinline__ void w4a16_decode(uint4 w, int z, float (&wl)[16], float (&wh)[16]) {
-  const uint32_t bias = w4a16_bias(z);
+  const W16Zero zz = w4a16_zero(z);
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int d = 0; d < 4; d++) {
-    const uint32_t lo = w4a16_lo(wd[d], bias), hi = w4a16_hi(wd[d], bias);
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      wl[4 * d + u] = sbyte(lo, u);
-      wh[4 * d + u] = sbyte(hi, u);
-    }
+    h2 p[4];
+    w4a16_pairs(wd[d], zz, p);
+    wl[4 * d + 0] = (float)p[0].x; wl[4 * d + 1] = (float)p[2].x;
+    wl[4 * d + 2] = (float)p[0].y; wl[4 * d + 3] = (float)p[2].y;
+    wh[4 * d + 0] = (float)p[1].x; wh[4 * d + 1] = (float)p[3].x;
+    wh[4 * d + 2] = (float)p[1].y; wh[4 * d + 3] = (float)p[3].y;
   }
 }
 
@@ -194,6 +214,7 @@ __device__ __forceinline__ void mxfp4_decode(uint4 w, float (&wl)[16], float (&w
 // sum_k w_k x_k of one chunk's decoded codes (MXFP4 before the block scale, W4A16
 // before the group scale): low-nibble half, then high-nibble half, each in element
 // order (the order of w4a16_chunk).
+template <int HSHIFT = 0>
 __device__ __forceinline__ float chunk_dot(const float (&wl)[16], const float (&wh)[16], const float4 (&xv)[8]) {
   float pl = 0.0f, ph = 0.0f;
 #pragma unroll
@@ -207,7 +228,8 @@ __device__ __forceinline__ float chunk_dot(const float (&wl)[16], const float (&
     ph = __builtin_fmaf(wh[4 * d + 2], xv[4 + d].z, ph);
     ph = __builtin_fmaf(wh[4 * d + 3], xv[4 + d].w, ph);
   }
-  return pl + ph;
+  // the high half decoded at 2^HSHIFT times its value (W4A16: 16), scaled back exactly
+  return HSHIFT ? pl + ph * (1.0f / (float)(1 << HSHIFT)) : pl + ph;
 }
 
 // W4A8: the exact int32 sum_k q_k a_k of one chunk (int8 dot4 on the unsigned codes,
@@ -253,7 +275,8 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
           for (int p = 0; p < 8; p++)
             xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], chunk_dot(wl, wh, xv), acc[m][r]);
+          const float part = F == F_MXFP4 ? chunk_dot(wl, wh, xv) : chunk_dot<4>(wl, wh, xv);
+          acc[m][r] = __builtin_fmaf(g.sc[r][it], part, acc[m][r]);
         }
       }
     } else {
@@ -636,15 +659,39 @@ __device__ __forceinline__ void paced_load(const GemmArgs &a, PacedStage<NIT> &s
   } else {
     const Rsrc rs = make_rsrc(a.scales + rr * G, in ? (uint32_t)G * 4 : 0u);
     const Rsrc rz = make_rsrc(a.zeros ? a.zeros + rr * G : a.qw, (in && a.zeros) ? (uint32_t)G : 0u);
+    auto gidx = [&](int it) {
+      const uint32_t ci = cbase + (uint32_t)lane + kWave * it;
+      return fmt_g32(F) ? ci : ci >> 2;
+    };
+    auto zload = [&](int it) {
+      if constexpr (DW) st.z[it] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)(gidx(it) & ~3u), 0, kPacedAux);
+      else st.z[it] = __builtin_amdgcn_raw_buffer_load_b8(rz, (int)gidx(it), 0, kPacedAux);
+    };
+    if constexpr (F == F_W4A16 || F == F_W4A16G32) {
+      // loads return in issue order, and W4A16 needs every chunk's zero-point before
+      // its products (q - z) and the scales after them: the zero-points first, then
+      // the weights chunk by chunk, then the scales
 #pragma unroll
-    for (int it = 0; it < NIT; it++) {
-      const uint32_t ci = cbase + (uint32_t)lane + kWave * it, gi = fmt_g32(F) ? ci : ci >> 2;
-      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
-      st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
-      st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gi * 4), 0, kPacedAux);
-      if constexpr (DW) st.z[it] = __builtin_amdgcn_raw_buffer_load_b32(rz, (int)(gi & ~3u), 0, kPacedAux);
-      else st.z[it] = __builtin_amdgcn_raw_buffer_load_b8(rz, (int)gi, 0, kPacedAux);
+      for (int it = 0; it < NIT; it++) zload(it);
+#pragma unroll
+      for (int it = 0; it < NIT; it++) {
+        const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)((cbase + lane + kWave * it) * 16), 0, kPacedAux);
+        st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int it = 0; it < NIT; it++) st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gidx(it) * 4), 0, kPacedAux);
       __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int it = 0; it < NIT; it++) {
+        const uint32_t ci = cbase + (uint32_t)lane + kWave * it;
+        const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(ci * 16), 0, kPacedAux);
+        st.w[it] = make_uint4(v.x, v.y, v.z, v.w);
+        st.s[it] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(gidx(it) * 4), 0, kPacedAux);
+        zload(it);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 }
