@@ -112,3 +112,32 @@ def test_random_shapes(fmt, route):
         if kind == 2 and m > 1:
             assert not y[m // 2].any()  # a zero activation row gives exact zeros
     print(f"[{fmt} {route}] worst err / limit {worst:.3g}")
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "mxfp4"])
+@pytest.mark.parametrize("m", [1, 3, 16, 64])
+@pytest.mark.parametrize("mag", [1e-36, 1e-33, 1e-30, 1e-10, 1e10, 1e30])
+def test_activation_magnitudes(fmt, m, mag):
+    """Rows of one magnitude far from 1, through the GEMVs (M <= 4) and the bf16x3
+    matrix cores (M >= 5), whose three bf16 terms keep fp32's 24 bits down to rows of
+    1e-36 (below that the matrix cores flush the smallest term)."""
+    rng = np.random.default_rng(int(abs(np.log10(mag))) * 10 + m)
+    n, k = 96, 1024
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    x = (rng.standard_normal((m, k)) * mag).astype(np.float32)
+    if fmt == "mxfp4":
+        W = lb.quantize_mxfp4(w)
+        xp = lb.formats.pad_acts(x, W.kp)
+        ref, bound = O.gemm_mxfp4_ref(xp, W.qw, W.e8m0), cref.c_gemm_mxfp4(xp, W.qw, W.e8m0, absval=True)
+        y = K.gemm_mxfp4(x, lb.to_device(W))
+    else:
+        W = lb.quantize_int4(w, asym=True)
+        xp = lb.formats.pad_acts(x, W.kp)
+        ref = O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros)
+        bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
+        y = K.gemm_w4a16(x, lb.to_device(W))
+    assert np.isfinite(y).all()
+    # assert_fp_close's absolute floor (1e-30) would hide errors at these magnitudes
+    err = np.abs(y.astype(np.float64) - ref)
+    worst = float((err / (RTOL * bound + 1e-300)).max())
+    assert worst <= 1.0, f"max err/limit = {worst:.3g}"
