@@ -426,7 +426,7 @@ void gemv_kernel(GemmArgs a) {
       xr[i].w = xr[i].w * rn * xe[i].w;
     }
   } else if constexpr (PRO == 3) {
-    xr[0] = threadIdx.x * 4 < Kp ? attn_merge8(apt[0], a.attn_ns) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    xr[0] = (int)threadIdx.x * 4 < Kp ? attn_merge8(apt[0], a.attn_ns) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   } else if constexpr (PRO == 2) {
 #pragma unroll
     for (int i = 0; i < S; i++) {
