@@ -42,13 +42,10 @@ def _run(fmt, D, x, m, split, f8=False):
     return dy.to_array((m, D.n), np.float32)
 
 
-@pytest.mark.parametrize("fmt", ["w4a16", "mxfp4"])
+@pytest.mark.parametrize("fmt,asym", [("w4a16", False), ("w4a16", True), ("mxfp4", False)])  # MXFP4: no zero-point
 @pytest.mark.parametrize("m,n,k", [(16, 520, 11008), (64, 300, 11008), (5, 77, 8200), (16, 96, 16384),
                                    (128, 200, 11008)])
-@pytest.mark.parametrize("asym", [False, True])
-def test_split_within_bound(rng, fmt, m, n, k, asym):
-    if fmt == "mxfp4" and asym:
-        pytest.skip("MXFP4 has no zero-point")
+def test_split_within_bound(rng, fmt, asym, m, n, k):
     x = rng.standard_normal((m, k)).astype(np.float32)
     w = (rng.standard_normal((n, k)) * rng.lognormal(0, 0.5, (n, 1))).astype(np.float32)
     W = lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=asym)
