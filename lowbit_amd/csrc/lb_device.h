@@ -61,6 +61,41 @@ __device__ __forceinline__ float wave_max(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Lane `lane` (wave-uniform) of v takes the wave-uniform value `bits`; the other
+// lanes keep theirs (v_writelane_b32, which clang exposes as no builtin; the lane
+// select goes through M0, as gfx9 reads one scalar register per VALU instruction).
+__device__ __forceinline__ void write_lane(float &v, int bits, int lane) {
+  asm("s_mov_b32 m0, %2\n\ts_nop 0\n\tv_writelane_b32 %0, %1, m0" : "+v"(v) : "s"(bits), "s"(lane) : "m0");
+}
+
+// Max over the wave of 64-bit keys (unsigned); every lane gets it. Each step moves
+// both halves by the same DPP pattern; lanes the pattern leaves out read 0, which
+// is below every key.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROWS, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROWS, 0xF, false);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  unsigned long long o;
+  o = dpp_u64<kDppQuad1032>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<kDppQuad2301>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<kDppRowHalfMirror>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<kDppRowMirror>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<kDppRowBcast15, 0xA>(v);
+  v = o > v ? o : v;
+  o = dpp_u64<kDppRowBcast31, 0xC>(v);
+  v = o > v ? o : v;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
 // Sum over each 32-lane half of the wave; the totals land in lanes 31 and 63
 // (other lanes hold partial sums).
 __device__ __forceinline__ int half_wave_sum(int v) {

@@ -90,8 +90,11 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int row = rb + (HW ? 2 * r : r);
-    const uint32_t nrows = row < rend ? ((HW && row + 1 < rend) ? 2u : 1u) : 0u;
-    const size_t rr = nrows ? (size_t)row : 0;
+    // wave-uniform; read back into scalar registers, since the compiler otherwise
+    // forms these selects on the vector unit and then loops over the lanes'
+    // descriptors one distinct value at a time
+    const uint32_t nrows = __builtin_amdgcn_readfirstlane(row < rend ? ((HW && row + 1 < rend) ? 2u : 1u) : 0u);
+    const size_t rr = (size_t)__builtin_amdgcn_readfirstlane(nrows ? row : 0);
     const Rsrc rw = make_rsrc(a.qw + rr * rowbytes, nrows * rowbytes);
     if constexpr (F == F_MXFP4) {
       const Rsrc re = make_rsrc(a.e8m0 + rr * nch, nrows * (uint32_t)nch);
@@ -381,19 +384,18 @@ void gemv_kernel(GemmArgs a) {
 
   // ---- 2. the weight stream of this wave's first R rows, then their epilogue
   //         operands (bias, residual), so that the epilogue waits for no load
+  //         (the epilogue runs once per window of up to WN rows, one row per lane:
+  //         lane j's operands are those of row wb + j)
   GemvRegs<F, R, NIT> g;
-  float bv[RR], rv[MB][RR];
-  auto epi_load = [&](int rb) {
+  float bv = 0.0f, rv[MB];
+  auto epi_load = [&](int wb) {
+    const int n = wb + lane < N ? wb + lane : N - 1;  // rows past the share are never stored
+    if (a.bias) bv = a.bias[n];
 #pragma unroll
-    for (int r = 0; r < RR; r++) {
-      const int n = rb + r < N ? rb + r : N - 1;  // rows past the share are never stored
-      bv[r] = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-      for (int m = 0; m < MB; m++) rv[m][r] = a.res ? a.res[(size_t)m * N + n] : 0.0f;
-    }
+    for (int m = 0; m < MB; m++) rv[m] = a.res ? a.res[(size_t)m * N + n] : 0.0f;
   };
+  epi_load(r0);  // ahead of the weights: a wait for the weights then covers these too
   gemv_load<F, R, NIT, HW>(a, g, r0, r1, lane, nch, G);
-  epi_load(r0);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. fused prologue, then stage the activations into LDS while the weights
@@ -530,65 +532,67 @@ void gemv_kernel(GemmArgs a) {
   __syncthreads();
 
   // ---- 4. decode + accumulate R rows at a time; later batches load as the
-  //         previous one finishes
-  unsigned long long best = 0;  // argmax key of this wave's outputs
-  float tg[MB];                 // glu: the gate output of the pair in progress (rows in order)
+  //         previous one finishes. Each row's total goes to lane (row - wb) of
+  //         `sum` for a window of WN rows starting at wb (a whole number of batches,
+  //         even, so that glu pairs never straddle windows); the epilogue then runs
+  //         once per window with one row per lane and one coalesced store.
+  constexpr int WN = (RR & 1) ? (kWave / (2 * RR)) * (2 * RR) : (kWave / RR) * RR;
+  unsigned long long best = 0;  // this lane's argmax key over the wave's windows
+  float sum[MB];
+  for (int wb = r0; wb < r1; wb += WN) {
+    const int we = min(wb + WN, r1);
+    if (wb != r0) epi_load(wb);
 #pragma unroll
-  for (int m = 0; m < MB; m++) tg[m] = 0.0f;
-  for (int rb = r0; rb < r1; rb += RR) {
-    if (rb != r0) {
-      gemv_load<F, R, NIT, HW>(a, g, rb, r1, lane, nch, G);
-      epi_load(rb);
-    }
-    const int nr = min(RR, r1 - rb);          // rows of this batch
-    const int ns = HW ? (nr + 1) >> 1 : nr;   // slots holding them
-    float acc[MB][R];
+    for (int m = 0; m < MB; m++) sum[m] = 0.0f;
+    for (int rb = wb; rb < we; rb += RR) {
+      if (rb != r0) gemv_load<F, R, NIT, HW>(a, g, rb, r1, lane, nch, G);
+      const int nr = min(RR, r1 - rb);          // rows of this batch
+      const int ns = HW ? (nr + 1) >> 1 : nr;   // slots holding them
+      float acc[MB][R];
 #pragma unroll
-    for (int m = 0; m < MB; m++)
+      for (int m = 0; m < MB; m++)
 #pragma unroll
-      for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
-    gemv_compute<F, MB, R, NIT, HW>(g, acc, ns, lane, nchp, Gp, xl, ql, asl);
-    // ---- 5. one wave (HW: half-wave) reduction per output (every lane gets it),
-    //         the epilogue, and lane m*RR + r stores it
+        for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
+      gemv_compute<F, MB, R, NIT, HW>(g, acc, ns, lane, nchp, Gp, xl, ql, asl);
+      // ---- 5. one wave (HW: half-wave) reduction per output, into its lane of `sum`
 #pragma unroll
-    for (int m = 0; m < MB; m++) {
-      float tt[RR];
+      for (int m = 0; m < MB; m++) {
 #pragma unroll
-      for (int r = 0; r < R; r++) {
-        if (r >= ns) break;
-        if constexpr (HW) {
-          const float v = half_wave_sum_f(acc[m][r]);
-          tt[2 * r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
-          tt[2 * r + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-        } else {
-          tt[r] = wave_sum(acc[m][r]);
+        for (int r = 0; r < R; r++) {
+          if (r >= ns) break;
+          if constexpr (HW) {
+            const float v = half_wave_sum_f(acc[m][r]);
+            const int j = rb + 2 * r - wb;
+            write_lane(sum[m], __builtin_amdgcn_readlane(__float_as_int(v), 31), j);
+            write_lane(sum[m], __builtin_amdgcn_readlane(__float_as_int(v), 63), j + 1);
+          } else {
+            write_lane(sum[m], __float_as_int(wave_sum(acc[m][r])), rb + r - wb);
+          }
         }
       }
+    }
+    // ---- 6. the window's epilogue: lane j holds row n = wb + j
+    const int n = wb + lane;
+    const bool live = n < we;
 #pragma unroll
-      for (int r = 0; r < RR; r++) {
-        if (r >= nr) break;
-        float t = tt[r];
-        const int n = rb + r;
-        size_t o = (size_t)m * N + n;
-        {
-          // y is rounded before the bias and the residual are added, as separate
-          // float32 adds after the GEMM would round it (no fused multiply-add)
+    for (int m = 0; m < MB; m++) {
+      float t = sum[m];
+      {
+        // y is rounded before the bias and the residual are added, as separate
+        // float32 adds after the GEMM would round it (no fused multiply-add)
 #pragma clang fp contract(off)
-          if constexpr (kInt8) t *= xsl[m];
-          if (a.bias) t += bv[r];
-          if (a.res) t = rv[m][r] + t;
-        }
-        if (a.glu) {
-          // wave-uniform: r0 is even, so even rows are gates and the next row is their up
-          if ((n & 1) == 0) {
-            tg[m] = t;
-            continue;
-          }
-          t = tg[m] / (1.0f + expf(-tg[m])) * t;  // the SwiGLU kernel's expression
-          o = (size_t)m * (N >> 1) + (n >> 1);
-        }
-        if (lane == m * RR + r) a.y[o] = t;
-        if (a.amax_key) {
+        if constexpr (kInt8) t *= xsl[m];
+        if (a.bias) t += bv;
+        if (a.res) t = rv[m] + t;
+      }
+      if (a.glu) {
+        // wb is even, so even lanes hold gates and the next lane their up row
+        const float up = dpp_f<kDppQuad1032>(t, 0.0f);
+        t = t / (1.0f + expf(-t)) * up;  // the SwiGLU kernel's expression
+        if (live && (lane & 1) == 0) a.y[(size_t)m * (N >> 1) + (n >> 1)] = t;
+      } else {
+        if (live) a.y[(size_t)m * N + n] = t;
+        if (a.amax_key && live) {
           const unsigned long long k = argmax_key(t, n);
           best = k > best ? k : best;
         }
@@ -596,7 +600,10 @@ void gemv_kernel(GemmArgs a) {
     }
   }
   // spread over the slots so that no address takes more than a few atomics
-  if (a.amax_key && lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
+  if (a.amax_key) {
+    best = wave_max_u64(best);
+    if (lane == 0 && best) atomicMax(a.amax_key + gw % kArgmaxSlots, best);
+  }
 }
 
 using GemvFn = void (*)(GemmArgs);
