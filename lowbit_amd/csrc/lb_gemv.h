@@ -72,6 +72,10 @@ struct GemvRegs {
   uint4 w[R][NIT];
   float sc[R][NIT];
   int zi[R][NIT];
+  // two rows per wave load, int4: the scales and zero-points of the batch's rows,
+  // one per lane (lane j: entry j of the rows' contiguous metadata)
+  float scb;
+  int zb;
 };
 
 // Rows rb .. rb+R-1; rows at or past `rend` get zero-length descriptors (read 0).
@@ -87,6 +91,22 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
   constexpr bool kG32 = fmt_g32(F);
   const uint32_t half = HW ? (uint32_t)lane >> 5 : 0u;
   const uint32_t cl = HW ? (uint32_t)lane & 31u : (uint32_t)lane;
+  constexpr bool kBatchMeta = HW && F != F_MXFP4;
+  if constexpr (kBatchMeta) {
+    // the metadata of the batch's 2R rows (at most 2R * 8 <= 64 entries: rows of at
+    // most 1024 elements) in one load per array instead of one per slot; gemv_compute
+    // hands each lane its own entry by a cross-lane permute
+    const uint32_t nb = __builtin_amdgcn_readfirstlane(rb < rend ? min(rend - rb, 2 * R) : 0);
+    const size_t rbb = (size_t)__builtin_amdgcn_readfirstlane(nb ? rb : 0);
+    const Rsrc rs = make_rsrc(a.scales + rbb * G, nb * (uint32_t)G * 4);
+    g.scb = ld_f32(rs, (uint32_t)lane * 4);
+    if (a.zeros) {
+      const Rsrc rz = make_rsrc(a.zeros + rbb * G, nb * (uint32_t)G);
+      g.zb = (int)ld_u8(rz, (uint32_t)lane);
+    } else {
+      g.zb = zadd;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int row = rb + (HW ? 2 * r : r);
@@ -114,6 +134,7 @@ __device__ __forceinline__ void gemv_load(const GemmArgs &a, GemvRegs<F, R, NIT>
         const uint32_t ci = cl + kWave * it;
         const bool live = !HW || ci < (uint32_t)nch;
         g.w[r][it] = ld_b128(rw, live ? half * rowbytes + ci * 16 : 2 * rowbytes);
+        if constexpr (kBatchMeta) continue;
         const uint32_t gi = kG32 ? ci : ci >> 2;  // the chunk's group
         g.sc[r][it] = ld_f32(rs, live ? (half * (uint32_t)G + gi) * 4 : 2 * (uint32_t)G * 4);
         g.zi[r][it] = (int)ld_u8(rz, live ? half * (uint32_t)G + gi : 2 * (uint32_t)G) + zadd;
@@ -255,8 +276,22 @@ __device__ __forceinline__ int w4a8_chunk(uint4 w, uint4 al, uint4 ah) {
 // weights, zero scales and zero activations.
 template <int F, int MB, int R, int NIT, bool HW>
 __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float (&acc)[MB][R], int nr, int lane,
-                                             int nchp, int Gp, const float *xl, const uint8_t *ql,
+                                             int nchp, int Gp, int G, const float *xl, const uint8_t *ql,
                                              const int32_t *asl) {
+  // the scale and zero-point of this lane's chunk in slot r (two rows per wave load,
+  // int4: fetched from the lane holding it; lanes past the row's chunks get scale 0,
+  // as their own loads past the row would have given)
+  auto meta = [&](int r, int it, float &sc, int &zi) {
+    if constexpr (HW && F != F_MXFP4) {
+      const int ci = lane & 31, idx = (2 * r + (lane >> 5)) * G + (ci >> 2);
+      const float v = __int_as_float(__builtin_amdgcn_ds_bpermute(idx * 4, __float_as_int(g.scb)));
+      sc = ci < 4 * G ? v : 0.0f;
+      zi = __builtin_amdgcn_ds_bpermute(idx * 4, g.zb);
+    } else {
+      sc = g.sc[r][it];
+      zi = g.zi[r][it];
+    }
+  };
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
     const int ci = (HW ? lane & 31 : lane) + kWave * it;
@@ -266,11 +301,13 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
       for (int r = 0; r < R; r++) {
         if (r >= nr) break;
-        float wl[16], wh[16];
+        float wl[16], wh[16], sc;
+        int zi;
+        meta(r, it, sc, zi);
         if constexpr (F == F_MXFP4) {
           mxfp4_decode(g.w[r][it], wl, wh);
         } else {
-          w4a16_decode(g.w[r][it], g.zi[r][it], wl, wh);
+          w4a16_decode(g.w[r][it], zi, wl, wh);
         }
 #pragma unroll
         for (int m = 0; m < MB; m++) {
@@ -279,7 +316,7 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
           for (int p = 0; p < 8; p++)
             xv[p] = *reinterpret_cast<const float4 *>(xl + ((size_t)(m * 8 + p) * nchp + ci) * 4);
           const float part = F == F_MXFP4 ? chunk_dot(wl, wh, xv) : chunk_dot<4>(wl, wh, xv);
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], part, acc[m][r]);
+          acc[m][r] = __builtin_fmaf(sc, part, acc[m][r]);
         }
       }
     } else {
@@ -296,9 +333,12 @@ __device__ __forceinline__ void gemv_compute(const GemvRegs<F, R, NIT> &g, float
 #pragma unroll
         for (int r = 0; r < R; r++) {
           if (r >= nr) break;
+          float sc;
+          int zi;
+          meta(r, it, sc, zi);
           int d = w4a8_chunk(g.w[r][it], al, ah);
-          d -= g.zi[r][it] * as;
-          acc[m][r] = __builtin_fmaf(g.sc[r][it], (float)d, acc[m][r]);
+          d -= zi * as;
+          acc[m][r] = __builtin_fmaf(sc, (float)d, acc[m][r]);
         }
       }
     }
@@ -553,7 +593,7 @@ void gemv_kernel(GemmArgs a) {
       for (int m = 0; m < MB; m++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[m][r] = 0.0f;
-      gemv_compute<F, MB, R, NIT, HW>(g, acc, ns, lane, nchp, Gp, xl, ql, asl);
+      gemv_compute<F, MB, R, NIT, HW>(g, acc, ns, lane, nchp, Gp, G, xl, ql, asl);
       // ---- 5. one wave (HW: half-wave) reduction per output, into its lane of `sum`
 #pragma unroll
       for (int m = 0; m < MB; m++) {
@@ -872,7 +912,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
         }
       }
       float ac[1][1] = {{0.0f}};
-      gemv_compute<F, 1, 1, NIT, false>(g, ac, 1, lane, nchp, Gp, xl, ql, asl);
+      gemv_compute<F, 1, 1, NIT, false>(g, ac, 1, lane, nchp, Gp, G, xl, ql, asl);
       acc = ac[0][0];
     }
     float t = wave_sum(acc);
