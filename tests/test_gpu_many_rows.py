@@ -9,7 +9,9 @@ MXFP4, the W4A8 lane bound on the oracle's codes; tests/conftest.py:22-27 and
 tests/test_kernels.py:108-116 of the reference) at one row (two rows per wave
 load) and three rows (one row per load), and, for the fused epilogues, bit for
 bit against the plain GEMV's output: fp32 `res + (y + bias)` in numpy, the SwiGLU
-pairs through lbd_swiglu_pairs, and numpy's argmax.
+pairs through lbd_swiglu_pairs, and numpy's argmax. Rows of 32 to 1024 elements
+on the two-rows-per-load path (each batch's metadata in one load per array) are
+checked at two row counts, with and without zero-points.
 """
 import numpy as np
 import pytest
@@ -99,3 +101,21 @@ def test_many_rows_glu_pairs(rng, fmt):
     ok(K.lib().lbd_swiglu_pairs(yp.ptr, 1, n // 2, ref.ptr, None))
     ok(fused(fmt, dw, dx.ptr, yg.ptr, glu=True))
     np.testing.assert_array_equal(yg.to_array((n // 2,), np.float32), ref.to_array((n // 2,), np.float32))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("k", [32, 96, 352, 1000, 1024])
+@pytest.mark.parametrize("n", [9000, 20011])
+def test_two_rows_per_load_row_lengths(rng, fmt, k, n):
+    """One activation row, rows of 1..8 groups (one to 32 chunks), two rows per wave
+    load with 1-3 slots per batch: each batch's scales and zero-points come in one
+    load each and reach their lanes by cross-lane permute. Symmetric and asymmetric
+    int4, against the oracle's bounds."""
+    for asym in ([False, True] if fmt != "mxfp4" else [False]):
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        W = lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=asym)
+        assert K.gemm_plan(fmt, 1, n, W.kp)["two_rows_per_load"] == 1
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        fn = {"w4a16": K.gemm_w4a16, "w4a8": K.gemm_w4a8, "mxfp4": K.gemm_mxfp4}[fmt]
+        y = fn(x, lb.to_device(W))
+        check_oracle(fmt, lb.formats.pad_acts(x, W.kp), W, y)
