@@ -961,13 +961,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_kernel(GemmArgs a) {
 // planes are padded to S * 128 chunks (zeros), so a slice past the row's end adds
 // exactly 0. (W4A8, whose int8 codes cost a quarter of the LDS bytes, measured no
 // faster this way: 8.48 -> 8.42 us cold, 7.51 -> 7.80 us hot at 1 x 4096 x 11008.)
+// WV waves per workgroup (a multiple of S where it matters: every slice then gets
+// as many waves as the others); SMAX the most slices the instantiation stages.
 constexpr int kSplitChunks = 2 * kWave;  // chunks per slice
 
-template <int F, bool DW>
-__global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs a) {
+template <int F, bool DW, int WV = kGemvWaves, int SMAX = 4>
+__global__ __launch_bounds__(WV * kWave) void gemv_paced_split_kernel(GemmArgs a) {
   static_assert(F == F_W4A16 || F == F_W4A16G32 || F == F_MXFP4, "fp32 activations");
   constexpr bool kW16 = (F == F_W4A16 || F == F_W4A16G32);
-  constexpr int T = kGemvThreads, NIT = 2, SX = kGemvMaxNit;  // X staging: up to 8 float4 per thread
+  // X staging: the float4 of up to SMAX slices over the workgroup's threads
+  constexpr int T = WV * kWave, NIT = 2, SX = (SMAX * kSplitChunks * 8 + T - 1) / T;
   extern __shared__ __align__(16) unsigned char lds[];
   const int Kp = a.Kp;
   const int nch = Kp >> 5;
@@ -991,7 +994,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
   const unsigned base = (unsigned)a.split_base, rem = (unsigned)a.split_rem;
   const int wr0 = (int)(bx * base + min(bx, rem)), wn = (int)(base + (bx < rem ? 1u : 0u));
   // slice sl of this wave, its index j among the P waves of that slice, its rows
-  const int sl = wave % S, j = wave / S, P = (kGemvWaves - 1 - sl) / S + 1;
+  const int sl = wave % S, j = wave / S, P = (WV - 1 - sl) / S + 1;
   const int r0 = wr0 + (j * wn) / P, r1 = wr0 + ((j + 1) * wn) / P;
   const uint32_t cb = (uint32_t)sl * kSplitChunks;
 
@@ -1004,7 +1007,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_paced_split_kernel(GemmArgs
   // ---- 2. stage the activations of all S slices into the LDS planes
 #pragma unroll
   for (int i = 0; i < SX; i++) {
-    if (i >= 2 * S) continue;  // block-uniform
+    if ((int)threadIdx.x + i * T >= S * kSplitChunks * 8) continue;  // past the S slices' float4
     int ci, half, within;
     chunk_pos(F, threadIdx.x * 4 + i * T * 4, ci, half, within);
     *reinterpret_cast<float4 *>(xl + ((size_t)(half * 4 + (within >> 2)) * nchp + ci) * 4) = xr[i];
@@ -1158,19 +1161,28 @@ static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipS
     // rows of more than 4096 elements: split over the waves, where the planes of
     // whole slices stay within the GEMV's LDS budget (rows up to 12288 elements)
     if (nit > 2 && gemv_split_lds_bytes(a.Kp, 0) <= kGemvLdsLimit) {
-      const GemvFn k = dw ? gemv_paced_split_kernel<F, true> : gemv_paced_split_kernel<F, false>;
       const int S = ((a.Kp >> 5) + kSplitChunks - 1) / kSplitChunks;
+      // waves per workgroup: the same number for every slice. Three slices: 12 waves
+      // (one workgroup per CU) against 8 (slices of 3, 3 and 2 waves, the last
+      // slice's waves taking half the rows each): 1 x 4096 x 11008 cold W4A16 8.0 ->
+      // 7.5 us, MXFP4 8.0 -> 7.5, 5-15 % at 4096 x 9000 and 11008 x 11008. Two slices:
+      // MXFP4 16 waves (one workgroup per CU) against 8 (two): 4096 x 8192 cold 5.7
+      // -> 5.2 us; W4A16 stays at 8 (16 measured 0-5 % slower)
+      constexpr int kW2 = F == F_MXFP4 ? 16 : kGemvWaves, kW3 = 12;
+      const int WV = S == 3 ? kW3 : kW2;
+      const GemvFn k = S == 3 ? (dw ? gemv_paced_split_kernel<F, true, kW3, 3> : gemv_paced_split_kernel<F, false, kW3, 3>)
+                              : (dw ? gemv_paced_split_kernel<F, true, kW2> : gemv_paced_split_kernel<F, false, kW2>);
       int per_cu = 2, grid = 0;
       size_t slds = 0;
       for (;;) {
-        grid = (a.N + kGemvWaves - 1) / kGemvWaves;
+        grid = (a.N + WV - 1) / WV;
         grid = grid < per_cu * cus ? grid : per_cu * cus;
         slds = gemv_split_lds_bytes(a.Kp, (a.N + grid - 1) / grid);
-        if (per_cu == 1 || gemv_wg_per_cu(reinterpret_cast<const void *>(k), slds) >= 2) break;
+        if (per_cu == 1 || gemv_wg_per_cu(reinterpret_cast<const void *>(k), slds, WV * kWave) >= 2) break;
         per_cu = 1;
       }
       if (plan) {
-        const int pmin = kGemvWaves / S;  // waves of the slice with the fewest
+        const int pmin = WV / S;  // waves of the slice with the fewest
         plan->workgroups = grid;
         plan->rows_per_wave = ((a.N + grid - 1) / grid + pmin - 1) / pmin;
         plan->rows_held = 2;
@@ -1184,7 +1196,7 @@ static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipS
       arg.split_base = a.N / grid;
       arg.split_rem = a.N % grid;
       void *args[] = {&arg};
-      const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(kGemvThreads), args,
+      const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(k), dim3(grid), dim3(WV * kWave), args,
                                            slds, s);
       return e != hipSuccess ? e : hipGetLastError();
     }

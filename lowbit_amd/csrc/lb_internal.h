@@ -118,9 +118,9 @@ struct GemvPlan {
   int k_slices = 1;  // slices each weight row is cut into across waves (rows past 4096 elements)
 };
 hipError_t launch_gemv(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, GemvPlan *plan = nullptr);
-// Workgroups of a small-M kernel (512 threads, `lds` bytes of dynamic LDS) that fit
-// on one CU at once; asked of the runtime once per kernel and size.
-int gemv_wg_per_cu(const void *kern, size_t lds);
+// Workgroups of a small-M kernel (`threads` per workgroup, `lds` bytes of dynamic
+// LDS) that fit on one CU at once; asked of the runtime once per kernel and size.
+int gemv_wg_per_cu(const void *kern, size_t lds, int threads = 512);
 // the group-32 instantiations of the small-M kernels (lb_gemv_g32.hip)
 hipError_t launch_gemv_g32(int fmt, const GemmArgs &a, int num_cus, size_t lds, hipStream_t s, GemvPlan *plan);
 // Per-token int8 quantizer: xq, xs, asum as lb_quant_act_int8, or (tiled) xq and asum

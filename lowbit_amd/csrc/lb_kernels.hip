@@ -144,7 +144,7 @@ bool gemv_eligible(int fmt, int M, int Kp) {
          gemv_lds_bytes(fmt, M, Kp) <= kGemvLdsLimit;
 }
 
-int gemv_wg_per_cu(const void *kern, size_t lds) {
+int gemv_wg_per_cu(const void *kern, size_t lds, int threads) {
   static std::mutex mu;
   static std::map<std::pair<const void *, size_t>, int> known;
   std::lock_guard<std::mutex> lock(mu);
@@ -152,7 +152,7 @@ int gemv_wg_per_cu(const void *kern, size_t lds) {
   const auto it = known.find(key);
   if (it != known.end()) return it->second;
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kGemvThreads, lds) != hipSuccess || n < 1) n = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess || n < 1) n = 1;
   known[key] = n;
   return n;
 }
