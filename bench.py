@@ -876,6 +876,10 @@ def main() -> int:
                     help="skip the synchronous Python call timings (kernel traces of the timed launches only)")
     ap.add_argument("--batch-m", type=int, default=BATCH[0], metavar="M",
                     help="rows of the hot batch GEMMs (default 64, the BASELINE shape)")
+    ap.add_argument("--shape", default=None, metavar="N,K",
+                    help="only time the three formats' decode (M = 1, cold) and batch (--batch-m rows, hot) "
+                         "GEMMs at N x K and print their JSON (profiles of the other benchmark shapes, e.g. "
+                         "4096,11008); no headline line")
     ap.add_argument("--machine-facts", action="store_true",
                     help="only measure the device facts the kernels are designed around (VALU issue cost per "
                          "instruction form, launch cost, the plain-read floor) and print their JSON")
@@ -921,6 +925,24 @@ def main() -> int:
         return 0
     if args.only_decoder:
         print(json.dumps({"decoder": measure_decoder(["w4a8", "mxfp4"], graph=graph)}), flush=True)
+        return 0
+    if args.shape:
+        n_s, k_s = (int(v) for v in args.shape.split(","))
+        rng = np.random.default_rng(0)
+        w = rng.standard_normal((n_s, k_s)).astype(np.float32)
+        packed = {"int4": lb.quantize_int4(w, asym=True), "mxfp4": lb.quantize_mxfp4(w)}
+        runs = {}
+        for mm, cold in ((1, True), (args.batch_m, False)):
+            xs = rng.standard_normal((mm, k_s)).astype(np.float32)
+            for fmt in ["w4a8", "w4a16", "mxfp4"]:
+                W = packed["mxfp4" if fmt == "mxfp4" else "int4"]
+                r = measure(dev, fmt, (mm, n_s, k_s), W, xs, cold=cold, steps=args.steps,
+                            warmup=args.warmup, graph=graph, call=False)
+                r["max_rel_err"] = float(f"{rel_err(fmt, W, xs, r.pop('y')):.3g}")
+                runs[f"{fmt}_m{mm}"] = r
+                log(f"{fmt:6s} {mm}x{n_s}x{k_s} {'cold' if cold else 'hot'}: {r['us_per_call']:8.2f} us  "
+                    f"path {r['path']}  rel err {r['max_rel_err']}")
+        print(json.dumps({"shape_runs": runs}), flush=True)
         return 0
     rng = np.random.default_rng(0)
     results = {}
