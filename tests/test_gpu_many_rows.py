@@ -109,13 +109,29 @@ def test_many_rows_glu_pairs(rng, fmt):
 def test_two_rows_per_load_row_lengths(rng, fmt, k, n):
     """One activation row, rows of 1..8 groups (one to 32 chunks), two rows per wave
     load with 1-3 slots per batch: each batch's scales and zero-points come in one
-    load each and reach their lanes by cross-lane permute. Symmetric and asymmetric
-    int4, against the oracle's bounds."""
-    for asym in ([False, True] if fmt != "mxfp4" else [False]):
+    load each and reach their lanes by cross-lane permute. Symmetric, asymmetric and
+    signed-max (negative scales) int4, against the oracle's bounds."""
+    for asym, scale in ([(False, "absmax"), (True, "absmax"), (False, "signed-max")] if fmt != "mxfp4"
+                        else [(False, None)]):
         w = rng.standard_normal((n, k)).astype(np.float32)
-        W = lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=asym)
+        W = lb.quantize_mxfp4(w) if fmt == "mxfp4" else lb.quantize_int4(w, asym=asym, scale=scale)
         assert K.gemm_plan(fmt, 1, n, W.kp)["two_rows_per_load"] == 1
         x = rng.standard_normal((1, k)).astype(np.float32)
         fn = {"w4a16": K.gemm_w4a16, "w4a8": K.gemm_w4a8, "mxfp4": K.gemm_mxfp4}[fmt]
         y = fn(x, lb.to_device(W))
         check_oracle(fmt, lb.formats.pad_acts(x, W.kp), W, y)
+
+
+@pytest.mark.parametrize("fmt", ["w4a16", "w4a8"])
+@pytest.mark.parametrize("k", [4096, 6000, 11008])
+def test_one_row_negative_scales(rng, fmt, k):
+    """signed-max int4 (negative group scales, tests/test_kernels.py:44-58 of the
+    reference) through the one-row paced GEMVs: unsplit rows, and rows cut into two
+    or three slices (W4A16)."""
+    n = 3001
+    W = lb.quantize_int4(rng.standard_normal((n, k)).astype(np.float32), scale="signed-max")
+    assert (W.scales < 0).any()
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    fn = {"w4a16": K.gemm_w4a16, "w4a8": K.gemm_w4a8}[fmt]
+    y = fn(x, lb.to_device(W))
+    check_oracle(fmt, lb.formats.pad_acts(x, W.kp), W, y)
