@@ -1172,17 +1172,28 @@ static hipError_t launch_gemv_paced(const GemmArgs &a, int cus, size_t lds, hipS
       const int WV = S == 3 ? kW3 : kW2;
       const GemvFn k = S == 3 ? (dw ? gemv_paced_split_kernel<F, true, kW3, 3> : gemv_paced_split_kernel<F, false, kW3, 3>)
                               : (dw ? gemv_paced_split_kernel<F, true, kW2> : gemv_paced_split_kernel<F, false, kW2>);
+      // Workgroups of WV rows each (S row-slices per wave) while they fill the CUs.
+      // Fewer rows than that: the fewest row-slices per wave q that the CUs allow,
+      // over the fewest workgroups that give it (at most one per CU). 1 x 1024 x
+      // 11008 cold W4A16 6.0 -> 4.2 us (86 -> 256 workgroups), MXFP4 5.7 -> 4.4;
+      // 1 x 896 x 4864 W4A16 4.2 -> 3.7, MXFP4 4.6 -> 3.8. A workgroup per CU
+      // without fewer row-slices per wave only adds activation staging
+      // (1 x 1536 x 5000 W4A16 192 -> 256 workgroups: 4.35 -> 4.45 us).
+      const int pmin = WV / S;  // waves of the slice with the fewest
       int per_cu = 2, grid = 0;
       size_t slds = 0;
       for (;;) {
         grid = (a.N + WV - 1) / WV;
+        if (grid < cus) {
+          const int q = (a.N + cus * pmin - 1) / (cus * pmin);
+          grid = (a.N + q * pmin - 1) / (q * pmin);
+        }
         grid = grid < per_cu * cus ? grid : per_cu * cus;
         slds = gemv_split_lds_bytes(a.Kp, (a.N + grid - 1) / grid);
         if (per_cu == 1 || gemv_wg_per_cu(reinterpret_cast<const void *>(k), slds, WV * kWave) >= 2) break;
         per_cu = 1;
       }
       if (plan) {
-        const int pmin = WV / S;  // waves of the slice with the fewest
         plan->workgroups = grid;
         plan->rows_per_wave = ((a.N + grid - 1) / grid + pmin - 1) / pmin;
         plan->rows_held = 2;

@@ -229,7 +229,11 @@ def test_c4_plan_splits_rows_over_waves():
 # chunks: four slices would need 64 KB) and every W4A8 row keep the unsplit kernel
 SPLIT = [("w4a16", True, 4097, 4224, 2), ("w4a16", False, 1000, 12288, 3), ("mxfp4", False, 4097, 8224, 3),
          ("mxfp4", False, 3000, 12288, 3), ("w4a16", True, 1500, 13312, 1), ("w4a8", True, 4096, 11008, 1),
-         ("w4a8", False, 1000, 16384, 1)]
+         ("w4a8", False, 1000, 16384, 1),
+         # fewer rows than the CUs' workgroups of full size: one to a few row-slices
+         # per wave, some waves without rows
+         ("w4a16", True, 1, 11008, 3), ("mxfp4", False, 7, 5000, 2), ("w4a16", False, 896, 4864, 2),
+         ("mxfp4", False, 1023, 11008, 3), ("w4a16", True, 2047, 8192, 2)]
 
 
 @pytest.mark.parametrize("fmt,asym,n,k,slices", SPLIT)
@@ -244,6 +248,19 @@ def test_split_rows_against_oracle(fmt, asym, n, k, slices):
     y = K.GEMMS[fmt](x, lb.to_device(W))
     assert K.last_path() == "gfx950"
     _check(fmt, x, W, y)
+
+
+def test_split_rows_few_rows_fill_the_cus():
+    """With fewer rows than workgroups of full size would give every CU, the split
+    GEMV spreads them over more workgroups (at most one per CU) to reach the fewest
+    row-slices per wave, and no more workgroups than that takes (row lengths padded
+    to whole groups, as `gemm_plan` takes them)."""
+    cus = K.gemm_plan("w4a16", 1, 4096, 11008)["workgroups"]  # one per CU at this shape
+    for fmt, n, k, wg, rpw in [("w4a16", 1024, 11008, cus, 1), ("mxfp4", 1024, 11008, cus, 1),
+                               ("w4a16", 896, 4864, 224, 1), ("mxfp4", 896, 4864, 112, 1),
+                               ("w4a16", 1536, 5120, 192, 2), ("mxfp4", 1, 11008, 1, 1)]:
+        plan = K.gemm_plan(fmt, 1, n, k)
+        assert plan["k_slices"] > 1 and plan["workgroups"] == wg and plan["rows_per_wave"] == rpw, (fmt, n, k, plan)
 
 
 def test_split_rows_zero_rows_exact():
