@@ -62,10 +62,12 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Lane `lane` (wave-uniform) of v takes the wave-uniform value `bits`; the other
-// lanes keep theirs (v_writelane_b32, which clang exposes as no builtin; the lane
-// select goes through M0, as gfx9 reads one scalar register per VALU instruction).
+// lanes keep theirs: v_writelane_b32 through LLVM's intrinsic, which clang exposes
+// as no builtin. The compiler then sets M0 for the lane select itself (gfx9 reads
+// one scalar register per VALU instruction) and knows that M0 changes.
+__device__ int lb_writelane_i32(int val, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
 __device__ __forceinline__ void write_lane(float &v, int bits, int lane) {
-  asm("s_mov_b32 m0, %2\n\ts_nop 0\n\tv_writelane_b32 %0, %1, m0" : "+v"(v) : "s"(bits), "s"(lane) : "m0");
+  v = __int_as_float(lb_writelane_i32(bits, lane, __float_as_int(v)));
 }
 
 // Max over the wave of 64-bit keys (unsigned); every lane gets it. Each step moves
