@@ -372,7 +372,8 @@ def read_floor_sizes(dev: Dev, base_bytes: int, steps: int, warmup: int, graph: 
 
 PROBE_FORMS = ["v_fmac_f32", "v_fma_f32", "v_add_f32", "v_mul_f32", "v_and_b32", "v_lshrrev_b32",
                "v_cvt_f32_ubyte1", "v_cvt_f32_u32", "v_bfe_u32", "v_perm_b32", "v_and_or_b32", "v_fma_mix_f32",
-               "v_dot4_i32_i8", "v_pk_add_f16", "v_cvt_scalef32_pk_f32_fp4"]
+               "v_dot4_i32_i8", "v_pk_add_f16", "v_cvt_scalef32_pk_f32_fp4", "v_dot2_f32_f16", "v_dot2c_f32_f16",
+               "v_cvt_f32_f16"]
 
 
 BARRIER_MODES = ("atomic counter", "flag per workgroup", "flags + agent release/acquire fences")

@@ -76,9 +76,15 @@ static hipError_t launch_read_t(const void *src, uint32_t bytes, int wgs, int lo
   X(10, "v_and_or_b32 %0, %1, %2, %0")                                      \
   X(11, "v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]")                   \
   X(12, "v_dot4_i32_i8 %0, %1, %2, %0")                                     \
-  X(13, "v_pk_add_f16 %0, %1, %0")
+  X(13, "v_pk_add_f16 %0, %1, %0")                                          \
+  X(15, "v_dot2_f32_f16 %0, %1, %2, %0")                                    \
+  X(16, "v_dot2c_f32_f16_e32 %0, %1, %2")                                   \
+  X(17, "v_cvt_f32_f16_e32 %0, %1")
 
-constexpr int kProbeForms = 15;  // the 14 forms above and v_cvt_scalef32_pk_f32_fp4
+// the 17 forms above and, as form 14, v_cvt_scalef32_pk_f32_fp4. The half-precision
+// forms read a and b as pairs of finite halves (the low halves of a are 0, +-2^-7,
+// +-2 or +-512; the rest are near 1.8)
+constexpr int kProbeForms = 18;
 
 template <int OP>
 __global__ __launch_bounds__(512) void valu_probe_kernel(int iters, float *out) {

@@ -174,10 +174,10 @@ def test_probe_argument_checks():
     forms bench.py names."""
     import bench
     L = K.lib()
-    assert L.lbd_probe_forms() == len(bench.PROBE_FORMS) == 15
+    assert L.lbd_probe_forms() == len(bench.PROBE_FORMS) == 18
     assert L.lbd_probe_valu(0, 16, 1, None, None) == -6            # no output buffer
     out = C.c_void_p(16)                                            # never dereferenced
-    assert L.lbd_probe_valu(15, 16, 1, out, None) == -6             # past the last form
+    assert L.lbd_probe_valu(18, 16, 1, out, None) == -6             # past the last form
     assert L.lbd_probe_valu(-1, 16, 1, out, None) == -6
     assert L.lbd_probe_valu(0, 0, 1, out, None) == -6               # no iterations
     assert L.lbd_probe_valu(0, 16, 0, out, None) == -6              # no workgroups
