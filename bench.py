@@ -10,8 +10,10 @@ weights from HBM (the cold rule of src/lowbit/bench.py:169-178, sized for the GP
 
 One step = one GEMM call on device-resident inputs. The timed launches are
 captured in a HIP graph and replayed, so host launch overhead is not counted;
-HIP events on the launch stream bracket the timed region (after W warm-up
-steps and a device synchronisation on both sides). The metric definitions
+HIP events on the launch stream bracket the timed replay (after W warm-up
+steps, a device synchronisation, and untimed replays of the same graph for at
+least 10 ms queued right before it, so that the GPU's clocks have risen as in
+steady use; a device synchronisation after it). The metric definitions
 follow src/lowbit/bench.py:213-214: weight GB/s = packed weight bytes / time,
 GFLOP/s = 2*M*N*K / time with the logical K.
 
@@ -117,10 +119,15 @@ class Dev:
 
     GATE_US_PER_LAUNCH = 40.0  # host time per queued launch the gate covers (tracer included)
 
+    WARM_MS = 10.0  # replays of the captured graph before the timed one, at least this long
+
     def time_launches(self, launch, n_launch: int, warmup: int, graph: bool = True) -> float:
         """ms per launch of `launch(i)` over n_launch launches (HIP events on the stream):
         a replayed graph, or (graph=False) plain launches queued behind a busy kernel so
-        that they run back to back as the graph's do."""
+        that they run back to back as the graph's do. The graph is replayed untimed for
+        at least WARM_MS first, the timed replay queued right behind those replays: an
+        idle GPU's clocks take milliseconds to rise, and the arithmetic-heavy W4A16
+        decode GEMV measured 0.3-0.7 us slower after a single warm-up replay."""
         L = self.L
         if not graph:
             self.gate(self.GATE_US_PER_LAUNCH * warmup)
@@ -134,9 +141,15 @@ class Dev:
                 launch(i)
             ex = C.c_void_p()
             self.check(L.lb_stream_end_capture(self.stream, C.byref(ex)), "end capture")
+            # one warm-up replay, timed, then as many more as fill WARM_MS, with the
+            # timed replay queued behind them (no idle gap before it)
+            self.check(L.lb_event_record(e0, self.stream), "record")
             self.check(L.lb_graph_launch(ex.value, self.stream), "graph warm-up")
-            self.check(L.lb_stream_synchronize(self.stream), "sync")
-            self.check(L.lb_dev_synchronize(), "sync")
+            self.check(L.lb_event_record(e1, self.stream), "record")
+            self.check(L.lb_event_synchronize(e1), "sync")
+            more = min(1000, max(0, math.ceil(self.WARM_MS / max(1e-3, self.elapsed_ms(e0, e1))) - 1))
+            for _ in range(more):
+                self.check(L.lb_graph_launch(ex.value, self.stream), "graph warm-up")
             self.check(L.lb_event_record(e0, self.stream), "record")
             self.check(L.lb_graph_launch(ex.value, self.stream), "graph launch")
             self.check(L.lb_event_record(e1, self.stream), "record")
