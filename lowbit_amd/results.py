@@ -31,6 +31,7 @@ import argparse
 import ctypes as C
 import datetime as _dt
 import json
+import math
 import platform
 import statistics
 import sys
@@ -120,8 +121,11 @@ class _Timer:
         _check(self.L.lb_event_create(C.byref(e)), "event")
         return e.value
 
+    WARM_MS = 10.0  # untimed replays first, at least this long (an idle GPU's clocks ramp up)
+
     def samples(self, launch, n_launch: int, reps: int) -> list[float]:
-        """Seconds per launch, one sample per replay of a graph of n_launch launches."""
+        """Seconds per launch, one sample per replay of a graph of n_launch launches,
+        after untimed replays of the same graph for at least WARM_MS."""
         L, s = self.L, self.stream
         _check(L.lb_stream_synchronize(s), "sync")
         _check(L.lb_stream_begin_capture(s), "begin capture")
@@ -134,7 +138,14 @@ class _Timer:
         e0, e1 = self._event(), self._event()
         out = []
         try:
+            _check(L.lb_event_record(e0, s), "record")
             _check(L.lb_graph_launch(ex.value, s), "graph warm-up")
+            _check(L.lb_event_record(e1, s), "record")
+            _check(L.lb_event_synchronize(e1), "sync")
+            ms = C.c_float()
+            _check(L.lb_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+            for _ in range(min(1000, max(0, math.ceil(self.WARM_MS / max(1e-3, ms.value)) - 1))):
+                _check(L.lb_graph_launch(ex.value, s), "graph warm-up")
             for _ in range(reps):
                 _check(L.lb_stream_synchronize(s), "sync")
                 _check(L.lb_event_record(e0, s), "record")
