@@ -256,7 +256,15 @@ int run_bf3(int fmt, const lbk::GemmArgs &a0, char *ws, hipStream_t s, bool f8 =
   if (device_info(&di) == 0) cus = di.cus;
   lbk::GemmArgs a = a0;
   a.x3 = reinterpret_cast<const uint4 *>(ws);
-  hipError_t e = lbk::launch_split3(fmt, a.x, a.M, a.Kp, reinterpret_cast<uint4 *>(ws), s);
+  hipError_t e;
+  if (fmt == lbk::F_W4A16) {
+    // two float16 terms per row and its exponent (within the bf16x3 workspace)
+    int *xexp = reinterpret_cast<int *>(ws + lbk::x2h_exp_offset(a.M, a.Kp));
+    a.xexp = xexp;
+    e = lbk::launch_split2h(a.x, a.M, a.Kp, reinterpret_cast<uint4 *>(ws), xexp, s);
+  } else {
+    e = lbk::launch_split3(fmt, a.x, a.M, a.Kp, reinterpret_cast<uint4 *>(ws), s);
+  }
   if (e != hipSuccess) return fail_hip(e, "activation split launch");
   e = lbk::launch_bf3_gemm(fmt, a, cus, s, f8);
   if (e != hipSuccess) return fail_hip(e, "bf16x3 GEMM launch");

@@ -31,7 +31,9 @@ struct GemmArgs {
   // one-row (paced) GEMV: rows per workgroup N / grid and N % grid, divided on the host so
   // that no division runs ahead of the kernel's first loads
   int split_base = 0, split_rem = 0;
-  const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path)
+  const uint4 *x3 = nullptr;      // activations as three bf16 terms, tiled (bf16x3 path);
+                                  // W4A16: two float16 terms of each row times 2^xexp[row]
+  const int *xexp = nullptr;      // W4A16 batch path: each activation row's power-of-two exponent
   float *ypart = nullptr;         // bf16x3 split over K: the slices' partial outputs [ks][M][N]
   bool tiled = false;             // xq / asum in the tiled layout of the MFMA path
   bool wt16 = false;              // qw / scales / zeros / e8m0 in the MFMA tile layout (t16)
@@ -87,6 +89,13 @@ hipError_t launch_repack_mxfp4_t16(const uint8_t *qw, const uint8_t *e8m0, int N
 // weights. Bytes of the split activations for M rows:
 __host__ __device__ inline size_t x3_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 3 * 1024; }
 hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipStream_t s);
+// W4A16: each activation row scaled by a power of two 2^E (its largest magnitude into
+// [2^14, 2^15)) and split into two float16 terms, the second times 2^11, in the same
+// tile order with two terms per slot; the exponents follow the terms at a 256-byte
+// boundary. Both fit in x3_bytes(M, Kp).
+__host__ __device__ inline size_t x2h_bytes(int M, int Kp) { return (size_t)((M + 15) / 16) * ((Kp + 127) / 128) * 4 * 2 * 1024; }
+__host__ __device__ inline size_t x2h_exp_offset(int M, int Kp) { return (x2h_bytes(M, Kp) + 255) & ~(size_t)255; }
+hipError_t launch_split2h(const float *x, int M, int Kp, uint4 *x2, int *xexp, hipStream_t s);
 hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t s, bool f8 = false);
 // K slices of the bf16x3 GEMM at this shape (1: no split), and the bytes of their
 // partial outputs that launch_bf3_gemm needs at a.ypart when the split is taken.

@@ -940,6 +940,72 @@ hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipS
   return hipGetLastError();
 }
 
+// W4A16 activations as two float16 terms for the f16 matrix cores (one workgroup per
+// row). The row is scaled by 2^E, E chosen so that its largest magnitude lands in
+// [2^14, 2^15) (E = 0 for a zero or non-finite row); then xs = x 2^E = hi + lo 2^-11
+// with hi = fp16(xs) and lo = fp16((xs - hi) 2^11) (the remainder is exact in fp32,
+// and the 2^11 keeps lo a normal float16 down to |xs| ~ 2^-14), so each element keeps
+// 22 significant bits while its scaled magnitude is at least 2^-14, i.e. within 2^28
+// of the row's largest. Slots as in split3_kernel's W4A16 tiles, two terms per slot.
+// Workgroups (m, p) of a row each take the row's maximum over all of it (from the
+// caches after the first) and split part p of its slots.
+__global__ __launch_bounds__(kThreads) void split2h_kernel(const float *__restrict__ x, int M, int Kp,
+                                                          uint4 *__restrict__ x2, int *__restrict__ xexp) {
+  __shared__ float red[kThreads / kWave];
+  const int m = blockIdx.x, G = Kp / 128, items = G * 16;  // (g, u, q): 8 elements each
+  const int P = gridDim.y, pt0 = (int)(((long long)items * blockIdx.y) / P),
+            pt1 = (int)(((long long)items * (blockIdx.y + 1)) / P);
+  const float *xr = x + (size_t)m * Kp;
+  auto e0_of = [](int t) { return 128 * (t >> 4) + 64 * ((t >> 3) & 1) + 16 * (t & 3) + 8 * ((t >> 2) & 1); };
+  float amax = 0.0f;
+  for (int t = threadIdx.x; t < items; t += kThreads) {
+    const float4 lo = *reinterpret_cast<const float4 *>(xr + e0_of(t));
+    const float4 hi = *reinterpret_cast<const float4 *>(xr + e0_of(t) + 4);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))));
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w))));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
+  __syncthreads();
+  float rmax = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / kWave; w++) rmax = fmaxf(rmax, red[w]);
+  int E = 0;
+  if (rmax > 0.0f && rmax <= 3.402823466e38f) {
+    int ex;
+    frexpf(rmax, &ex);  // rmax = f 2^ex, f in [0.5, 1)
+    E = 15 - ex;
+  }
+  if (threadIdx.x == 0 && blockIdx.y == 0) xexp[m] = E;
+  const int mb = m >> 4, r = m & 15;
+  for (int t = pt0 + (int)threadIdx.x; t < pt1; t += kThreads) {
+    const float4 lo = *reinterpret_cast<const float4 *>(xr + e0_of(t));
+    const float4 hi = *reinterpret_cast<const float4 *>(xr + e0_of(t) + 4);
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    uint32_t th[4], tl[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float a0 = ldexpf(v[2 * k], E), a1 = ldexpf(v[2 * k + 1], E);
+      const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1;
+      const _Float16 l0 = (_Float16)((a0 - (float)h0) * 2048.0f), l1 = (_Float16)((a1 - (float)h1) * 2048.0f);
+      th[k] = __builtin_bit_cast(uint32_t, h2v{h0, h1});
+      tl[k] = __builtin_bit_cast(uint32_t, h2v{l0, l1});
+    }
+    const int g = t >> 4, u = (t >> 2) & 3, q = t & 3;
+    uint4 *dst = x2 + (((size_t)mb * G + g) * 4 + u) * 2 * kWave + 16 * q + r;
+    dst[0] = make_uint4(th[0], th[1], th[2], th[3]);
+    dst[kWave] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+  }
+}
+
+hipError_t launch_split2h(const float *x, int M, int Kp, uint4 *x2, int *xexp, hipStream_t s) {
+  if (M <= 0 || Kp % 128) return hipErrorInvalidValue;
+  // about 256 workgroups: each row's slots in up to G parts
+  const int G = Kp / 128, P = std::max(1, std::min(G, 256 / M));
+  hipLaunchKernelGGL(split2h_kernel, dim3(M, P), dim3(kThreads), 0, s, x, M, Kp, x2, xexp);
+  return hipGetLastError();
+}
+
 // Weight stage of one subtile: the lane's 16 bytes of the group's tile and, for
 // W4A16, its row's scale and the dword of zero-points holding its group's; for
 // MXFP4, the dword of E8M0 bytes holding its block's; for the t16f8 layout, the
@@ -961,6 +1027,15 @@ __device__ __forceinline__ void w4_bf16x4(uint32_t nib, float zf, uint32_t &d0, 
   d1 = pack_bf16(__float_as_uint(f2), __float_as_uint(f3));
 }
 
+// Four float32 of (byte k of nib) - zf as two float16x2 (exact: integers below 16).
+__device__ __forceinline__ void w4_f16x4(uint32_t nib, float zf, uint32_t &d0, uint32_t &d1) {
+  const uint32_t n = opaque(nib);
+  const float f0 = (float)(n & 0xFF) - zf, f1 = (float)((n >> 8) & 0xFF) - zf;
+  const float f2 = (float)((n >> 16) & 0xFF) - zf, f3 = (float)(n >> 24) - zf;
+  d0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
+  d1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f2, f3));
+}
+
 // Waves split the K groups (wave w takes group 8 ph + w of phase ph) and keep
 // their activation operands (4 x 3 x TM x 1 KiB) in registers across the
 // workgroup's subtiles; per subtile and row block, 12 MFMAs accumulate the group
@@ -975,9 +1050,16 @@ __device__ __forceinline__ void w4_bf16x4(uint32_t nib, float zf, uint32_t &d0, 
 // already less their zero-point as E4M3 bytes n 2^-9 (sign and magnitude n <= 15),
 // so that one conversion with scale 2^9 makes two bf16 operands, the same values
 // as the nibble path's (float)code - z, with no zero-point load.
-template <int F, int TM, int NS, int PF, bool F8>
+// H2 (W4A16 only): the activations as two float16 terms of each row times 2^E
+// (split2h_kernel) on the float16 matrix cores, 8 MFMAs per tile and group instead
+// of 12 and two thirds of the activation bytes; the high terms and the low terms
+// (times 2^11) accumulate apart and meet as hi + 2^-11 lo before the scale FMA,
+// and the stored outputs are scaled back by 2^-E of their row (exact).
+template <int F, int TM, int NS, int PF, bool F8, bool H2 = false>
 __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   static_assert(!F8 || F == F_W4A16, "the t16f8 layout holds int4 weights");
+  static_assert(!H2 || F == F_W4A16, "two float16 terms: integer weights only");
+  constexpr int T3 = H2 ? 2 : 3;  // activation terms per slot
   __shared__ __align__(16) float red[NS * TM * kW8Waves * kWave * 4];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -996,7 +1078,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   const int nph = (GL + kW8Waves - 1) / kW8Waves;
   float *const yo = KS > 1 ? a.ypart + (size_t)ks * M * N : a.y;
 
-  const Rsrc rx = make_rsrc(a.x3, (uint32_t)min(x3_bytes(M, Kp), (size_t)0xFFFFFFF0u));
+  const Rsrc rx = make_rsrc(a.x3, (uint32_t)min(H2 ? x2h_bytes(M, Kp) : x3_bytes(M, Kp), (size_t)0xFFFFFFF0u));
   const Rsrc rw = make_rsrc(a.qw, (uint32_t)min(F8 ? t16f8_qw_bytes(N, Kp) : t16_qw_bytes(N, Kp),
                                                 (size_t)0xFFFFFFF0u));
   const size_t gents = t16_group_entries(N, Kp);
@@ -1005,7 +1087,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
   const Rsrc rz = make_rsrc(a.zeros ? a.zeros : a.qw, (F == F_W4A16 && !F8 && a.zeros) ? (uint32_t)gents : 0u);
   const int zadd = (F == F_W4A16 && !a.zeros) ? 8 : 0;
 
-  v4u xa[4][3][TM];
+  v4u xa[4][T3][TM];
   for (int cb = sb; cb < se; cb += NS) {
     const int ce = min(cb + NS, se);
     if (wave >= GL) {
@@ -1054,11 +1136,11 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; u++)
 #pragma unroll
-          for (int p = 0; p < 3; p++)
+          for (int p = 0; p < T3; p++)
 #pragma unroll
             for (int i = 0; i < TM; i++) {
               // row blocks past the last one read zeros (past the descriptor)
-              const uint32_t off = ((((uint32_t)(mb0 + i) * G + g) * 4 + u) * 3 + p) * kWave * 16 + lane * 16;
+              const uint32_t off = ((((uint32_t)(mb0 + i) * G + g) * 4 + u) * T3 + p) * kWave * 16 + lane * 16;
               const uint4 v = ld_b128(rx, off);
               xa[u][p][i] = v4u{v.x, v.y, v.z, v.w};
             }
@@ -1094,12 +1176,21 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
           const uint32_t wd[8] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w, cur.w2.x, cur.w2.y, cur.w2.z, cur.w2.w};
 #pragma unroll
           for (int u = 0; u < 4; u++) {
-            b[u][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, false));
-            b[u][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, true));
-            b[u][2] =
-                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, false));
-            b[u][3] =
-                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, true));
+            if constexpr (H2) {
+              b[u][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * u], 512.0f, false));
+              b[u][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * u], 512.0f, true));
+              b[u][2] =
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * u + 1], 512.0f, false));
+              b[u][3] =
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * u + 1], 512.0f, true));
+            } else {
+              b[u][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, false));
+              b[u][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u], 512.0f, true));
+              b[u][2] =
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, false));
+              b[u][3] =
+                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * u + 1], 512.0f, true));
+            }
           }
           fs = cur.s;
         } else if constexpr (F == F_W4A16) {
@@ -1110,10 +1201,12 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int d = 0; d < 2; d++) {
               uint32_t x0, x1;
-              w4_bf16x4(lo_nibbles(wd[2 * h + d]), zf, x0, x1);
+              if constexpr (H2) w4_f16x4(lo_nibbles(wd[2 * h + d]), zf, x0, x1);
+              else w4_bf16x4(lo_nibbles(wd[2 * h + d]), zf, x0, x1);
               b[h][2 * d] = x0;
               b[h][2 * d + 1] = x1;
-              w4_bf16x4(hi_nibbles(wd[2 * h + d]), zf, x0, x1);
+              if constexpr (H2) w4_f16x4(hi_nibbles(wd[2 * h + d]), zf, x0, x1);
+              else w4_bf16x4(hi_nibbles(wd[2 * h + d]), zf, x0, x1);
               b[2 + h][2 * d] = x0;
               b[2 + h][2 * d + 1] = x1;
             }
@@ -1140,12 +1233,25 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           v4f dacc = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (H2) {
+            v4f dlo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int u = 0; u < 4; u++)
+            for (int u = 0; u < 4; u++) {
+              dacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, xa[u][0][i]),
+                                                            __builtin_bit_cast(v8h, b[u]), dacc, 0, 0, 0);
+              dlo = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, xa[u][T3 - 1][i]),
+                                                           __builtin_bit_cast(v8h, b[u]), dlo, 0, 0, 0);
+            }
 #pragma unroll
-            for (int p = 0; p < 3; p++)
-              dacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[u][p][i]),
-                                                             __builtin_bit_cast(v8bf, b[u]), dacc, 0, 0, 0);
+            for (int r = 0; r < 4; r++) dacc[r] = __builtin_fmaf(dlo[r], 0x1p-11f, dacc[r]);
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+              for (int p = 0; p < T3; p++)
+                dacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xa[u][p][i]),
+                                                               __builtin_bit_cast(v8bf, b[u]), dacc, 0, 0, 0);
+          }
           v4f f;
 #pragma unroll
           for (int r = 0; r < 4; r++) f[r] = __builtin_fmaf(fs, dacc[r], prev[i][r]);
@@ -1168,7 +1274,7 @@ __global__ __launch_bounds__(kW8Threads) void bf3_gemm_kernel(GemmArgs a) {
       if (n < N) {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (m0 + lr + r < M) yo[(size_t)(m0 + lr + r) * N + n] = v[r];
+          if (m0 + lr + r < M) yo[(size_t)(m0 + lr + r) * N + n] = H2 ? ldexpf(v[r], -a.xexp[m0 + lr + r]) : v[r];
       }
     }
     __syncthreads();  // red is rewritten by the next chunk
@@ -1201,7 +1307,7 @@ static void bf3_grid(int M, int N, int TM, int cus, int &gx, int &gy, int &spw) 
   spw = (S + gx - 1) / gx;
 }
 
-template <int F, int TM, bool F8>
+template <int F, int TM, bool F8, bool H2 = false>
 static void launch_bf3_t(const GemmArgs &a, int cus, int ks, hipStream_t s) {
   constexpr int NS = B3Cfg<TM>::NS, PF = B3Cfg<TM>::PF;
   // every subtile slot of a chunk but the last is computed, so the chunk length
@@ -1216,7 +1322,7 @@ static void launch_bf3_t(const GemmArgs &a, int cus, int ks, hipStream_t s) {
   }
   auto go = [&](auto ns) {
     constexpr int C = decltype(ns)::value < NS ? decltype(ns)::value : NS;
-    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF), F8>), dim3(gx, gy, ks),
+    hipLaunchKernelGGL((bf3_gemm_kernel<F, TM, C, (C - 1 < PF ? C - 1 : PF), F8, H2>), dim3(gx, gy, ks),
                        dim3(kW8Threads), 0, s, a);
   };
   switch (spw) {
@@ -1293,12 +1399,13 @@ hipError_t launch_bf3_gemm(int fmt, const GemmArgs &a, int num_cus, hipStream_t 
     };
     tall = cu_bytes(1) > 0.75 * cu_bytes(2);
   }
+  if (fmt == F_W4A16 && !a.xexp) return hipErrorInvalidValue;  // W4A16 reads the two-term split
   if (fmt == F_W4A16 && f8) {
-    if (tall) launch_bf3_t<F_W4A16, 2, true>(a, cus, ks, s);
-    else launch_bf3_t<F_W4A16, 1, true>(a, cus, ks, s);
+    if (tall) launch_bf3_t<F_W4A16, 2, true, true>(a, cus, ks, s);
+    else launch_bf3_t<F_W4A16, 1, true, true>(a, cus, ks, s);
   } else if (fmt == F_W4A16) {
-    if (tall) launch_bf3_t<F_W4A16, 2, false>(a, cus, ks, s);
-    else launch_bf3_t<F_W4A16, 1, false>(a, cus, ks, s);
+    if (tall) launch_bf3_t<F_W4A16, 2, false, true>(a, cus, ks, s);
+    else launch_bf3_t<F_W4A16, 1, false, true>(a, cus, ks, s);
   } else if (fmt == F_MXFP4) {
     if (tall) launch_bf3_t<F_MXFP4, 2, false>(a, cus, ks, s);
     else launch_bf3_t<F_MXFP4, 1, false>(a, cus, ks, s);

@@ -118,9 +118,10 @@ def test_random_shapes(fmt, route):
 @pytest.mark.parametrize("m", [1, 3, 16, 64])
 @pytest.mark.parametrize("mag", [1e-36, 1e-33, 1e-30, 1e-10, 1e10, 1e30])
 def test_activation_magnitudes(fmt, m, mag):
-    """Rows of one magnitude far from 1, through the GEMVs (M <= 4) and the bf16x3
-    matrix cores (M >= 5), whose three bf16 terms keep fp32's 24 bits down to rows of
-    1e-36 (below that the matrix cores flush the smallest term)."""
+    """Rows of one magnitude far from 1, through the GEMVs (M <= 4) and the matrix
+    cores (M >= 5): MXFP4's three bf16 terms keep fp32's 24 bits down to rows of 1e-36
+    (below that the matrix cores flush the smallest term); W4A16's two float16 terms
+    of each row scaled by its own power of two keep 22 bits at any row magnitude."""
     rng = np.random.default_rng(int(abs(np.log10(mag))) * 10 + m)
     n, k = 96, 1024
     w = rng.standard_normal((n, k)).astype(np.float32)
@@ -141,3 +142,37 @@ def test_activation_magnitudes(fmt, m, mag):
     err = np.abs(y.astype(np.float64) - ref)
     worst = float((err / (RTOL * bound + 1e-300)).max())
     assert worst <= 1.0, f"max err/limit = {worst:.3g}"
+
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_w4a16_batch_rows_of_mixed_magnitude_and_range(m):
+    """The W4A16 matrix-core path scales each activation row by its own power of two
+    before the float16 split: rows from 1e-36 to 1e30 in one call, and rows whose
+    few huge entries (2^26 times the rest, at the weights' zero-point codes, so the
+    reference's bound takes nothing from them) leave the other entries within 2^28
+    of the row's largest, where every element keeps 22 significant bits."""
+    rng = np.random.default_rng(4242 + m)
+    n, k = 96, 1024
+    mags = np.array([1e-36, 1e-20, 1e-3, 1.0, 1e5, 1e18, 1e30])
+    x = rng.standard_normal((m, k)) * mags[np.arange(m) % len(mags)][:, None]
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    W = lb.quantize_int4(w, asym=True)
+    codes = W.codes()
+    z = np.repeat(W.zeros, W.group, axis=1)[:, :W.kp]
+    for i in range(1, m, 3):  # every third row: outliers at zero-point codes
+        cols = rng.choice(k, size=3, replace=False)
+        x[i] = rng.standard_normal(k)
+        x[i, cols] = 2.0 ** 26 * rng.choice([-1.0, 1.0], size=3)
+        codes[:, cols] = z[:, cols]
+    W = lb.formats.Int4Weights(lb.formats.pack_nibbles(codes.astype(np.uint8), W.group), W.scales, W.zeros,
+                               W.k, W.group)
+    x = x.astype(np.float32)
+    assert K.gemm_plan("w4a16", m, n, W.kp)["path"] == "gfx950-mfma"
+    xp = lb.formats.pad_acts(x, W.kp)
+    ref = O.gemm_w4a16_ref(xp, W.qw, W.scales, W.zeros)
+    bound = cref.c_gemm_w4a16(xp, W.qw, W.scales, W.zeros, absval=True)
+    for y in (K.gemm_w4a16(x, W), K.gemm_w4a16(x, lb.to_device(W))):
+        assert np.isfinite(y).all()
+        err = np.abs(y.astype(np.float64) - ref)
+        worst = float((err / (RTOL * bound + 1e-300)).max())
+        assert worst <= 1.0, f"max err/limit = {worst:.3g}"
