@@ -943,10 +943,12 @@ hipError_t launch_split3(int fmt, const float *x, int M, int Kp, uint4 *x3, hipS
 // W4A16 activations as two float16 terms for the f16 matrix cores (one workgroup per
 // row). The row is scaled by 2^E, E chosen so that its largest magnitude lands in
 // [2^14, 2^15) (E = 0 for a zero or non-finite row); then xs = x 2^E = hi + lo 2^-11
-// with hi = fp16(xs) and lo = fp16((xs - hi) 2^11) (the remainder is exact in fp32,
-// and the 2^11 keeps lo a normal float16 down to |xs| ~ 2^-14), so each element keeps
-// 22 significant bits while its scaled magnitude is at least 2^-14, i.e. within 2^28
-// of the row's largest. Slots as in split3_kernel's W4A16 tiles, two terms per slot.
+// with hi = fp16(xs) and lo = fp16((xs - hi) 2^11) (the remainder is exact in fp32;
+// the 2^11 keeps lo clear of float16's subnormals, which the matrix cores flush, for
+// |xs| >= 2^-3). So an element keeps 22 significant bits within 2^17 of the row's
+// largest, has an absolute error of at most 2^-39 of the largest down to 2^28 below
+// it, and is dropped below that. Slots as in split3_kernel's W4A16 tiles, two terms
+// per slot.
 // Workgroups (m, p) of a row each take the row's maximum over all of it (from the
 // caches after the first) and split part p of its slots.
 __global__ __launch_bounds__(kThreads) void split2h_kernel(const float *__restrict__ x, int M, int Kp,

@@ -150,7 +150,8 @@ def test_w4a16_batch_rows_of_mixed_magnitude_and_range(m):
     before the float16 split: rows from 1e-36 to 1e30 in one call, and rows whose
     few huge entries (2^26 times the rest, at the weights' zero-point codes, so the
     reference's bound takes nothing from them) leave the other entries within 2^28
-    of the row's largest, where every element keeps 22 significant bits."""
+    of the row's largest, where each keeps an absolute error of at most 2^-39 of
+    that largest entry."""
     rng = np.random.default_rng(4242 + m)
     n, k = 96, 1024
     mags = np.array([1e-36, 1e-20, 1e-3, 1.0, 1e5, 1e18, 1e30])
