@@ -49,7 +49,8 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA, published (POP/s -> TOP/s here)
 FP32_PEAK_TFLOPS = 157.3     # dense fp32 matrix, published
 BF16_PEAK_TFLOPS = 2500.0    # dense bf16 MFMA, published
-BF16X3_TERMS = 3             # bf16 products per fp32 product on the bf16x3 path
+BF16X3_TERMS = 3             # bf16 products per fp32 product on the bf16x3 path (MXFP4)
+F16X2_TERMS = 2              # float16 products per product on the W4A16 two-term path
 COLD_POOL_BYTES = 1280 << 20  # > 2 x (256 MB MALL + 32 MB L2)
 DECODE = (1, 11008, 4096)
 BATCH = (64, 11008, 4096)
@@ -1001,9 +1002,11 @@ def main() -> int:
                 r["mfma"] = "int8"
                 r["mfma_frac"] = round(r["gflops"] / 1e3 / INT8_PEAK_TOPS, 4)
             elif r["weight_layout"] in ("t16", "t16f8"):
-                # fp32 semantics on bf16 matrix cores: three bf16 products per fp32 product
-                r["mfma"] = "bf16x3"
-                r["mfma_frac"] = round(BF16X3_TERMS * r["gflops"] / 1e3 / BF16_PEAK_TFLOPS, 4)
+                # MXFP4: three bf16 products per fp32 product; W4A16: two float16
+                # products per product (the same dense peak for both types)
+                terms = F16X2_TERMS if fmt == "w4a16" else BF16X3_TERMS
+                r["mfma"] = "f16x2" if fmt == "w4a16" else "bf16x3"
+                r["mfma_frac"] = round(terms * r["gflops"] / 1e3 / BF16_PEAK_TFLOPS, 4)
                 r["fp32_equiv_frac"] = round(r["gflops"] / 1e3 / FP32_PEAK_TFLOPS, 4)
             else:
                 r["mfma"] = "fp32"

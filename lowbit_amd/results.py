@@ -223,11 +223,14 @@ def _gemm_case(timer: _Timer, fmt: str, shape, W, x: np.ndarray, cold: bool):
 
 def _roofline(fmt: str, layout: str, m: int, n: int, k: int, t: float, wbytes: int) -> tuple[str, float]:
     """(roofline name, fraction) of one row: HBM for the decode kernels, the matrix
-    cores' dense peak otherwise (three bf16 products per fp32 product on bf16x3)."""
+    cores' dense peak otherwise (three bf16 products per fp32 product on MXFP4's
+    bf16x3, two float16 products per product on W4A16's f16x2; one dense peak)."""
     if layout == "row-major":
         return "hbm", (wbytes + 4 * m * (k + n)) / t / 1e9 / HBM_GBS
     if fmt == "w4a8":
         return "int8 mfma", 2.0 * m * n * k / t / 1e12 / PEAK_TFLOPS["int8"]
+    if fmt == "w4a16":
+        return "f16x2 mfma", 2 * 2.0 * m * n * k / t / 1e12 / PEAK_TFLOPS["bf16"]
     return "bf16x3 mfma", 3 * 2.0 * m * n * k / t / 1e12 / PEAK_TFLOPS["bf16"]
 
 
@@ -355,7 +358,7 @@ def report(res: dict) -> str:
                        f"{r['weight_gbps']:.0f} | {100 * r['roofline_frac']:.1f} % | {refc} |")
         out.append("")
     out += ["**All shapes, hot cache** — MI355X GFLOP/s (fraction of the roofline that bounds the kernel: HBM "
-            "for the decode kernels, the dense int8 / bf16x3 matrix-core peak otherwise), and the reference's "
+            "for the decode kernels, the dense int8 / bf16x3 (MXFP4) / f16x2 (W4A16) matrix-core peak otherwise), and the reference's "
             "best 4-thread CPU GFLOP/s:\n",
             "| M | N | K | W4A16 | W4A8 | MXFP4 | ref W4A16 (4T) | ref W4A8 (4T) | ref MXFP4 (4T) |",
             "|---|---|---|---|---|---|---|---|---|"]
