@@ -1368,10 +1368,15 @@ bool w4a16_prefers_t16f8(int M, int N, int Kp, int num_cus) {
 // the split took 65.9 against 49.6 us hot on t16 (57.8 against 43.3 on t16f8); 256
 // rows gained 8 % (94.8 against 102.8 on t16f8), too little for a partial-output
 // workspace that grows with M (ks M N 4 bytes, 256 MiB at 8192 x 4096 x 11008).
+// Since W4A16 reads two float16 terms (4 bytes per element) one row block no longer
+// gains from the split (hot, split against unsplit: 16 x 4096 x 11008 16.3-16.5
+// against 15.4 us, 16 x 11008 x 11008 28.2 against 26.9, 16 x 4096 x 8192 13.7-14.0
+// against 12.9) while two or more still do (32 x 4096 x 11008 21.1-21.2 against
+// 25.0, 64 x 4096 x 11008 26.0-26.3 against 27.6-27.8; 64 x 4096 x 8192 even).
 int bf3_k_slices(int fmt, int M, int Kp) {
   if (Kp < 8192) return 1;
   if (fmt == F_MXFP4) return M <= 16 ? 4 : 1;
-  return fmt == F_W4A16 && M <= 64 ? 2 : 1;
+  return fmt == F_W4A16 && M > 16 && M <= 64 ? 2 : 1;
 }
 
 size_t bf3_part_bytes(int fmt, int M, int N, int Kp) {

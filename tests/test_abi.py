@@ -157,8 +157,10 @@ def test_bf16x3_split_workspace_sizes():
     L = K.lib()
     base = L.lbd_bf16x3_workspace_bytes(16, 11008)
     align = (base + 255) // 256 * 256
-    assert L.lbd_bf16x3_workspace_bytes_split(0, 16, 4096, 11008) == align + 2 * 16 * 4096 * 4
+    assert L.lbd_bf16x3_workspace_bytes_split(0, 16, 4096, 11008) == align  # W4A16, one row block: no split
     assert L.lbd_bf16x3_workspace_bytes_split(1, 16, 4096, 11008) == align + 4 * 16 * 4096 * 4
+    a32 = (L.lbd_bf16x3_workspace_bytes(32, 11008) + 255) // 256 * 256
+    assert L.lbd_bf16x3_workspace_bytes_split(0, 32, 4096, 11008) == a32 + 2 * 32 * 4096 * 4
     b64 = L.lbd_bf16x3_workspace_bytes(64, 11008)
     assert L.lbd_bf16x3_workspace_bytes_split(1, 64, 4096, 11008) == (b64 + 255) // 256 * 256  # MXFP4, 64 rows: no split
     b4 = L.lbd_bf16x3_workspace_bytes(16, 4096)
