@@ -213,12 +213,13 @@ int lbd_gemm_w4a8_t16(const float *x, int M, int Kp, const uint8_t *qwt,
 size_t lbd_noalloc_scratch_bytes(void);
 int lbd_gemm_w4a8_t16_noalloc(const float *x, int M, int Kp, const uint8_t *qwt, const float *st,
                               const uint8_t *zt, int N, float *y, const lb_params *p, void *stream);
-/* y = x . w^T as lbd_gemm_w4a16, weights in the t16 layout, on bf16 matrix cores
- * with the float32 semantics of the reference's kernels (src/lowbit/csrc/
- * kern_scalar.c:10-47): x is split exactly into three bf16 terms (in `workspace`,
- * lbd_bf16x3_workspace_bytes(M, Kp) bytes, 256-byte aligned, or NULL for the
- * per-thread buffer) and every weight is exact in bf16, so each product is an
- * exact float32 value and the sums are float32. Always the matrix-core path. */
+/* y = x . w^T as lbd_gemm_w4a16, weights in the t16 layout, on float16 matrix
+ * cores within the reference's float32 bound (src/lowbit/csrc/kern_scalar.c:10-47,
+ * tests/test_kernels.py:108-116): each row of x is scaled by a power of two and
+ * split into two float16 terms (in `workspace`, lbd_bf16x3_workspace_bytes(M, Kp)
+ * bytes, 256-byte aligned, or NULL for the per-thread buffer), 22 significant bits
+ * of every element within 2^17 of its row's largest magnitude; every weight q - z is
+ * exact in float16 and the sums are float32. Always the matrix-core path. */
 int lbd_gemm_w4a16_t16(const float *x, int M, int Kp, const uint8_t *qwt,
                        const float *st, const uint8_t *zt, int N, float *y,
                        const lb_params *p, void *workspace,
@@ -234,10 +235,10 @@ size_t lbd_bf16x3_workspace_bytes(int M, int Kp);
  * taken; 0 for an invalid argument. (No reference counterpart: the reference's
  * GEMMs take no workspace.) */
 size_t lbd_bf16x3_workspace_bytes_split(int kind, int M, int N, int Kp);
-/* ---- "t16f8": int4 g128 weights for lbd_gemm_w4a16 on bf16 matrix cores with the
+/* ---- "t16f8": int4 g128 weights for lbd_gemm_w4a16 on the matrix cores with the
  *      zero-point folded in (no reference counterpart: a device-private copy of an
- *      Int4Weights matrix, src/lowbit/formats.py:56-87, that the bf16 matrix cores
- *      convert two operands per instruction). Each code less its group's zero-point
+ *      Int4Weights matrix, src/lowbit/formats.py:56-87, converted two operands per
+ *      instruction). Each code less its group's zero-point
  *      (z = 8 when zeros is NULL) is one E4M3 byte of value (code - z) 2^-9: sign
  *      and magnitude, exact for |code - z| <= 15, which holds for every zero-point
  *      the reference's packer writes (0-15, src/lowbit/formats.py:122); a larger
