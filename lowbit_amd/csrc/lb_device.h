@@ -146,6 +146,12 @@ __device__ __forceinline__ uint4 ld_b128(Rsrc r, uint32_t off) {
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// the same with cache-policy bits AUX (2: non-temporal, for data read once)
+template <int AUX>
+__device__ __forceinline__ uint4 ld_b128_aux(Rsrc r, uint32_t off) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ float4 ld_f4(Rsrc r, uint32_t off) {
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
